@@ -1,0 +1,185 @@
+/* iro_hip.h -- C ABI of the MI355X (gfx950) int8 W8A8 path of irodori-c.
+ *
+ * Two layers, both plain C (pointers and sizes, no HIP or torch types):
+ *
+ *  1. The device API (`iro_hip_*`).  Every pointer argument marked "device"
+ *     is HIP device memory; work is queued on the context's stream and the
+ *     call returns once it is queued (call iro_hip_sync to wait).  Calls
+ *     return 0 on success and -1 on error; the error text is sticky in the
+ *     context (iro_hip_error) until iro_hip_clear_error.
+ *
+ *  2. The ops.h drop-in (`iro_int8_*`, declared in iro_int8_ops.h): the
+ *     reference's host-pointer int8 API with identical names, signatures and
+ *     semantics, routed through a process-wide default context.
+ *
+ * Rounding follows one of the reference's two builds, chosen per context:
+ *   IRO_HIP_STRICT        ops.c compiled with -O2 (Makefile:4, the default
+ *                         `make irodori` / `make test-int8-ops` build);
+ *   IRO_HIP_GCC_FASTMATH  ops.c/dit.c/dacvae.c compiled with FAST_CFLAGS
+ *                         (Makefile:7, the oneMKL release build).
+ * int8 codes, scales, zero points and int32 sums are bit-exact against the
+ * chosen build; fp32 outputs too, except the SwiGLU gate's expf (see
+ * iro_hip_dit_swiglu).
+ *
+ * Contexts are not re-entrant: calls on one context must be serialized,
+ * as the reference engine's contract requires (generate.h:49-51).
+ */
+#ifndef IRO_HIP_H
+#define IRO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { IRO_HIP_STRICT = 0, IRO_HIP_GCC_FASTMATH = 1 };
+
+typedef struct IroHipContext IroHipContext;
+typedef struct IroHipWeight IroHipWeight;
+
+/* ---- context, stream, memory ------------------------------------------ */
+
+/* Create a context on `device` with its own HIP stream.  Runs the int32
+   known-answer test (ops.c:375-398) through the MFMA GEMM and fails if it
+   does not sum exactly, as iro_engine_init refuses an inexact backend
+   (generate.c:527-536). */
+int iro_hip_create(int device, int convention, IroHipContext **out);
+void iro_hip_destroy(IroHipContext *ctx);
+int iro_hip_get_convention(const IroHipContext *ctx);
+const char *iro_hip_error(const IroHipContext *ctx);
+void iro_hip_clear_error(IroHipContext *ctx);
+int iro_hip_sync(IroHipContext *ctx);
+/* The context's hipStream_t, for callers that share it. */
+void *iro_hip_stream(IroHipContext *ctx);
+
+int iro_hip_alloc(IroHipContext *ctx, size_t bytes, void **dptr);
+int iro_hip_free(IroHipContext *ctx, void *dptr);
+/* Synchronous copies between host and device memory. */
+int iro_hip_upload(IroHipContext *ctx, void *dst_device, const void *src_host, size_t bytes);
+int iro_hip_download(IroHipContext *ctx, void *dst_host, const void *src_device, size_t bytes);
+/* Byte fill with a kernel on the context stream (capture-safe). */
+int iro_hip_fill(IroHipContext *ctx, void *dst_device, int value, size_t bytes);
+
+/* Stream-ordered timing on the context stream. */
+int iro_hip_event_create(void **event);
+void iro_hip_event_destroy(void *event);
+int iro_hip_event_record(IroHipContext *ctx, void *event);
+int iro_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* ---- weights: ops.h:23-28 IroInt8Weight, device resident -------------- */
+
+/* Quantize an fp32 [N,K] row-major device matrix per output row exactly as
+   iro_int8_weight_quantize (ops.c:259-293) and pre-pack it once into the
+   MFMA fragment layout the GEMM streams (32 rows x 32 k per 1 KiB tile). */
+int iro_hip_weight_create(IroHipContext *ctx, const float *w_device, int N, int K,
+                          IroHipWeight **out);
+/* Same for a [K,N] row-major source (ops.c:295-306, ConvTranspose). */
+int iro_hip_weight_create_transposed(IroHipContext *ctx, const float *w_device,
+                                     int N, int K, IroHipWeight **out);
+/* Fused projection: `parts` fp32 [N_i,K] device matrices quantized row by
+   row as above and packed into one weight.  layout 0 concatenates them
+   (QKVG: [Wq;Wk;Wv;Wgate], dit.c:786-792 run as one GEMM); layout 1
+   interleaves two equal parts in 32-row blocks so each output tile holds
+   matching W1 and W3 columns (dit.c:944-956, SwiGLU).  Quantization is per
+   row, so codes, scales and sums are identical to separate weights. */
+int iro_hip_weight_create_fused(IroHipContext *ctx, const float *const *parts_device,
+                                const int *parts_N, int nparts, int K, int layout,
+                                IroHipWeight **out);
+/* Adopt an already quantized host weight (codes [N,K], scale[N], colsum[N]). */
+int iro_hip_weight_from_host(IroHipContext *ctx, const int8_t *data, const float *scale,
+                             const int32_t *colsum, int N, int K, IroHipWeight **out);
+/* Copy a weight back to host arrays in its logical row order. */
+int iro_hip_weight_export(IroHipContext *ctx, const IroHipWeight *w, int8_t *data,
+                          float *scale, int32_t *colsum);
+void iro_hip_weight_destroy(IroHipWeight *w);
+/* Logical N (all parts) and K. */
+int iro_hip_weight_dims(const IroHipWeight *w, int *N, int *K);
+/* Same accounting as iro_int8_weight_bytes (ops.c:316-319). */
+size_t iro_hip_weight_bytes(const IroHipWeight *w);
+
+/* ---- activations ------------------------------------------------------ */
+
+/* iro_int8_quantize_rows (ops.c:321-348) on device memory.  x [M,K] fp32,
+   q [M,K] u8, scale[M], zero[M]. */
+int iro_hip_quantize_rows(IroHipContext *ctx, const float *x, int M, int K, uint8_t *q,
+                          float *scale, int32_t *zero);
+/* iro_int8_quantize_rows_residual (ops.c:427-442); residual may be NULL. */
+int iro_hip_quantize_rows_residual(IroHipContext *ctx, const float *x, int M, int K,
+                                   uint8_t *q1, float *scale1, int32_t *zero1,
+                                   float *residual, uint8_t *q2, float *scale2,
+                                   int32_t *zero2);
+
+/* ---- linear ----------------------------------------------------------- */
+
+/* iro_int8_linear_ex (ops.c:450-491): int32 work[M,N] = q . W^T (u8 x s8,
+   raw, as cblas_gemm_s8u8s32 with zero offsets) and
+   y = float(work - zero*colsum) * (scale*w.scale) [+ bias], or y += ... when
+   accumulate.  work may be NULL (then it is not written).  q rows are
+   K bytes apart. */
+int iro_hip_int8_linear_ex(IroHipContext *ctx, const uint8_t *q, const float *scale,
+                           const int32_t *zero, const IroHipWeight *w, const float *bias,
+                           float *y, int M, int32_t *work, int accumulate);
+
+/* Two quantized planes of one activation against the same weight in one
+   pass (dit.c:477-485 int8_scratch_linear with residual):
+   y = lin(q1) [+bias]; y += lin(q2). */
+int iro_hip_int8_linear_two_term(IroHipContext *ctx, const uint8_t *q1, const float *scale1,
+                                 const int32_t *zero1, const uint8_t *q2,
+                                 const float *scale2, const int32_t *zero2,
+                                 const IroHipWeight *w, const float *bias, float *y, int M,
+                                 int accumulate);
+
+/* ---- fused DiT projections (device memory, rows m = b*S + s) ---------- */
+
+/* dit.c:780-798: quantize x [M,D] once, one GEMM against the fused QKVG
+   weight ([4D,D], layout 0), split store into q,k,v,gate [M,D].
+   residual != 0 runs the two-term activation (IRO_INT8_RESIDUAL bit 1). */
+int iro_hip_dit_qkvg(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w_qkvg,
+                     float *q, float *k, float *v, float *gate, int residual);
+
+/* dit.c:876-884 then dit.c:1013-1020: quantize mix [M,D], GEMM with w
+   ([D,D]) and, when x_res is not NULL, x_res[b,s,:] += gate[b,:] * out
+   fused in the epilogue (out then may be NULL); otherwise out = result. */
+int iro_hip_dit_linear_gated(IroHipContext *ctx, const float *mix, int M,
+                             const IroHipWeight *w, int residual, float *out, float *x_res,
+                             const float *gate, int S);
+
+/* dit.c:939-972 then dit.c:1032-1039: SwiGLU MLP.  h [M,D] quantized once;
+   fused W1/W3 GEMM (layout 1 weight, [2H,D]) whose epilogue writes
+   hidden = silu(w1)*w3 [M,H]; hidden quantized with the two-term residual
+   when residual_w2 (the reference default, dit.c:422-436); W2 ([D,H]) GEMM
+   over both planes; x_res += gate * out fused when x_res is not NULL,
+   else out = result.  hidden may be NULL (context scratch is used).
+   The gate's expf is evaluated in double precision and rounded once, which
+   matches glibc's scalar expf except where glibc itself misrounds. */
+int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
+                       const IroHipWeight *w2, int residual_w13, int residual_w2,
+                       float *hidden, float *out, float *x_res, const float *gate, int S);
+
+/* ---- DACVAE int8 Conv1d (dacvae.c:543-688, no snake) ------------------- */
+
+/* input [T, C] fp32 time-major, weight [N, kernel*C] (tap-major K as
+   iro_dacvae_int8_quantize lays it out, dacvae.c:228-240), bias [N] or
+   NULL; residual adds the fixed-scale second plane (dacvae.c:637-663).
+   output [T_out, N].  Each output row is quantized over its whole
+   kernel*C window with one scale and zero point; padding taps hold the zero
+   point.  Returns T_out through *t_out when not NULL. */
+int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
+                        const IroHipWeight *w, int kernel, int stride, int dilation,
+                        int padding, const float *bias, int residual, float *output,
+                        int *t_out);
+
+/* ---- backend queries: ops.h:55-78 ------------------------------------- */
+
+/* Runs the ops.c:375-398 known answer through the MFMA GEMM: 0 exact. */
+int iro_hip_selfcheck(IroHipContext *ctx);
+/* "gfx950 MFMA i8" plus device name; never NULL. */
+const char *iro_hip_backend_name(IroHipContext *ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

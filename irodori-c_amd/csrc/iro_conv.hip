@@ -1,0 +1,175 @@
+// iro_conv.hip -- the DACVAE int8 Conv1d (dacvae.c:543-688) as an implicit
+// GEMM: quantized im2col rows, then the MFMA GEMM of iro_gemm.hip.
+//
+// Quantization is per OUTPUT time step over its whole kernel*C window
+// (dacvae.c:617-636): each input element is coded under up to `kernel`
+// different (scale, zero point) pairs, so the codes cannot be produced once
+// per input row.  Two passes:
+//   conv_rows    per input time step lo/hi over channels (dacvae.c:607-616),
+//                one wavefront per row;
+//   conv_im2col  per output time step: window lo/hi from the tap rows that
+//                fall inside [0, T), the row scale/zero point, and the u8
+//                im2col row [tap*C + c] (padding taps hold the zero point);
+//                with `residual`, the second plane with scale s/255 and zero
+//                point 128 (dacvae.c:637-663).
+// Roofline: HBM.  conv_im2col reads kernel*C*4 bytes (mostly L2 hits: the
+// taps of neighbouring rows overlap) and writes kernel*C (x2) bytes per row.
+#include "iro_internal.h"
+#include "iro_round.h"
+
+namespace iro {
+
+namespace {
+
+__global__ __launch_bounds__(256) void conv_rows_kernel(const float *__restrict__ x, int T, int C,
+                                                        float *__restrict__ row_lo,
+                                                        float *__restrict__ row_hi) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= T) return;
+    const float *xr = x + (size_t)t * C;
+    float lo = 0.0f, hi = 0.0f;
+    if ((C & 3) == 0) {
+        for (int c = lane * 4; c < C; c += 256) {
+            const float4 v = *reinterpret_cast<const float4 *>(xr + c);
+            lo = sel_min(lo, v.x); lo = sel_min(lo, v.y); lo = sel_min(lo, v.z); lo = sel_min(lo, v.w);
+            hi = sel_max(hi, v.x); hi = sel_max(hi, v.y); hi = sel_max(hi, v.z); hi = sel_max(hi, v.w);
+        }
+    } else {
+        for (int c = lane; c < C; c += 64) {
+            lo = sel_min(lo, xr[c]);
+            hi = sel_max(hi, xr[c]);
+        }
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (lane == 0) {
+        row_lo[t] = lo;
+        row_hi[t] = hi;
+    }
+}
+
+// Plane-2 code of one element (dacvae.c:656-660).
+template <int CONV>
+__device__ __forceinline__ uint32_t plane2_code(float x, float v, const RowQ &r, float inv2) {
+    const float rem = residual_value<CONV>(x, v, r);
+    float v2 = CONV == 1 ? __builtin_rintf(__builtin_fmaf(rem, inv2, 128.0f))
+                         : __builtin_rintf(rem * inv2 + 128.0f);
+    v2 = v2 < 0.0f ? 0.0f : v2;
+    v2 = v2 > 255.0f ? 255.0f : v2;
+    return (uint32_t)v2;
+}
+
+template <int CONV, bool RES>
+__global__ __launch_bounds__(256) void conv_im2col_kernel(
+    const float *__restrict__ x, int T, int C, int T_out, int kernel, int stride, int dilation,
+    int padding, const float *__restrict__ row_lo, const float *__restrict__ row_hi,
+    uint8_t *__restrict__ cols1, uint8_t *__restrict__ cols2, int ldc, float *__restrict__ s1,
+    int32_t *__restrict__ z1, float *__restrict__ s2, int32_t *__restrict__ z2) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= T_out) return;
+    // Window range: taps inside [0, T) only (dacvae.c:619-627).
+    float lo = 0.0f, hi = 0.0f;
+    for (int tap = 0; tap < kernel; ++tap) {
+        const int it = r * stride - padding + tap * dilation;
+        if (it < 0 || it >= T) continue;
+        lo = sel_min(lo, row_lo[it]);
+        hi = sel_max(hi, row_hi[it]);
+    }
+    const RowQ q = row_params<CONV>(lo, hi);
+    float sc2 = 0.0f, inv2 = 0.0f;
+    if (RES) {
+        if (CONV == 1) {
+            const float d = hi - lo;
+            sc2 = q.s * c_inv255();
+            inv2 = d * c_inv255() > 0.0f ? c_255_inv255_b() / d : 255.0f;
+        } else {
+            sc2 = q.s / 255.0f;
+            inv2 = 255.0f / q.s;
+        }
+    }
+    uint8_t *d1 = cols1 + (size_t)r * ldc;
+    uint8_t *d2 = RES ? cols2 + (size_t)r * ldc : nullptr;
+    const uint32_t zp4 = 0x01010101u * (uint32_t)q.zp;
+    const uint32_t h4 = 0x80808080u;
+    for (int tap = 0; tap < kernel; ++tap) {
+        const int it = r * stride - padding + tap * dilation;
+        uint8_t *t1 = d1 + (size_t)tap * C;
+        uint8_t *t2 = RES ? d2 + (size_t)tap * C : nullptr;
+        const bool inside = it >= 0 && it < T;
+        const float *xr = x + (size_t)(inside ? it : 0) * C;
+        if ((C & 3) == 0 && (ldc & 3) == 0) {
+            for (int c = lane * 4; c < C; c += 256) {
+                if (!inside) {
+                    *reinterpret_cast<uint32_t *>(t1 + c) = zp4;
+                    if (RES) *reinterpret_cast<uint32_t *>(t2 + c) = h4;
+                    continue;
+                }
+                const float4 v = *reinterpret_cast<const float4 *>(xr + c);
+                const float a = quant_value<CONV>(v.x, q), b = quant_value<CONV>(v.y, q);
+                const float e = quant_value<CONV>(v.z, q), f = quant_value<CONV>(v.w, q);
+                *reinterpret_cast<uint32_t *>(t1 + c) =
+                    (uint32_t)a | ((uint32_t)b << 8) | ((uint32_t)e << 16) | ((uint32_t)f << 24);
+                if (RES) {
+                    *reinterpret_cast<uint32_t *>(t2 + c) =
+                        plane2_code<CONV>(v.x, a, q, inv2) | (plane2_code<CONV>(v.y, b, q, inv2) << 8) |
+                        (plane2_code<CONV>(v.z, e, q, inv2) << 16) |
+                        (plane2_code<CONV>(v.w, f, q, inv2) << 24);
+                }
+            }
+        } else {
+            for (int c = lane; c < C; c += 64) {
+                if (!inside) {
+                    t1[c] = (uint8_t)q.zp;
+                    if (RES) t2[c] = 128;
+                    continue;
+                }
+                const float v = quant_value<CONV>(xr[c], q);
+                t1[c] = (uint8_t)v;
+                if (RES) t2[c] = (uint8_t)plane2_code<CONV>(xr[c], v, q, inv2);
+            }
+        }
+    }
+    if (lane == 0) {
+        s1[r] = q.s;
+        z1[r] = q.zp;
+        if (RES) {
+            s2[r] = sc2;
+            z2[r] = 128;
+        }
+    }
+}
+
+}  // namespace
+
+int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi) {
+    hipLaunchKernelGGL(conv_rows_kernel, dim3((T + 3) / 4), dim3(256), 0, ctx->stream, x, T, C, lo,
+                       hi);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+int launch_conv_im2col(IroHipContext *ctx, const float *x, int T, int C, int T_out, int kernel,
+                       int stride, int dilation, int padding, const float *row_lo,
+                       const float *row_hi, uint8_t *cols1, uint8_t *cols2, int ldc, float *s1,
+                       int32_t *z1, float *s2, int32_t *z2) {
+    const dim3 grid((T_out + 3) / 4), block(256);
+    const bool res = cols2 != nullptr;
+#define IRO_IM2COL(CV, RS)                                                                      \
+    hipLaunchKernelGGL((conv_im2col_kernel<CV, RS>), grid, block, 0, ctx->stream, x, T, C, T_out, \
+                       kernel, stride, dilation, padding, row_lo, row_hi, cols1, cols2, ldc, s1, \
+                       z1, s2, z2)
+    if (ctx->convention == IRO_HIP_GCC_FASTMATH) {
+        if (res) IRO_IM2COL(1, true);
+        else IRO_IM2COL(1, false);
+    } else {
+        if (res) IRO_IM2COL(0, true);
+        else IRO_IM2COL(0, false);
+    }
+#undef IRO_IM2COL
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+}  // namespace iro

@@ -1,0 +1,133 @@
+// iro_internal.h -- types shared by the gfx950 kernels and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "iro_hip.h"
+
+// Context: one device, one stream, one rounding convention, one growable
+// device workspace for the activations the fused entry points stage
+// (quantized codes, row scales, the SwiGLU hidden state, im2col rows).
+struct IroHipContext {
+    int device = 0;
+    int convention = IRO_HIP_STRICT;
+    hipStream_t stream = nullptr;
+    char err[512] = {0};
+    int has_err = 0;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    char backend[256] = {0};
+};
+
+// A quantized weight, pre-packed for the MFMA B operand.
+//
+// Packed layout: [Np/32][Kp/32] fragments of 1 KiB.  Fragment (nb, kb)
+// holds rows nb*32 .. +31 (in packed order) and k = kb*32 .. +31; lane L of
+// a wave owns bytes [L*16, L*16+16): row nb*32 + (L & 31), k = kb*32 +
+// (L >> 5)*16 .. +15.  A wave therefore loads one fragment with one
+// 16-byte read per lane, and a GEMM tile of BN x BK is BN/32 contiguous
+// runs of BK/32 fragments.  Rows beyond N and k beyond K are zero.
+//
+// Packed row order: layout 0 keeps the logical order (parts concatenated);
+// layout 1 interleaves two equal parts in 32-row blocks (packed block 2t
+// is part 0 block t, 2t+1 is part 1 block t), so an output tile of 64
+// columns holds matching W1 and W3 columns.  scale/colsum are stored in
+// packed order.
+struct IroHipWeight {
+    IroHipContext *ctx = nullptr;
+    int N = 0, K = 0;    // logical
+    int Np = 0, Kp = 0;  // padded to kNPad / kKPad
+    int layout = 0;
+    int nparts = 1;
+    int part_N[8] = {0};
+    int8_t *packed = nullptr;
+    float *scale = nullptr;
+    int32_t *colsum = nullptr;  // as given (used by the epilogue)
+    int32_t *rowsum = nullptr;  // true sum of the packed codes of each row;
+                                // equals colsum unless a caller supplied an
+                                // inconsistent one (ops.c:391 selfcheck does)
+};
+
+namespace iro {
+
+constexpr int kNPad = 256;  // packed rows padded to a multiple of this
+constexpr int kKPad = 128;  // packed k padded to a multiple of this
+
+int set_error(IroHipContext *ctx, const char *fmt, ...);
+
+#define IRO_HIP_TRY(ctx, expr)                                                        \
+    do {                                                                              \
+        hipError_t e_ = (expr);                                                       \
+        if (e_ != hipSuccess)                                                         \
+            return ::iro::set_error((ctx), "%s:%d %s: %s", __FILE__, __LINE__, #expr, \
+                                    hipGetErrorString(e_));                           \
+    } while (0)
+
+#define IRO_HIP_CHECK_LAUNCH(ctx) IRO_HIP_TRY(ctx, hipGetLastError())
+
+// Bump allocation from the context workspace; grows it (after draining the
+// stream) when a call needs more.  Offsets are 256-byte aligned.
+struct Workspace {
+    IroHipContext *ctx;
+    size_t need = 0;
+    size_t reserve(size_t bytes) {
+        size_t off = need;
+        need += (bytes + 255) & ~size_t(255);
+        return off;
+    }
+    int commit();  // ensures ctx->ws holds `need` bytes
+    template <class T>
+    T *at(size_t off) const {
+        return reinterpret_cast<T *>(static_cast<char *>(ctx->ws) + off);
+    }
+};
+
+// ---- kernel launchers (iro_quant.hip, iro_gemm.hip, iro_conv.hip) -------
+
+int launch_quant_rows(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
+                      int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
+                      int32_t *z2);
+int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long long stride_n,
+                        long long stride_k, int8_t *q, float *scale, int32_t *colsum);
+int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const int32_t *colsum,
+                const int32_t *rowsum, IroHipWeight *w);
+int launch_fill(IroHipContext *ctx, void *dst, int value, size_t bytes);
+
+enum Epi { EPI_LINEAR = 0, EPI_QKVG = 1, EPI_SWIGLU = 2, EPI_GATED = 3 };
+
+struct GemmArgs {
+    const uint8_t *a1 = nullptr;  // u8 codes [M, lda] (plane 1)
+    const uint8_t *a2 = nullptr;  // plane 2, nullptr for one plane
+    int lda = 0;
+    const float *sx1 = nullptr, *sx2 = nullptr;
+    const int32_t *zx1 = nullptr, *zx2 = nullptr;
+    int M = 0;
+    int K = 0;  // k extent read from A (multiple of 16, <= w->Kp)
+    const float *bias = nullptr;
+    float *y = nullptr;  // EPI_LINEAR output [M, ldy]
+    int ldy = 0;
+    int32_t *work = nullptr;  // raw plane-1 sums [M, ldw], nullable
+    int ldw = 0;
+    int accumulate = 0;
+    float *seg[4] = {nullptr, nullptr, nullptr, nullptr};  // EPI_QKVG
+    int seg_n = 0;
+    float *hidden = nullptr;  // EPI_SWIGLU [M, ldh]
+    int ldh = 0;
+    float *xres = nullptr;  // EPI_GATED [M, ldx]
+    const float *gate = nullptr;
+    int ldx = 0;
+    int rows_per_branch = 1;
+};
+
+int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi);
+
+int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi);
+int launch_conv_im2col(IroHipContext *ctx, const float *x, int T, int C, int T_out, int kernel,
+                       int stride, int dilation, int padding, const float *row_lo,
+                       const float *row_hi, uint8_t *cols1, uint8_t *cols2, int ldc, float *s1,
+                       int32_t *z1, float *s2, int32_t *z2);
+
+}  // namespace iro

@@ -1,0 +1,354 @@
+// iro_quant.hip -- per-row activation quantization, per-output-row weight
+// quantization and MFMA pre-packing for gfx950.
+//
+// Activations (ops.c:321-348, ops.c:427-442): one 64-lane wavefront per
+// row.  The row is read once into registers (CH float4 per lane, coalesced
+// 1 KiB per wave instruction), min/max are wave reductions, and the codes
+// are written as one u32 (4 codes) per lane per chunk.  The two-term
+// variant keeps the row in registers, forms the remainder in place and
+// quantizes it again, so the input is read from HBM exactly once.
+// Roofline: HBM, 4K + K (+K) + 8 bytes per row.
+#include "iro_internal.h"
+#include "iro_round.h"
+
+namespace iro {
+
+namespace {
+
+template <int CONV>
+__device__ __forceinline__ uint32_t codes4(const float4 &v, const RowQ &r, float4 *vals) {
+    float a = quant_value<CONV>(v.x, r), b = quant_value<CONV>(v.y, r);
+    float c = quant_value<CONV>(v.z, r), d = quant_value<CONV>(v.w, r);
+    if (vals) *vals = make_float4(a, b, c, d);
+    return (uint32_t)a | ((uint32_t)b << 8) | ((uint32_t)c << 16) | ((uint32_t)d << 24);
+}
+
+// Vector path: K % 4 == 0, 16-byte aligned rows, K <= 256*CH.
+template <int CONV, int CH, bool RES>
+__global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ x, int M, int K,
+                                                      int ldx, uint8_t *__restrict__ q1, int ldq,
+                                                      float *__restrict__ s1,
+                                                      int32_t *__restrict__ z1,
+                                                      float *__restrict__ res,
+                                                      uint8_t *__restrict__ q2,
+                                                      float *__restrict__ s2,
+                                                      int32_t *__restrict__ z2) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const float *xr = x + (size_t)row * ldx;
+    float4 v[CH];
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < K) {
+            v[c] = *reinterpret_cast<const float4 *>(xr + col);
+        } else {
+            v[c] = make_float4(0.f, 0.f, 0.f, 0.f);  // zero is inside every range
+        }
+        lo = sel_min(lo, v[c].x); lo = sel_min(lo, v[c].y);
+        lo = sel_min(lo, v[c].z); lo = sel_min(lo, v[c].w);
+        hi = sel_max(hi, v[c].x); hi = sel_max(hi, v[c].y);
+        hi = sel_max(hi, v[c].z); hi = sel_max(hi, v[c].w);
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    const RowQ r = row_params<CONV>(lo, hi);
+    uint8_t *qr = q1 + (size_t)row * ldq;
+    float lo2 = 0.0f, hi2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int col = (c * 64 + lane) * 4;
+        float4 qv;
+        const uint32_t packed = codes4<CONV>(v[c], r, RES ? &qv : nullptr);
+        if (col < K) *reinterpret_cast<uint32_t *>(qr + col) = packed;
+        if (RES) {
+            if (col < K) {
+                v[c].x = residual_value<CONV>(v[c].x, qv.x, r);
+                v[c].y = residual_value<CONV>(v[c].y, qv.y, r);
+                v[c].z = residual_value<CONV>(v[c].z, qv.z, r);
+                v[c].w = residual_value<CONV>(v[c].w, qv.w, r);
+            }
+            lo2 = sel_min(lo2, v[c].x); lo2 = sel_min(lo2, v[c].y);
+            lo2 = sel_min(lo2, v[c].z); lo2 = sel_min(lo2, v[c].w);
+            hi2 = sel_max(hi2, v[c].x); hi2 = sel_max(hi2, v[c].y);
+            hi2 = sel_max(hi2, v[c].z); hi2 = sel_max(hi2, v[c].w);
+        }
+    }
+    if (lane == 0) {
+        s1[row] = r.s;
+        z1[row] = r.zp;
+    }
+    if (RES) {
+        lo2 = wave_min(lo2);
+        hi2 = wave_max(hi2);
+        const RowQ r2 = row_params<CONV>(lo2, hi2);
+        uint8_t *q2r = q2 + (size_t)row * ldq;
+        float *rr = res ? res + (size_t)row * K : nullptr;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int col = (c * 64 + lane) * 4;
+            const uint32_t packed = codes4<CONV>(v[c], r2, nullptr);
+            if (col < K) {
+                *reinterpret_cast<uint32_t *>(q2r + col) = packed;
+                if (rr) *reinterpret_cast<float4 *>(rr + col) = v[c];
+            }
+        }
+        if (lane == 0) {
+            s2[row] = r2.s;
+            z2[row] = r2.zp;
+        }
+    }
+}
+
+// Generic path: any K and alignment; the row is re-read from cache.
+template <int CONV, bool RES>
+__global__ __launch_bounds__(256) void quant_rows_any(const float *__restrict__ x, int M, int K,
+                                                      int ldx, uint8_t *__restrict__ q1, int ldq,
+                                                      float *__restrict__ s1,
+                                                      int32_t *__restrict__ z1,
+                                                      float *__restrict__ res,
+                                                      uint8_t *__restrict__ q2,
+                                                      float *__restrict__ s2,
+                                                      int32_t *__restrict__ z2) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const float *xr = x + (size_t)row * ldx;
+    float lo = 0.0f, hi = 0.0f;
+    for (int k = lane; k < K; k += 64) {
+        lo = sel_min(lo, xr[k]);
+        hi = sel_max(hi, xr[k]);
+    }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    const RowQ r = row_params<CONV>(lo, hi);
+    uint8_t *qr = q1 + (size_t)row * ldq;
+    float lo2 = 0.0f, hi2 = 0.0f;
+    for (int k = lane; k < K; k += 64) {
+        const float v = quant_value<CONV>(xr[k], r);
+        qr[k] = (uint8_t)v;
+        if (RES) {
+            const float rv = residual_value<CONV>(xr[k], v, r);
+            lo2 = sel_min(lo2, rv);
+            hi2 = sel_max(hi2, rv);
+        }
+    }
+    if (lane == 0) {
+        s1[row] = r.s;
+        z1[row] = r.zp;
+    }
+    if (RES) {
+        lo2 = wave_min(lo2);
+        hi2 = wave_max(hi2);
+        const RowQ r2 = row_params<CONV>(lo2, hi2);
+        uint8_t *q2r = q2 + (size_t)row * ldq;
+        for (int k = lane; k < K; k += 64) {
+            const float rv = residual_value<CONV>(xr[k], (float)qr[k], r);
+            q2r[k] = (uint8_t)quant_value<CONV>(rv, r2);
+            if (res) res[(size_t)row * K + k] = rv;
+        }
+        if (lane == 0) {
+            s2[row] = r2.s;
+            z2[row] = r2.zp;
+        }
+    }
+}
+
+// ops.c:259-293: one wave per output row.  Source element (n, k) is
+// w[n*stride_n + k*stride_k] so the [K,N] source of ops.c:295-306 needs no
+// transposed copy.
+template <int CONV>
+__global__ __launch_bounds__(256) void weight_quant_kernel(const float *__restrict__ w, int N,
+                                                           int K, long long stride_n,
+                                                           long long stride_k,
+                                                           int8_t *__restrict__ q,
+                                                           float *__restrict__ scale,
+                                                           int32_t *__restrict__ colsum) {
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (n >= N) return;
+    const float *wr = w + n * stride_n;
+    float amax = 0.0f;
+    for (int k = lane; k < K; k += 64) {
+        const float a = fabsf(wr[k * stride_k]);
+        amax = a > amax ? a : amax;
+    }
+    amax = wave_max(amax);
+    float s, inv;
+    if (CONV == 1) {
+        if (amax > 0.0f) {
+            s = amax * c_inv127();
+            inv = 127.0f / amax;
+        } else {
+            s = 1.0f;
+            inv = 1.0f;
+        }
+    } else {
+        s = amax > 0.0f ? amax / 127.0f : 1.0f;
+        inv = 1.0f / s;
+    }
+    int sum = 0;
+    int8_t *qr = q + (size_t)n * K;
+    for (int k = lane; k < K; k += 64) {
+        const int v = clampi((int)__builtin_rintf(wr[k * stride_k] * inv), -127, 127);
+        qr[k] = (int8_t)v;
+        sum += v;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) {
+        scale[n] = s;
+        colsum[n] = sum;
+    }
+}
+
+// Logical row of packed 32-row block `pb` (see IroHipWeight), or -1.
+__device__ __forceinline__ int packed_block_source(int pb, int layout, int half_blocks) {
+    if (layout == 1) {
+        const int t = pb >> 1;
+        if (t >= half_blocks) return -1;
+        return (pb & 1) ? half_blocks + t : t;
+    }
+    return pb;
+}
+
+// One thread per 16-byte chunk of the packed buffer.
+__global__ __launch_bounds__(256) void pack_kernel(const int8_t *__restrict__ q, int N, int K,
+                                                   int Np, int Kp, int layout, int half_blocks,
+                                                   int8_t *__restrict__ packed) {
+    const long long chunk = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = (long long)Np * Kp / 16;
+    if (chunk >= total) return;
+    const int kb_count = Kp / 32;
+    const long long frag = chunk >> 6;
+    const int lane = (int)(chunk & 63);
+    const int pb = (int)(frag / kb_count);
+    const int kb = (int)(frag % kb_count);
+    const int lb = packed_block_source(pb, layout, half_blocks);
+    const int n = lb * 32 + (lane & 31);
+    const int k0 = kb * 32 + (lane >> 5) * 16;
+    union {
+        int8_t b[16];
+        int4 v;
+    } u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = k0 + i;
+        u.b[i] = (lb >= 0 && n < N && k < K) ? q[(size_t)n * K + k] : (int8_t)0;
+    }
+    *reinterpret_cast<int4 *>(packed + chunk * 16) = u.v;
+}
+
+__global__ __launch_bounds__(256) void pack_cols_kernel(const float *__restrict__ scale,
+                                                        const int32_t *__restrict__ colsum,
+                                                        const int32_t *__restrict__ rowsum, int N,
+                                                        int Np, int layout, int half_blocks,
+                                                        float *__restrict__ pscale,
+                                                        int32_t *__restrict__ pcolsum,
+                                                        int32_t *__restrict__ prowsum) {
+    const int pc = blockIdx.x * 256 + threadIdx.x;
+    if (pc >= Np) return;
+    const int lb = packed_block_source(pc >> 5, layout, half_blocks);
+    const int n = lb * 32 + (pc & 31);
+    const bool ok = lb >= 0 && n < N;
+    pscale[pc] = ok ? scale[n] : 0.0f;
+    pcolsum[pc] = ok ? colsum[n] : 0;
+    if (prowsum) prowsum[pc] = ok ? rowsum[n] : 0;
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(uint8_t *__restrict__ dst, uint8_t value,
+                                                   size_t bytes) {
+    size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 16;
+    const size_t stride = (size_t)gridDim.x * 256 * 16;
+    const uint32_t v4 = 0x01010101u * value;
+    for (; i < bytes; i += stride) {
+        if (i + 16 <= bytes && (((uintptr_t)(dst + i)) & 15) == 0) {
+            *reinterpret_cast<uint4 *>(dst + i) = make_uint4(v4, v4, v4, v4);
+        } else {
+            for (size_t j = i; j < i + 16 && j < bytes; ++j) dst[j] = value;
+        }
+    }
+}
+
+template <int CONV, bool RES>
+int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
+                        int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
+                        int32_t *z2) {
+    const dim3 grid((M + 3) / 4), block(256);
+    const bool vec = (K % 4 == 0) && (ldx % 4 == 0) && (ldq % 4 == 0) &&
+                     (((uintptr_t)x) & 15) == 0 && (((uintptr_t)q1) & 3) == 0 &&
+                     (!RES || (((uintptr_t)q2) & 3) == 0) &&
+                     (!RES || !res || (((uintptr_t)res) & 15) == 0);
+    const int ch = (K + 255) / 256;
+    hipStream_t st = ctx->stream;
+#define IRO_QR(CH)                                                                               \
+    hipLaunchKernelGGL((quant_rows_vec<CONV, CH, RES>), grid, block, 0, st, x, M, K, ldx, q1, ldq, \
+                       s1, z1, res, q2, s2, z2)
+    if (vec && ch <= 1) IRO_QR(1);
+    else if (vec && ch <= 2) IRO_QR(2);
+    else if (vec && ch <= 4) IRO_QR(4);
+    else if (vec && ch <= 8) IRO_QR(8);
+    else if (vec && ch <= 12) IRO_QR(12);
+    else if (vec && ch <= 16) IRO_QR(16);
+    else
+        hipLaunchKernelGGL((quant_rows_any<CONV, RES>), grid, block, 0, st, x, M, K, ldx, q1, ldq,
+                           s1, z1, res, q2, s2, z2);
+#undef IRO_QR
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+}  // namespace
+
+int launch_quant_rows(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
+                      int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
+                      int32_t *z2) {
+    if (M <= 0 || K <= 0) return 0;
+    const bool two = q2 != nullptr;
+    if (ctx->convention == IRO_HIP_GCC_FASTMATH)
+        return two ? quant_rows_dispatch<1, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
+                   : quant_rows_dispatch<1, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
+    return two ? quant_rows_dispatch<0, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
+               : quant_rows_dispatch<0, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
+}
+
+int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long long stride_n,
+                        long long stride_k, int8_t *q, float *scale, int32_t *colsum) {
+    const dim3 grid((N + 3) / 4), block(256);
+    if (ctx->convention == IRO_HIP_GCC_FASTMATH)
+        hipLaunchKernelGGL((weight_quant_kernel<1>), grid, block, 0, ctx->stream, w, N, K,
+                           stride_n, stride_k, q, scale, colsum);
+    else
+        hipLaunchKernelGGL((weight_quant_kernel<0>), grid, block, 0, ctx->stream, w, N, K,
+                           stride_n, stride_k, q, scale, colsum);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const int32_t *colsum,
+                const int32_t *rowsum, IroHipWeight *w) {
+    const int half_blocks = w->layout == 1 ? w->part_N[0] / 32 : 0;
+    const long long chunks = (long long)w->Np * w->Kp / 16;
+    hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                       ctx->stream, q, w->N, w->K, w->Np, w->Kp, w->layout, half_blocks,
+                       w->packed);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    hipLaunchKernelGGL(pack_cols_kernel, dim3((w->Np + 255) / 256), dim3(256), 0, ctx->stream,
+                       scale, colsum, rowsum, w->N, w->Np, w->layout, half_blocks, w->scale,
+                       w->colsum, w->rowsum != w->colsum ? w->rowsum : nullptr);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+int launch_fill(IroHipContext *ctx, void *dst, int value, size_t bytes) {
+    if (!bytes) return 0;
+    size_t blocks = (bytes + 256 * 16 - 1) / (256 * 16);
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx->stream,
+                       static_cast<uint8_t *>(dst), (uint8_t)value, bytes);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+}  // namespace iro

@@ -1,0 +1,416 @@
+"""ctypes binding of libiro_hip.so (include/iro_hip.h, include/iro_int8_ops.h).
+
+The host-side mirror of the reference's int8 operator interface for tests,
+the smoke check and the benchmark.  Everything runs through the C ABI of the
+HIP library; there is no other implementation behind these calls, and
+loading fails loudly when the library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libiro_hip.so")
+INCLUDE_DIR = os.path.join(os.path.dirname(HERE), "include")
+
+STRICT, GCC_FASTMATH = 0, 1
+
+_vp = C.c_void_p
+_i = C.c_int
+_lib = None
+
+
+def declared_symbols() -> list[str]:
+    """Every function name the C headers in include/ declare."""
+    names = []
+    for hdr in sorted(os.listdir(INCLUDE_DIR)):
+        if not hdr.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE_DIR, hdr)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(iro_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() "
+                           f"or make -C irodori-c_amd")
+    L = C.CDLL(LIB_PATH)
+    sig = {
+        "iro_hip_create": ([_i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_destroy": ([_vp], None),
+        "iro_hip_get_convention": ([_vp], _i),
+        "iro_hip_error": ([_vp], C.c_char_p),
+        "iro_hip_clear_error": ([_vp], None),
+        "iro_hip_sync": ([_vp], _i),
+        "iro_hip_stream": ([_vp], _vp),
+        "iro_hip_alloc": ([_vp, C.c_size_t, C.POINTER(_vp)], _i),
+        "iro_hip_free": ([_vp, _vp], _i),
+        "iro_hip_upload": ([_vp, _vp, _vp, C.c_size_t], _i),
+        "iro_hip_download": ([_vp, _vp, _vp, C.c_size_t], _i),
+        "iro_hip_fill": ([_vp, _vp, _i, C.c_size_t], _i),
+        "iro_hip_event_create": ([C.POINTER(_vp)], _i),
+        "iro_hip_event_destroy": ([_vp], None),
+        "iro_hip_event_record": ([_vp, _vp], _i),
+        "iro_hip_event_elapsed_ms": ([_vp, _vp, C.POINTER(C.c_float)], _i),
+        "iro_hip_weight_create": ([_vp, _vp, _i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_weight_create_transposed": ([_vp, _vp, _i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_weight_create_fused": ([_vp, C.POINTER(_vp), C.POINTER(_i), _i, _i, _i,
+                                         C.POINTER(_vp)], _i),
+        "iro_hip_weight_from_host": ([_vp, _vp, _vp, _vp, _i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_weight_export": ([_vp, _vp, _vp, _vp, _vp], _i),
+        "iro_hip_weight_destroy": ([_vp], None),
+        "iro_hip_weight_dims": ([_vp, C.POINTER(_i), C.POINTER(_i)], _i),
+        "iro_hip_weight_bytes": ([_vp], C.c_size_t),
+        "iro_hip_quantize_rows": ([_vp, _vp, _i, _i, _vp, _vp, _vp], _i),
+        "iro_hip_quantize_rows_residual": ([_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                                            _vp], _i),
+        "iro_hip_int8_linear_ex": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i], _i),
+        "iro_hip_int8_linear_two_term": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _i, _i], _i),
+        "iro_hip_dit_qkvg": ([_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i], _i),
+        "iro_hip_dit_linear_gated": ([_vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _i], _i),
+        "iro_hip_dit_swiglu": ([_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i], _i),
+        "iro_hip_conv1d_int8": ([_vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _vp, _i, _vp,
+                                 C.POINTER(_i)], _i),
+        "iro_hip_selfcheck": ([_vp], _i),
+        "iro_hip_backend_name": ([_vp], C.c_char_p),
+        # ops.h drop-in
+        "iro_int8_weight_quantize": ([_vp, _vp, _i, _i], _i),
+        "iro_int8_weight_quantize_transposed": ([_vp, _vp, _i, _i], _i),
+        "iro_int8_weight_free": ([_vp], None),
+        "iro_int8_weight_bytes": ([_vp], C.c_size_t),
+        "iro_int8_quantize_rows": ([_vp, _i, _i, _vp, _vp, _vp], None),
+        "iro_int8_quantize_rows_residual": ([_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+                                            None),
+        "iro_int8_linear": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp], None),
+        "iro_int8_linear_ex": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i], None),
+        "iro_int8_fast_available": ([], _i),
+        "iro_int8_prepare_backend": ([], C.c_char_p),
+        "iro_int8_selfcheck": ([], _i),
+        "iro_int8_last_error": ([], _i),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def _ptr(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+class DeviceArray:
+    """A device allocation with a numpy shape/dtype; freed with its context."""
+
+    def __init__(self, ctx: "Context", shape, dtype):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = C.c_void_p()
+        ctx._check(ctx.lib.iro_hip_alloc(ctx.h, max(self.nbytes, 1), C.byref(p)), "alloc")
+        self.ptr = p.value
+        ctx._arrays.append(self)
+
+    @property
+    def vp(self):
+        return C.c_void_p(self.ptr)
+
+    def upload(self, host):
+        host = np.ascontiguousarray(host, dtype=self.dtype)
+        assert host.nbytes == self.nbytes, (host.shape, self.shape)
+        self.ctx._check(self.ctx.lib.iro_hip_upload(self.ctx.h, self.vp, _ptr(host), self.nbytes),
+                        "upload")
+        return self
+
+    def numpy(self):
+        out = np.empty(self.shape, self.dtype)
+        self.ctx._check(self.ctx.lib.iro_hip_download(self.ctx.h, _ptr(out), self.vp, self.nbytes),
+                        "download")
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.ctx.lib.iro_hip_free(self.ctx.h, self.vp)
+            self.ptr = None
+
+
+class Weight:
+    def __init__(self, ctx: "Context", handle: int):
+        self.ctx = ctx
+        self.h = C.c_void_p(handle)
+        n, k = C.c_int(), C.c_int()
+        ctx.lib.iro_hip_weight_dims(self.h, C.byref(n), C.byref(k))
+        self.N, self.K = n.value, k.value
+
+    def export(self):
+        q = np.empty((self.N, self.K), np.int8)
+        s = np.empty(self.N, np.float32)
+        cs = np.empty(self.N, np.int32)
+        self.ctx._check(self.ctx.lib.iro_hip_weight_export(self.ctx.h, self.h, _ptr(q), _ptr(s),
+                                                           _ptr(cs)), "weight_export")
+        return q, s, cs
+
+    def nbytes(self):
+        return self.ctx.lib.iro_hip_weight_bytes(self.h)
+
+    def destroy(self):
+        if self.h:
+            self.ctx.lib.iro_hip_weight_destroy(self.h)
+            self.h = None
+
+
+class Context:
+    """One HIP device context (stream, convention, workspace)."""
+
+    def __init__(self, device: int = 0, convention: int = STRICT):
+        self.lib = load()
+        h = C.c_void_p()
+        rc = self.lib.iro_hip_create(device, convention, C.byref(h))
+        if rc != 0 or not h.value:
+            raise HipError("iro_hip_create failed (no usable gfx950 device or selfcheck failed)")
+        self.h = h
+        self.convention = convention
+        self._arrays: list[DeviceArray] = []
+        self._weights: list[Weight] = []
+
+    # -- plumbing --------------------------------------------------------------
+    def _check(self, rc, what):
+        if rc != 0:
+            msg = self.lib.iro_hip_error(self.h).decode(errors="replace")
+            self.lib.iro_hip_clear_error(self.h)
+            raise HipError(f"{what}: {msg}")
+
+    def release_all(self):
+        """Free every array and weight made through this context so far."""
+        for w in self._weights:
+            w.destroy()
+        for a in self._arrays:
+            a.free()
+        self._weights.clear()
+        self._arrays.clear()
+
+    def close(self):
+        for w in self._weights:
+            w.destroy()
+        for a in self._arrays:
+            a.free()
+        self._weights.clear()
+        self._arrays.clear()
+        if self.h:
+            self.lib.iro_hip_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def sync(self):
+        self._check(self.lib.iro_hip_sync(self.h), "sync")
+
+    def backend(self) -> str:
+        return self.lib.iro_hip_backend_name(self.h).decode()
+
+    def empty(self, shape, dtype) -> DeviceArray:
+        return DeviceArray(self, shape, dtype)
+
+    def to_device(self, host) -> DeviceArray:
+        host = np.ascontiguousarray(host)
+        return DeviceArray(self, host.shape, host.dtype).upload(host)
+
+    def fill(self, arr: DeviceArray, value: int = 0):
+        self._check(self.lib.iro_hip_fill(self.h, arr.vp, value, arr.nbytes), "fill")
+
+    def selfcheck(self) -> int:
+        return self.lib.iro_hip_selfcheck(self.h)
+
+    # -- events --------------------------------------------------------------------
+    def event(self):
+        e = C.c_void_p()
+        if self.lib.iro_hip_event_create(C.byref(e)) != 0:
+            raise HipError("event_create")
+        return e
+
+    def record(self, ev):
+        self._check(self.lib.iro_hip_event_record(self.h, ev), "event_record")
+
+    def elapsed_ms(self, e0, e1) -> float:
+        ms = C.c_float()
+        if self.lib.iro_hip_event_elapsed_ms(e0, e1, C.byref(ms)) != 0:
+            raise HipError("event_elapsed")
+        return ms.value
+
+    # -- weights ---------------------------------------------------------------------
+    def weight(self, w_dev: DeviceArray, N: int, K: int, transposed: bool = False) -> Weight:
+        h = C.c_void_p()
+        fn = (self.lib.iro_hip_weight_create_transposed if transposed
+              else self.lib.iro_hip_weight_create)
+        self._check(fn(self.h, w_dev.vp, N, K, C.byref(h)), "weight_create")
+        w = Weight(self, h.value)
+        self._weights.append(w)
+        return w
+
+    def weight_fused(self, parts: list[DeviceArray], parts_N: list[int], K: int,
+                     layout: int) -> Weight:
+        h = C.c_void_p()
+        arr = (C.c_void_p * len(parts))(*[p.ptr for p in parts])
+        pn = (C.c_int * len(parts))(*parts_N)
+        self._check(self.lib.iro_hip_weight_create_fused(self.h, arr, pn, len(parts), K, layout,
+                                                         C.byref(h)), "weight_create_fused")
+        w = Weight(self, h.value)
+        self._weights.append(w)
+        return w
+
+    def weight_from_host(self, q, scale, colsum) -> Weight:
+        q = np.ascontiguousarray(q, np.int8)
+        N, K = q.shape
+        h = C.c_void_p()
+        self._check(self.lib.iro_hip_weight_from_host(
+            self.h, _ptr(q), _ptr(np.ascontiguousarray(scale, np.float32)),
+            _ptr(np.ascontiguousarray(colsum, np.int32)), N, K, C.byref(h)), "weight_from_host")
+        w = Weight(self, h.value)
+        self._weights.append(w)
+        return w
+
+    # -- ops (device arrays in, device arrays out) -----------------------------------
+    def quantize_rows(self, x: DeviceArray, q, s, z):
+        M, K = x.shape
+        self._check(self.lib.iro_hip_quantize_rows(self.h, x.vp, M, K, q.vp, s.vp, z.vp),
+                    "quantize_rows")
+
+    def quantize_rows_residual(self, x, q1, s1, z1, r, q2, s2, z2):
+        M, K = x.shape
+        self._check(self.lib.iro_hip_quantize_rows_residual(
+            self.h, x.vp, M, K, q1.vp, s1.vp, z1.vp, None if r is None else r.vp, q2.vp, s2.vp,
+            z2.vp), "quantize_rows_residual")
+
+    def linear_ex(self, q, s, z, w: Weight, bias, y, M, work=None, accumulate=False):
+        self._check(self.lib.iro_hip_int8_linear_ex(
+            self.h, q.vp, s.vp, z.vp, w.h, None if bias is None else bias.vp, y.vp, M,
+            None if work is None else work.vp, int(bool(accumulate))), "int8_linear_ex")
+
+    def linear_two_term(self, q1, s1, z1, q2, s2, z2, w: Weight, bias, y, M, accumulate=False):
+        self._check(self.lib.iro_hip_int8_linear_two_term(
+            self.h, q1.vp, s1.vp, z1.vp, q2.vp, s2.vp, z2.vp, w.h,
+            None if bias is None else bias.vp, y.vp, M, int(bool(accumulate))),
+            "int8_linear_two_term")
+
+    def dit_qkvg(self, x, M, w, q, k, v, g, residual=False):
+        self._check(self.lib.iro_hip_dit_qkvg(self.h, x.vp, M, w.h, q.vp, k.vp, v.vp, g.vp,
+                                              int(bool(residual))), "dit_qkvg")
+
+    def dit_linear_gated(self, mix, M, w, residual, out=None, x_res=None, gate=None, S=1):
+        self._check(self.lib.iro_hip_dit_linear_gated(
+            self.h, mix.vp, M, w.h, int(bool(residual)), None if out is None else out.vp,
+            None if x_res is None else x_res.vp, None if gate is None else gate.vp, S),
+            "dit_linear_gated")
+
+    def dit_swiglu(self, h, M, w13, w2, residual_w13=False, residual_w2=True, hidden=None,
+                   out=None, x_res=None, gate=None, S=1):
+        self._check(self.lib.iro_hip_dit_swiglu(
+            self.h, h.vp, M, w13.h, w2.h, int(bool(residual_w13)), int(bool(residual_w2)),
+            None if hidden is None else hidden.vp, None if out is None else out.vp,
+            None if x_res is None else x_res.vp, None if gate is None else gate.vp, S),
+            "dit_swiglu")
+
+    def conv1d(self, x, T, Cin, w, kernel, stride, dilation, padding, bias, residual, y):
+        t_out = C.c_int()
+        self._check(self.lib.iro_hip_conv1d_int8(
+            self.h, x.vp, T, Cin, w.h, kernel, stride, dilation, padding,
+            None if bias is None else bias.vp, int(bool(residual)), y.vp, C.byref(t_out)),
+            "conv1d_int8")
+        return t_out.value
+
+
+class _Int8Weight(C.Structure):
+    # include/iro_int8_ops.h IroInt8Weight (ops.h:23-28)
+    _fields_ = [("data", C.POINTER(C.c_int8)), ("scale", C.POINTER(C.c_float)),
+                ("colsum", C.POINTER(C.c_int32)), ("N", C.c_int), ("K", C.c_int)]
+
+
+class Ops:
+    """The ops.h drop-in (host pointers), exactly as dit.c/dacvae.c call it."""
+
+    def __init__(self):
+        self.lib = load()
+
+    def weight_quantize(self, w, transposed_shape=None):
+        w = np.ascontiguousarray(w, np.float32)
+        st = _Int8Weight()
+        if transposed_shape is None:
+            N, K = w.shape
+            rc = self.lib.iro_int8_weight_quantize(C.byref(st), _ptr(w), N, K)
+        else:
+            N, K = transposed_shape
+            rc = self.lib.iro_int8_weight_quantize_transposed(C.byref(st), _ptr(w), N, K)
+        if rc != 0:
+            raise HipError("iro_int8_weight_quantize failed")
+        return st
+
+    @staticmethod
+    def weight_arrays(st):
+        N, K = st.N, st.K
+        return (np.ctypeslib.as_array(st.data, (N * K,)).reshape(N, K).copy(),
+                np.ctypeslib.as_array(st.scale, (N,)).copy(),
+                np.ctypeslib.as_array(st.colsum, (N,)).copy())
+
+    def weight_free(self, st):
+        self.lib.iro_int8_weight_free(C.byref(st))
+
+    def weight_bytes(self, st):
+        return self.lib.iro_int8_weight_bytes(C.byref(st))
+
+    def quantize_rows(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        q = np.empty((M, K), np.uint8)
+        s = np.empty(M, np.float32)
+        z = np.empty(M, np.int32)
+        self.lib.iro_int8_quantize_rows(_ptr(x), M, K, _ptr(q), _ptr(s), _ptr(z))
+        return q, s, z
+
+    def quantize_rows_residual(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        q1, q2 = np.empty((M, K), np.uint8), np.empty((M, K), np.uint8)
+        r = np.empty((M, K), np.float32)
+        s1, s2 = np.empty(M, np.float32), np.empty(M, np.float32)
+        z1, z2 = np.empty(M, np.int32), np.empty(M, np.int32)
+        self.lib.iro_int8_quantize_rows_residual(_ptr(x), M, K, _ptr(q1), _ptr(s1), _ptr(z1),
+                                                 _ptr(r), _ptr(q2), _ptr(s2), _ptr(z2))
+        return (q1, s1, z1), r, (q2, s2, z2)
+
+    def linear_ex(self, q, s, z, st, bias=None, y=None, accumulate=False):
+        q = np.ascontiguousarray(q, np.uint8)
+        M = q.shape[0]
+        N = st.N
+        y = np.zeros((M, N), np.float32) if y is None else np.array(y, np.float32, copy=True)
+        work = np.empty((M, N), np.int32)
+        self.lib.iro_int8_linear_ex(_ptr(q), _ptr(np.ascontiguousarray(s, np.float32)),
+                                    _ptr(np.ascontiguousarray(z, np.int32)), C.byref(st),
+                                    None if bias is None else _ptr(np.ascontiguousarray(bias, np.float32)),
+                                    _ptr(y), M, _ptr(work), int(bool(accumulate)))
+        return y, work
+
+    def selfcheck(self):
+        return self.lib.iro_int8_selfcheck()
+
+    def last_error(self):
+        return self.lib.iro_int8_last_error()

@@ -1,0 +1,392 @@
+/* iro_oracle.c -- CPU restatement of irodori-c's int8 W8A8 path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker): never linked into, loaded by or
+ * called from the HIP product library.
+ *
+ * Build with -ffp-contract=off and without -ffast-math: every float
+ * operation below rounds exactly where it is written.  Where the reference's
+ * fast-math build fuses a multiply-add, this file calls fmaf() explicitly.
+ * Each function cites the reference lines it restates.
+ */
+#include "iro_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Constants GCC 11 folds into the fast-math build of ops.c/dacvae.c:
+ *   x / 255.0f   ->  x * fl(1/255)            0x3B808081
+ *   1 / (d/255)  ->  fl(1/fl(1/255)) / d       0x437EFFFF (254.99998)
+ *   255 / (d/255)->  fl(255/fl(1/255)) / d     0x477E00FF (65024.996)
+ *   x / 127.0f   ->  x * fl(1/127)            0x3C010204
+ *   1 / (a/127)  ->  127 / a                   0x42FE0000
+ */
+static float f32_bits(uint32_t u) {
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+#define C_INV255 f32_bits(0x3B808081u)
+#define C_255_OVER_INV255 f32_bits(0x437EFFFFu)
+#define C_255_OVER_INV255_B f32_bits(0x477E00FFu)
+#define C_INV127 f32_bits(0x3C010204u)
+
+static int clamp_i(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* Round-to-nearest-even, as nearbyintf / cvtss2si / vrndscaleps $12 under
+   the default MXCSR. */
+static float rne(float v) { return rintf(v); }
+
+/* ---- weights: ops.c:259-293 ------------------------------------------ */
+
+static void weight_row(int conv, const float *row, int K, int8_t *q,
+                       float *scale_out, int32_t *colsum_out) {
+    float amax = 0.0f;
+    for (int k = 0; k < K; k++) {
+        float a = fabsf(row[k]);
+        if (a > amax) amax = a;
+    }
+    float scale, inv;
+    if (conv == ORC_GCC_FASTMATH) {
+        if (amax > 0.0f) {
+            scale = amax * C_INV127;
+            inv = 127.0f / amax;
+        } else {
+            scale = 1.0f;
+            inv = 1.0f;
+        }
+    } else {
+        scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        inv = 1.0f / scale;
+    }
+    int32_t sum = 0;
+    for (int k = 0; k < K; k++) {
+        int v = (int)rne(row[k] * inv);
+        v = clamp_i(v, -127, 127);
+        q[k] = (int8_t)v;
+        sum += v;
+    }
+    *scale_out = scale;
+    *colsum_out = sum;
+}
+
+int orc_weight_quantize(int conv, const float *w, int N, int K,
+                        int8_t *q, float *scale, int32_t *colsum) {
+    if (!w || !q || !scale || !colsum || N <= 0 || K <= 0) return -1;
+    for (int n = 0; n < N; n++)
+        weight_row(conv, w + (size_t)n * K, K, q + (size_t)n * K, &scale[n],
+                   &colsum[n]);
+    return 0;
+}
+
+int orc_weight_quantize_transposed(int conv, const float *w, int N, int K,
+                                   int8_t *q, float *scale, int32_t *colsum) {
+    if (!w || N <= 0 || K <= 0) return -1;
+    float *t = malloc(sizeof(float) * (size_t)N * K);
+    if (!t) return -1;
+    for (int k = 0; k < K; k++)
+        for (int n = 0; n < N; n++) t[(size_t)n * K + k] = w[(size_t)k * N + n];
+    int rc = orc_weight_quantize(conv, t, N, K, q, scale, colsum);
+    free(t);
+    return rc;
+}
+
+/* ---- activations: ops.c:321-348 -------------------------------------- */
+
+typedef struct {
+    float s, inv, zpf;
+    int zp;
+} RowQuant;
+
+/* Scale and zero point of a row whose range (with zero) is [lo, hi]. */
+static RowQuant row_params(int conv, float lo, float hi) {
+    RowQuant r;
+    float d = hi - lo;
+    if (conv == ORC_GCC_FASTMATH) {
+        r.s = d * C_INV255;
+        if (!(r.s > 0.0f)) {
+            r.s = 1.0f;
+            r.inv = 1.0f;
+            r.zp = clamp_i((int)rne(-lo), 0, 255);
+        } else {
+            r.inv = C_255_OVER_INV255 / d;
+            r.zp = clamp_i((int)rne(-(lo * r.inv)), 0, 255);
+        }
+    } else {
+        r.s = d / 255.0f;
+        if (!(r.s > 0.0f)) r.s = 1.0f;
+        r.inv = 1.0f / r.s;
+        r.zp = clamp_i((int)rne(-lo * r.inv), 0, 255);
+    }
+    r.zpf = (float)r.zp;
+    return r;
+}
+
+static uint8_t quant_code(int conv, float x, const RowQuant *r) {
+    float v = conv == ORC_GCC_FASTMATH ? rne(fmaf(x, r->inv, r->zpf))
+                                        : rne(x * r->inv + r->zpf);
+    v = v < 0.0f ? 0.0f : v;
+    v = v > 255.0f ? 255.0f : v;
+    return (uint8_t)v;
+}
+
+static void row_range(const float *row, int K, float *lo_out, float *hi_out) {
+    float lo = 0.0f, hi = 0.0f;
+    for (int k = 0; k < K; k++) {
+        lo = row[k] < lo ? row[k] : lo;
+        hi = row[k] > hi ? row[k] : hi;
+    }
+    *lo_out = lo;
+    *hi_out = hi;
+}
+
+void orc_quantize_rows(int conv, const float *x, int M, int K,
+                       uint8_t *q, float *scale, int32_t *zero) {
+    for (int m = 0; m < M; m++) {
+        const float *row = x + (size_t)m * K;
+        uint8_t *qrow = q + (size_t)m * K;
+        float lo, hi;
+        row_range(row, K, &lo, &hi);
+        RowQuant r = row_params(conv, lo, hi);
+        for (int k = 0; k < K; k++) qrow[k] = quant_code(conv, row[k], &r);
+        scale[m] = r.s;
+        zero[m] = r.zp;
+    }
+}
+
+/* ops.c:427-442: r = x - s1*(q1 - zp1), then requantize r. */
+void orc_quantize_rows_residual(int conv, const float *x, int M, int K,
+                                uint8_t *q1, float *scale1, int32_t *zero1,
+                                float *residual,
+                                uint8_t *q2, float *scale2, int32_t *zero2) {
+    float *r = residual;
+    float *own = NULL;
+    if (!r) {
+        own = malloc(sizeof(float) * (size_t)K);
+        if (!own) return;
+    }
+    orc_quantize_rows(conv, x, M, K, q1, scale1, zero1);
+    for (int m = 0; m < M; m++) {
+        const float *row = x + (size_t)m * K;
+        const uint8_t *qrow = q1 + (size_t)m * K;
+        float *rrow = own ? own : r + (size_t)m * K;
+        const float s = scale1[m];
+        const float zp = (float)zero1[m];
+        for (int k = 0; k < K; k++) {
+            if (conv == ORC_GCC_FASTMATH)
+                rrow[k] = fmaf(s, zp - (float)qrow[k], row[k]);
+            else
+                rrow[k] = row[k] - s * ((float)qrow[k] - zp);
+        }
+        if (own)
+            orc_quantize_rows(conv, own, 1, K, q2 + (size_t)m * K, scale2 + m,
+                              zero2 + m);
+    }
+    if (!own) orc_quantize_rows(conv, r, M, K, q2, scale2, zero2);
+    free(own);
+}
+
+/* ---- integer GEMM: ops.c:351-364 ------------------------------------- */
+
+void orc_gemm_u8s8(const uint8_t *a, const int8_t *b, int32_t *c,
+                   int M, int N, int K, int threads) {
+#ifdef _OPENMP
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) num_threads(threads)
+#else
+    (void)threads;
+#endif
+    for (int m = 0; m < M; m++) {
+        const uint8_t *arow = a + (size_t)m * K;
+        int32_t *crow = c + (size_t)m * N;
+        for (int n = 0; n < N; n++) {
+            const int8_t *brow = b + (size_t)n * K;
+            int32_t acc = 0;
+            for (int k = 0; k < K; k++) acc += (int32_t)arow[k] * (int32_t)brow[k];
+            crow[n] = acc;
+        }
+    }
+}
+
+/* ---- epilogue: ops.c:468-490 ------------------------------------------ */
+
+void orc_epilogue(int conv, const int32_t *acc, const float *sx,
+                  const int32_t *zx, const float *sw, const int32_t *colsum,
+                  const float *bias, float *y, int M, int N, int accumulate) {
+    const int fast = conv == ORC_GCC_FASTMATH;
+    for (int m = 0; m < M; m++) {
+        const int32_t *crow = acc + (size_t)m * N;
+        float *yrow = y + (size_t)m * N;
+        for (int n = 0; n < N; n++) {
+            const float t = (float)(crow[n] - zx[m] * colsum[n]);
+            const float c = sx[m] * sw[n];
+            if (accumulate && bias) {
+                yrow[n] = fast ? fmaf(t, c, yrow[n] + bias[n])
+                               : yrow[n] + (t * c + bias[n]);
+            } else if (accumulate) {
+                yrow[n] = fast ? fmaf(t, c, yrow[n]) : yrow[n] + t * c;
+            } else if (bias) {
+                yrow[n] = fast ? fmaf(t, c, bias[n]) : t * c + bias[n];
+            } else {
+                yrow[n] = t * c;
+            }
+        }
+    }
+}
+
+void orc_int8_linear_ex(int conv, const uint8_t *q, const float *sx,
+                        const int32_t *zx, const int8_t *wq, const float *sw,
+                        const int32_t *colsum, int N, int K,
+                        const float *bias, float *y, int M, int32_t *work,
+                        int accumulate, int threads) {
+    orc_gemm_u8s8(q, wq, work, M, N, K, threads);
+    orc_epilogue(conv, work, sx, zx, sw, colsum, bias, y, M, N, accumulate);
+}
+
+/* ---- known answer: ops.c:375-398 ---------------------------------------- */
+
+void orc_selfcheck_kat(uint8_t *a, int8_t *b, int32_t *want) {
+    enum { M = 3, N = 5, K = 64 };
+    for (int i = 0; i < M * K; i++) a[i] = (uint8_t)(i % 3 == 0 ? 255 : 200 + i % 50);
+    for (int i = 0; i < N * K; i++)
+        b[i] = (int8_t)(i % 4 == 0 ? 127 : (i % 4 == 1 ? -127 : 90 - i % 60));
+    orc_gemm_u8s8(a, b, want, M, N, K, 1);
+}
+
+/* ---- SwiGLU gate: ops.c:781-784 (strict build) ------------------------ */
+
+void orc_silu_mul(float *x, const float *g, size_t n) {
+    for (size_t i = 0; i < n; i++) x[i] = (x[i] / (1.0f + expf(-x[i]))) * g[i];
+}
+
+/* ---- gated residual: dit.c:1013-1020, 1032-1039 ------------------------ */
+
+void orc_gated_residual(int conv, float *x, const float *gate,
+                        const float *branch, int B, int S, int D) {
+    for (int b = 0; b < B; b++) {
+        const float *grow = gate + (size_t)b * D;
+        for (int s = 0; s < S; s++) {
+            size_t row = ((size_t)b * S + s) * D;
+            for (int i = 0; i < D; i++) {
+                if (conv == ORC_GCC_FASTMATH)
+                    x[row + i] = fmaf(grow[i], branch[row + i], x[row + i]);
+                else
+                    x[row + i] = x[row + i] + grow[i] * branch[row + i];
+            }
+        }
+    }
+}
+
+/* ---- int8 Conv1d: dacvae.c:340-348, 543-688 ----------------------------- */
+
+int orc_conv1d_output_length(int T, int kernel, int stride, int dilation,
+                             int padding) {
+    if (T <= 0 || stride <= 0 || kernel <= 0 || dilation <= 0) return -1;
+    long long effective = (long long)dilation * (kernel - 1) + 1;
+    long long num = (long long)T + 2LL * padding - effective;
+    long long out = num < 0 ? -1 : num / stride + 1;
+    return out <= 0 || out > 0x7fffffffLL ? -1 : (int)out;
+}
+
+int orc_conv1d_int8(int conv, const float *input, int T, int C,
+                    const int8_t *wq, const float *sw, const int32_t *colsum,
+                    int N, int kernel, int stride, int dilation, int padding,
+                    const float *bias, int residual, float *output,
+                    uint8_t *cols, float *row_scale, int32_t *row_zero,
+                    int threads) {
+    const int T_out = orc_conv1d_output_length(T, kernel, stride, dilation, padding);
+    if (T_out <= 0 || C <= 0 || N <= 0) return -1;
+    const int inner = kernel * C;
+    const int fast = conv == ORC_GCC_FASTMATH;
+    /* Per input row (time step) range over channels, with zero included
+       (dacvae.c:607-616). */
+    float *row_lo = malloc(sizeof(float) * (size_t)T);
+    float *row_hi = malloc(sizeof(float) * (size_t)T);
+    uint8_t *c1 = cols ? cols : malloc((size_t)T_out * inner);
+    uint8_t *c2 = residual ? malloc((size_t)T_out * inner) : NULL;
+    float *s1 = malloc(sizeof(float) * (size_t)T_out);
+    int32_t *z1 = malloc(sizeof(int32_t) * (size_t)T_out);
+    float *s2 = residual ? malloc(sizeof(float) * (size_t)T_out) : NULL;
+    int32_t *z2 = residual ? malloc(sizeof(int32_t) * (size_t)T_out) : NULL;
+    int32_t *work = malloc(sizeof(int32_t) * (size_t)T_out * N);
+    int ok = row_lo && row_hi && c1 && s1 && z1 && work &&
+             (!residual || (c2 && s2 && z2));
+    if (ok) {
+        for (int t = 0; t < T; t++) row_range(input + (size_t)t * C, C, &row_lo[t], &row_hi[t]);
+        for (int r = 0; r < T_out; r++) {
+            /* Window range over the taps that land inside [0, T)
+               (dacvae.c:617-627); padding taps do not widen it. */
+            float lo = 0.0f, hi = 0.0f;
+            for (int tap = 0; tap < kernel; tap++) {
+                int it = r * stride - padding + tap * dilation;
+                if (it < 0 || it >= T) continue;
+                lo = row_lo[it] < lo ? row_lo[it] : lo;
+                hi = row_hi[it] > hi ? row_hi[it] : hi;
+            }
+            RowQuant q = row_params(conv, lo, hi);
+            float sc2, inv2;
+            if (fast) {
+                /* dacvae.c:637-638 under fast-math: s/255 -> s*fl(1/255),
+                   255/s -> 0x477E00FF/(hi-lo) (s=1 rows are all-zero windows
+                   whose plane-2 codes are 128 regardless of inv2). */
+                sc2 = q.s * C_INV255;
+                float d = hi - lo;
+                inv2 = (hi - lo) * C_INV255 > 0.0f ? C_255_OVER_INV255_B / d : 255.0f;
+            } else {
+                sc2 = q.s / 255.0f;
+                inv2 = 255.0f / q.s;
+            }
+            s1[r] = q.s;
+            z1[r] = q.zp;
+            if (residual) {
+                s2[r] = sc2;
+                z2[r] = 128;
+            }
+            uint8_t *dst = c1 + (size_t)r * inner;
+            uint8_t *dst2 = residual ? c2 + (size_t)r * inner : NULL;
+            for (int tap = 0; tap < kernel; tap++) {
+                int it = r * stride - padding + tap * dilation;
+                uint8_t *td = dst + (size_t)tap * C;
+                if (it < 0 || it >= T) {
+                    memset(td, q.zp, (size_t)C);
+                    if (residual) memset(dst2 + (size_t)tap * C, 128, (size_t)C);
+                    continue;
+                }
+                const float *row = input + (size_t)it * C;
+                for (int c = 0; c < C; c++) {
+                    uint8_t code = quant_code(conv, row[c], &q);
+                    td[c] = code;
+                    if (residual) {
+                        float v = (float)code;
+                        float rem, v2;
+                        if (fast) {
+                            rem = fmaf(q.s, q.zpf - v, row[c]);
+                            v2 = rne(fmaf(rem, inv2, 128.0f));
+                        } else {
+                            rem = row[c] - q.s * (v - q.zpf);
+                            v2 = rne(rem * inv2 + 128.0f);
+                        }
+                        v2 = v2 < 0.0f ? 0.0f : v2;
+                        v2 = v2 > 255.0f ? 255.0f : v2;
+                        dst2[(size_t)tap * C + c] = (uint8_t)v2;
+                    }
+                }
+            }
+        }
+        orc_int8_linear_ex(conv, c1, s1, z1, wq, sw, colsum, N, inner, bias,
+                           output, T_out, work, 0, threads);
+        if (residual)
+            orc_int8_linear_ex(conv, c2, s2, z2, wq, sw, colsum, N, inner, NULL,
+                               output, T_out, work, 1, threads);
+        if (row_scale) memcpy(row_scale, s1, sizeof(float) * (size_t)T_out);
+        if (row_zero) memcpy(row_zero, z1, sizeof(int32_t) * (size_t)T_out);
+    }
+    free(row_lo); free(row_hi);
+    if (!cols) free(c1);
+    free(c2); free(s1); free(z1); free(s2); free(z2); free(work);
+    return ok ? T_out : -1;
+}

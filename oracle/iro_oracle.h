@@ -1,0 +1,100 @@
+/* iro_oracle.h -- CPU restatement of irodori-c's int8 W8A8 path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: the HIP product
+ * path never links, loads or calls it.  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may use it.
+ *
+ * Two rounding conventions are restated, because the reference's results
+ * depend on how it was compiled (Makefile:4-7):
+ *   ORC_STRICT        ops.c built with -O2 (the default `make irodori`,
+ *                     `make test-int8-ops`): every float op rounds
+ *                     separately, divisions are true divisions.
+ *   ORC_GCC_FASTMATH  ops.c/dit.c/dacvae.c built with FAST_CFLAGS
+ *                     (-O3 -march=native -ffast-math, the oneMKL release
+ *                     build): GCC 11 folds the divisions by 255/127 into
+ *                     reciprocal constants and contracts mul+add into FMA.
+ * Integer results (codes, int32 sums) are convention-independent only
+ * through the scales that produce them.
+ */
+#ifndef IRO_ORACLE_H
+#define IRO_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_STRICT = 0, ORC_GCC_FASTMATH = 1 };
+
+/* ops.c:259-293 (iro_int8_weight_quantize). q [N,K] s8, scale[N], colsum[N]. */
+int orc_weight_quantize(int conv, const float *w, int N, int K,
+                        int8_t *q, float *scale, int32_t *colsum);
+/* ops.c:295-306: source stored [K,N]; result as orc_weight_quantize. */
+int orc_weight_quantize_transposed(int conv, const float *w, int N, int K,
+                                   int8_t *q, float *scale, int32_t *colsum);
+
+/* ops.c:321-348 (iro_int8_quantize_rows). */
+void orc_quantize_rows(int conv, const float *x, int M, int K,
+                       uint8_t *q, float *scale, int32_t *zero);
+
+/* ops.c:427-442 (iro_int8_quantize_rows_residual). residual may be NULL. */
+void orc_quantize_rows_residual(int conv, const float *x, int M, int K,
+                                uint8_t *q1, float *scale1, int32_t *zero1,
+                                float *residual,
+                                uint8_t *q2, float *scale2, int32_t *zero2);
+
+/* ops.c:351-364 (int8_gemm_reference): exact c = a[M,K]u8 . b[N,K]s8^T.
+   threads > 1 splits rows across OpenMP threads (integer, order-free). */
+void orc_gemm_u8s8(const uint8_t *a, const int8_t *b, int32_t *c,
+                   int M, int N, int K, int threads);
+
+/* ops.c:468-490: the four epilogue branches on a precomputed accumulator. */
+void orc_epilogue(int conv, const int32_t *acc, const float *sx,
+                  const int32_t *zx, const float *sw, const int32_t *colsum,
+                  const float *bias, float *y, int M, int N, int accumulate);
+
+/* ops.c:450-491 (iro_int8_linear_ex): gemm then epilogue. work [M,N]. */
+void orc_int8_linear_ex(int conv, const uint8_t *q, const float *sx,
+                        const int32_t *zx, const int8_t *wq, const float *sw,
+                        const int32_t *colsum, int N, int K,
+                        const float *bias, float *y, int M, int32_t *work,
+                        int accumulate, int threads);
+
+/* ops.c:375-398 (iro_int8_selfcheck): fills the known-answer arrays
+   a[3*64], b[5*64] and the exact sums want[3*5]. */
+void orc_selfcheck_kat(uint8_t *a, int8_t *b, int32_t *want);
+
+/* ops.c:781-784 (iro_silu_mul_inplace), strict build: x = x/(1+expf(-x))*g
+   with glibc's scalar expf. The fast-math build vectorises this with libmvec
+   expf and an rcpps Newton step, whose results depend on the host CPU; it
+   has no portable restatement. */
+void orc_silu_mul(float *x, const float *g, size_t n);
+
+/* dit.c:1013-1020 / 1032-1039: x[b,s,:] += gate[b,:] * branch[b,s,:].
+   Strict: two roundings.  Fast-math: one FMA (vfmadd132ps). */
+void orc_gated_residual(int conv, float *x, const float *gate,
+                        const float *branch, int B, int S, int D);
+
+/* dacvae.c:543-688 (conv1d_int8_forward) without snake: input [T, C]
+   time-major, weight [N, kernel*C] (tap-major K).  cols (nullable) receives
+   the u8 im2col [T_out, kernel*C]; scale/zero (nullable) the per-output-row
+   quantization.  residual adds the fixed-scale second plane
+   (s/255, zero point 128).  Returns T_out, or -1 on bad shape. */
+int orc_conv1d_int8(int conv, const float *input, int T, int C,
+                    const int8_t *wq, const float *sw, const int32_t *colsum,
+                    int N, int kernel, int stride, int dilation, int padding,
+                    const float *bias, int residual, float *output,
+                    uint8_t *cols, float *row_scale, int32_t *row_zero,
+                    int threads);
+
+/* dacvae.c:340-348 (iro_conv1d_output_length). */
+int orc_conv1d_output_length(int T, int kernel, int stride, int dilation,
+                             int padding);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,290 @@
+"""ctypes bindings for the CPU checker (TEST INFRASTRUCTURE ONLY).
+
+`Oracle` wraps liboracle.so, the C restatement of irodori-c's int8 W8A8
+path (iro_oracle.c).  `Reference` wraps oracle/_ref/libref_{strict,fast}.so,
+the reference's own ops.c/dacvae.c compiled from its sources by
+`make -C oracle ref`; it only exists where the reference sources were
+present when the checker was built.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module.  The HIP product path never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+STRICT, GCC_FASTMATH = 0, 1
+
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int32)
+_u8p = C.POINTER(C.c_uint8)
+_i8p = C.POINTER(C.c_int8)
+
+
+def _p(a, ct):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ct)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Oracle:
+    """The C restatement (iro_oracle.c), both rounding conventions."""
+
+    def __init__(self, path: str | None = None):
+        path = path or os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        self.lib = L = C.CDLL(path)
+        L.orc_weight_quantize.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p]
+        L.orc_weight_quantize_transposed.argtypes = L.orc_weight_quantize.argtypes
+        L.orc_quantize_rows.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _u8p, _f32p, _i32p]
+        L.orc_quantize_rows_residual.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _u8p, _f32p,
+                                                 _i32p, _f32p, _u8p, _f32p, _i32p]
+        L.orc_gemm_u8s8.argtypes = [_u8p, _i8p, _i32p, C.c_int, C.c_int, C.c_int, C.c_int]
+        L.orc_epilogue.argtypes = [C.c_int, _i32p, _f32p, _i32p, _f32p, _i32p, _f32p, _f32p,
+                                   C.c_int, C.c_int, C.c_int]
+        L.orc_selfcheck_kat.argtypes = [_u8p, _i8p, _i32p]
+        L.orc_silu_mul.argtypes = [_f32p, _f32p, C.c_size_t]
+        L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_conv1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p,
+                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int,
+                                      _f32p, _u8p, _f32p, _i32p, C.c_int]
+        L.orc_conv1d_int8.restype = C.c_int
+        L.orc_conv1d_output_length.argtypes = [C.c_int] * 5
+        L.orc_conv1d_output_length.restype = C.c_int
+        self.threads = min(8, os.cpu_count() or 1)
+
+    def weight_quantize(self, conv, w):
+        w = _f32(w)
+        N, K = w.shape
+        q = np.empty((N, K), np.int8)
+        s = np.empty(N, np.float32)
+        cs = np.empty(N, np.int32)
+        rc = self.lib.orc_weight_quantize(conv, _p(w, _f32p), N, K, _p(q, _i8p), _p(s, _f32p),
+                                          _p(cs, _i32p))
+        assert rc == 0
+        return q, s, cs
+
+    def weight_quantize_transposed(self, conv, w_kn, N, K):
+        w_kn = _f32(w_kn)
+        q = np.empty((N, K), np.int8)
+        s = np.empty(N, np.float32)
+        cs = np.empty(N, np.int32)
+        rc = self.lib.orc_weight_quantize_transposed(conv, _p(w_kn, _f32p), N, K, _p(q, _i8p),
+                                                     _p(s, _f32p), _p(cs, _i32p))
+        assert rc == 0
+        return q, s, cs
+
+    def quantize_rows(self, conv, x):
+        x = _f32(x)
+        M, K = x.shape
+        q = np.empty((M, K), np.uint8)
+        s = np.empty(M, np.float32)
+        z = np.empty(M, np.int32)
+        self.lib.orc_quantize_rows(conv, _p(x, _f32p), M, K, _p(q, _u8p), _p(s, _f32p),
+                                   _p(z, _i32p))
+        return q, s, z
+
+    def quantize_rows_residual(self, conv, x):
+        x = _f32(x)
+        M, K = x.shape
+        q1 = np.empty((M, K), np.uint8)
+        q2 = np.empty((M, K), np.uint8)
+        r = np.empty((M, K), np.float32)
+        s1, s2 = np.empty(M, np.float32), np.empty(M, np.float32)
+        z1, z2 = np.empty(M, np.int32), np.empty(M, np.int32)
+        self.lib.orc_quantize_rows_residual(conv, _p(x, _f32p), M, K, _p(q1, _u8p), _p(s1, _f32p),
+                                            _p(z1, _i32p), _p(r, _f32p), _p(q2, _u8p),
+                                            _p(s2, _f32p), _p(z2, _i32p))
+        return (q1, s1, z1), r, (q2, s2, z2)
+
+    def gemm(self, a, b):
+        a = np.ascontiguousarray(a, np.uint8)
+        b = np.ascontiguousarray(b, np.int8)
+        M, K = a.shape
+        N = b.shape[0]
+        c = np.empty((M, N), np.int32)
+        self.lib.orc_gemm_u8s8(_p(a, _u8p), _p(b, _i8p), _p(c, _i32p), M, N, K, self.threads)
+        return c
+
+    def epilogue(self, conv, acc, sx, zx, sw, colsum, bias=None, y=None, accumulate=False):
+        acc = np.ascontiguousarray(acc, np.int32)
+        M, N = acc.shape
+        if y is None:
+            y = np.zeros((M, N), np.float32)
+        else:
+            y = np.array(y, np.float32, copy=True)
+        self.lib.orc_epilogue(conv, _p(acc, _i32p), _p(_f32(sx), _f32p),
+                              _p(np.ascontiguousarray(zx, np.int32), _i32p), _p(_f32(sw), _f32p),
+                              _p(np.ascontiguousarray(colsum, np.int32), _i32p),
+                              _p(None if bias is None else _f32(bias), _f32p), _p(y, _f32p), M, N,
+                              int(bool(accumulate)))
+        return y
+
+    def linear(self, conv, q, sx, zx, wq, sw, colsum, bias=None, y=None, accumulate=False):
+        """ops.c:450-491: returns (y, work)."""
+        work = self.gemm(q, wq)
+        return self.epilogue(conv, work, sx, zx, sw, colsum, bias, y, accumulate), work
+
+    def selfcheck_kat(self):
+        a = np.empty(3 * 64, np.uint8)
+        b = np.empty(5 * 64, np.int8)
+        want = np.empty(15, np.int32)
+        self.lib.orc_selfcheck_kat(_p(a, _u8p), _p(b, _i8p), _p(want, _i32p))
+        return a.reshape(3, 64), b.reshape(5, 64), want.reshape(3, 5)
+
+    def silu_mul(self, a, g):
+        a = np.array(a, np.float32, copy=True)
+        g = _f32(g)
+        self.lib.orc_silu_mul(_p(a, _f32p), _p(g, _f32p), a.size)
+        return a
+
+    def gated_residual(self, conv, x, gate, branch, B, S):
+        x = np.array(x, np.float32, copy=True)
+        D = x.shape[-1]
+        self.lib.orc_gated_residual(conv, _p(x, _f32p), _p(_f32(gate), _f32p),
+                                    _p(_f32(branch), _f32p), B, S, D)
+        return x
+
+    def conv_out_len(self, T, kernel, stride, dilation, padding):
+        return self.lib.orc_conv1d_output_length(T, kernel, stride, dilation, padding)
+
+    def conv1d(self, conv, x, wq, sw, colsum, kernel, stride, dilation, padding, bias=None,
+               residual=False, want_cols=False):
+        x = _f32(x)
+        T, Cin = x.shape
+        N = wq.shape[0]
+        To = self.conv_out_len(T, kernel, stride, dilation, padding)
+        assert To > 0
+        y = np.empty((To, N), np.float32)
+        cols = np.empty((To, kernel * Cin), np.uint8) if want_cols else None
+        s = np.empty(To, np.float32)
+        z = np.empty(To, np.int32)
+        rc = self.lib.orc_conv1d_int8(conv, _p(x, _f32p), T, Cin,
+                                      _p(np.ascontiguousarray(wq, np.int8), _i8p),
+                                      _p(_f32(sw), _f32p),
+                                      _p(np.ascontiguousarray(colsum, np.int32), _i32p), N, kernel,
+                                      stride, dilation, padding,
+                                      _p(None if bias is None else _f32(bias), _f32p),
+                                      int(bool(residual)), _p(y, _f32p), _p(cols, _u8p),
+                                      _p(s, _f32p), _p(z, _i32p), self.threads)
+        assert rc == To
+        return y, cols, s, z
+
+
+class _Weight(C.Structure):
+    # ops.h:23-28 IroInt8Weight
+    _fields_ = [("data", _i8p), ("scale", _f32p), ("colsum", _i32p), ("N", C.c_int),
+                ("K", C.c_int)]
+
+
+class Reference:
+    """The reference's own ops.c/dacvae.c built from source (oracle/_ref)."""
+
+    def __init__(self, flavour: str):
+        path = os.path.join(HERE, "_ref", f"libref_{flavour}.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = L = C.CDLL(path)
+        L.iro_int8_weight_quantize.argtypes = [C.POINTER(_Weight), _f32p, C.c_int, C.c_int]
+        L.iro_int8_weight_quantize.restype = C.c_int
+        L.iro_int8_weight_quantize_transposed.argtypes = L.iro_int8_weight_quantize.argtypes
+        L.iro_int8_weight_quantize_transposed.restype = C.c_int
+        L.iro_int8_weight_free.argtypes = [C.POINTER(_Weight)]
+        L.iro_int8_quantize_rows.argtypes = [_f32p, C.c_int, C.c_int, _u8p, _f32p, _i32p]
+        L.iro_int8_quantize_rows_residual.argtypes = [_f32p, C.c_int, C.c_int, _u8p, _f32p, _i32p,
+                                                      _f32p, _u8p, _f32p, _i32p]
+        L.iro_int8_linear_ex.argtypes = [_u8p, _f32p, _i32p, C.POINTER(_Weight), _f32p, _f32p,
+                                         C.c_int, _i32p, C.c_int]
+        L.iro_int8_selfcheck.restype = C.c_int
+        L.iro_silu_mul_inplace.argtypes = [_f32p, _f32p, C.c_size_t]
+        L.ref_conv1d_int8.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, _i8p, _f32p, _i32p, _f32p, C.c_int, _f32p]
+        L.ref_conv1d_int8.restype = C.c_int
+
+    def weight_quantize(self, w, transposed_shape=None):
+        w = _f32(w)
+        wt = _Weight()
+        if transposed_shape is None:
+            N, K = w.shape
+            rc = self.lib.iro_int8_weight_quantize(C.byref(wt), _p(w, _f32p), N, K)
+        else:
+            N, K = transposed_shape
+            rc = self.lib.iro_int8_weight_quantize_transposed(C.byref(wt), _p(w, _f32p), N, K)
+        assert rc == 0
+        q = np.ctypeslib.as_array(wt.data, (N * K,)).reshape(N, K).copy()
+        s = np.ctypeslib.as_array(wt.scale, (N,)).copy()
+        cs = np.ctypeslib.as_array(wt.colsum, (N,)).copy()
+        self.lib.iro_int8_weight_free(C.byref(wt))
+        return q, s, cs
+
+    def quantize_rows(self, x):
+        x = _f32(x)
+        M, K = x.shape
+        q = np.empty((M, K), np.uint8)
+        s = np.empty(M, np.float32)
+        z = np.empty(M, np.int32)
+        self.lib.iro_int8_quantize_rows(_p(x, _f32p), M, K, _p(q, _u8p), _p(s, _f32p),
+                                        _p(z, _i32p))
+        return q, s, z
+
+    def quantize_rows_residual(self, x):
+        x = _f32(x)
+        M, K = x.shape
+        q1 = np.empty((M, K), np.uint8)
+        q2 = np.empty((M, K), np.uint8)
+        r = np.empty((M, K), np.float32)
+        s1, s2 = np.empty(M, np.float32), np.empty(M, np.float32)
+        z1, z2 = np.empty(M, np.int32), np.empty(M, np.int32)
+        self.lib.iro_int8_quantize_rows_residual(_p(x, _f32p), M, K, _p(q1, _u8p), _p(s1, _f32p),
+                                                 _p(z1, _i32p), _p(r, _f32p), _p(q2, _u8p),
+                                                 _p(s2, _f32p), _p(z2, _i32p))
+        return (q1, s1, z1), r, (q2, s2, z2)
+
+    def linear(self, q, sx, zx, wq, sw, colsum, bias=None, y=None, accumulate=False):
+        q = np.ascontiguousarray(q, np.uint8)
+        M, K = q.shape
+        N = wq.shape[0]
+        wq = np.ascontiguousarray(wq, np.int8)
+        sw = _f32(sw)
+        colsum = np.ascontiguousarray(colsum, np.int32)
+        wt = _Weight(_p(wq, _i8p), _p(sw, _f32p), _p(colsum, _i32p), N, K)
+        y = np.zeros((M, N), np.float32) if y is None else np.array(y, np.float32, copy=True)
+        work = np.empty((M, N), np.int32)
+        self.lib.iro_int8_linear_ex(_p(q, _u8p), _p(_f32(sx), _f32p),
+                                    _p(np.ascontiguousarray(zx, np.int32), _i32p), C.byref(wt),
+                                    _p(None if bias is None else _f32(bias), _f32p), _p(y, _f32p),
+                                    M, _p(work, _i32p), int(bool(accumulate)))
+        return y, work
+
+    def selfcheck(self):
+        return self.lib.iro_int8_selfcheck()
+
+    def silu_mul(self, a, g):
+        a = np.array(a, np.float32, copy=True)
+        self.lib.iro_silu_mul_inplace(_p(a, _f32p), _p(_f32(g), _f32p), a.size)
+        return a
+
+    def conv1d(self, x, wq, sw, colsum, kernel, stride, dilation, padding, bias=None,
+               residual=False, out_len=None):
+        x = _f32(x)
+        T, Cin = x.shape
+        N = wq.shape[0]
+        y = np.empty((out_len, N), np.float32)
+        rc = self.lib.ref_conv1d_int8(_p(x, _f32p), T, Cin, N, kernel, stride, dilation, padding,
+                                      _p(np.ascontiguousarray(wq, np.int8), _i8p),
+                                      _p(_f32(sw), _f32p),
+                                      _p(np.ascontiguousarray(colsum, np.int32), _i32p),
+                                      _p(None if bias is None else _f32(bias), _f32p),
+                                      int(bool(residual)), _p(y, _f32p))
+        assert rc == 0
+        return y

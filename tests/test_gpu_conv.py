@@ -1,0 +1,57 @@
+"""Parity of the int8 Conv1d (dacvae.c:543-688) on the GPU against the oracle.
+
+Edge cases follow the reference's window logic: output rows whose taps
+fall before 0 or after T-1 (padding holds the zero point and does not widen
+the row range), dilation, stride > 1, all-zero windows (scale 1), channel
+counts that are not a multiple of 4, and the fixed-scale second plane of the
+last decoder stage (dacvae.c:637-663).  The BASELINE shapes run at full size.
+"""
+import numpy as np
+import pytest
+
+from iro_synth import gauss
+from parity_util import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # T, C, N, kernel, stride, dilation, padding
+    (50, 16, 24, 7, 1, 1, 3),
+    (50, 16, 24, 7, 1, 3, 9),
+    (40, 8, 8, 7, 2, 1, 3),
+    (64, 32, 16, 3, 1, 9, 9),
+    (33, 6, 10, 7, 1, 1, 3),
+    (300, 96, 96, 7, 1, 9, 27),
+    (5, 4, 4, 7, 1, 1, 3),
+]
+
+
+def _conv(ctx, oracle, T, C, N, k, st, dil, pad, residual, seed, zero_band=True):
+    conv = ctx.convention
+    x = gauss(seed, (T, C))
+    if zero_band and T > 30:
+        x[10:30] = 0.0  # all-zero windows
+    w = gauss(seed + 1, (N, k * C), 0.02)
+    b = gauss(seed + 2, (N,), 0.01)
+    W = ctx.weight(ctx.to_device(w), N, k * C)
+    To = oracle.conv_out_len(T, k, st, dil, pad)
+    yd = ctx.empty((To, N), np.float32)
+    got_len = ctx.conv1d(ctx.to_device(x), T, C, W, k, st, dil, pad, ctx.to_device(b), residual,
+                         yd)
+    assert got_len == To
+    yo, _, _, _ = oracle.conv1d(conv, x, *oracle.weight_quantize(conv, w), k, st, dil, pad,
+                                bias=b, residual=residual)
+    return yd.numpy(), yo
+
+
+@pytest.mark.parametrize("T,C,N,k,st,dil,pad", CASES)
+@pytest.mark.parametrize("residual", [0, 1], ids=["one-plane", "two-plane"])
+def test_conv_small(ctx, oracle, T, C, N, k, st, dil, pad, residual):
+    got, want = _conv(ctx, oracle, T, C, N, k, st, dil, pad, residual, 70 + T + C)
+    assert_bits_equal(got, want, "conv output")
+
+
+@pytest.mark.parametrize("T,C,N,dil,pad", [(24000, 512, 512, 1, 3), (6000, 1024, 256, 3, 9)],
+                         ids=["cfg4-T24000-C512", "cfg4-T6000-C1024-dil3"])
+def test_conv_baseline_shapes(ctx, oracle, T, C, N, dil, pad):
+    got, want = _conv(ctx, oracle, T, C, N, 7, 1, dil, pad, 0, 90, zero_band=False)
+    assert_bits_equal(got, want, "conv output")
