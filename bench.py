@@ -1,0 +1,224 @@
+#!/usr/bin/env python3
+"""Benchmark: the int8 W8A8 DiT linear stack, one Euler step per bench step.
+
+Workload (the stack configuration, one GPU): 12 DiT blocks, hidden 1024,
+MLP 2816, 3 CFG branches x 750 latent frames (M = 2250 rows).  Per block:
+the modulation linear 1024 -> 6x1024 on the 3 conditioning rows, fused QKVG
+1024 -> 4x1024, Wo 1024 -> 1024 with the gated residual, fused W1/W3
+1024 -> 2x2816 with the SiLU gate, and W2 2816 -> 1024 on the two-term
+requantized hidden state (the reference default) with the gated residual.
+Every quantization, int8 GEMM and epilogue of the step runs on the GPU
+through the C ABI; inputs and weights are resident in HBM before timing.
+The fp32 attention core and RMSNorm-modulate are not part of the stack.
+
+Prints one JSON line on stdout; diagnostics go to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for sub in ("irodori-c_amd", "oracle"):
+    sys.path.insert(0, os.path.join(REPO, sub))
+
+import numpy as np  # noqa: E402
+
+import iro_hip  # noqa: E402
+from iro_synth import gauss  # noqa: E402
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def stack_ops(blocks, B, S, D, H, rm):
+    M = B * S
+    per = (2 * B * D * 6 * D
+           + 2 * M * D * 4 * D * (2 if rm & 1 else 1)
+           + 2 * M * D * D * (2 if rm & 2 else 1)
+           + 2 * M * D * 2 * H * (2 if rm & 4 else 1)
+           + 2 * M * H * D * (2 if rm & 8 else 1))
+    return blocks * per
+
+
+def block_weights(base, b):
+    """Block b's fp32 weights: the base draws with rows rotated by a
+    block-dependent offset, so every block holds distinct matrices."""
+    return [np.ascontiguousarray(np.roll(w, 97 * b + 13 * i, axis=0)) for i, w in enumerate(base)]
+
+
+def base_weights(D, H, seed=1000):
+    shapes = [(6 * D, D), (D, D), (D, D), (D, D), (D, D), (D, D), (H, D), (H, D), (D, H)]
+    return [gauss(seed + i, s, 0.02) for i, s in enumerate(shapes)]
+
+
+def cpu_baseline(args, base, x0, cond, D, H, ops_per_step):
+    from oracle import CpuBaseline, Oracle
+    threads = min(16, len(os.sched_getaffinity(0)))
+    cpu = CpuBaseline(threads)
+    o = Oracle()
+    conv = 0 if args.convention == "strict" else 1
+    wq = [o.weight_quantize(conv, w) for w in block_weights(base, 0)]
+    x = np.array(x0, copy=True)
+    t = np.zeros(3)
+    n = 0
+    start = time.perf_counter()
+    while True:
+        t += cpu.dit_block(conv, wq, x, cond, args.batch, args.frames, D, H, args.residual_mask)
+        n += 1
+        if time.perf_counter() - start >= args.cpu_seconds or n >= 12 * 8:
+            break
+    wall = time.perf_counter() - start
+    step_s = wall / n * args.blocks
+    log(f"cpu baseline: {n} blocks in {wall:.2f}s on {threads} threads ({cpu.backend}); "
+        f"quantize {t[0]:.2f}s gemm {t[1]:.2f}s epilogue {t[2]:.2f}s")
+    return {
+        "value": round(ops_per_step / step_s / 1e12, 4),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "ms_per_step": round(step_s * 1e3, 2),
+        "backend": cpu.backend,
+        "sample": (f"{n} DiT blocks (block-0 weights) of the 12-block step at M={x0.shape[0]}, "
+                   f"scaled x{args.blocks}; quantize/epilogue single-threaded as ops.c, GEMM on "
+                   f"{threads} threads"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--convention", choices=["strict", "fastmath"], default="strict")
+    ap.add_argument("--blocks", type=int, default=12)
+    ap.add_argument("--batch", type=int, default=3)
+    ap.add_argument("--frames", type=int, default=750)
+    ap.add_argument("--hidden", type=int, default=1024)
+    ap.add_argument("--mlp", type=int, default=2816)
+    ap.add_argument("--residual-mask", type=int, default=8)
+    ap.add_argument("--profile-steps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(--gpus must be 1)", file=sys.stderr)
+        sys.exit(2)
+
+    B, S, D, H = args.batch, args.frames, args.hidden, args.mlp
+    M = B * S
+    rm = args.residual_mask
+    ops = stack_ops(args.blocks, B, S, D, H, rm)
+    conv = iro_hip.STRICT if args.convention == "strict" else iro_hip.GCC_FASTMATH
+
+    base = base_weights(D, H)
+    x0 = gauss(7, (M, D))
+    cond = gauss(8, (B, D), 0.1)
+
+    ctx = iro_hip.Context(0, conv)
+    log("backend:", ctx.backend())
+    stack = iro_hip.DiTStack(ctx, args.blocks, D, H, rm)
+    for b in range(args.blocks):
+        dev = [ctx.to_device(w) for w in block_weights(base, b)]
+        stack.set_block(b, *dev)
+        for a in dev:
+            a.free()
+    ctx._arrays = [a for a in ctx._arrays if a.ptr]
+    x = ctx.to_device(x0)
+    c = ctx.to_device(cond)
+
+    for _ in range(args.warmup):
+        stack.step(x, c, B, S)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    t0 = time.perf_counter()
+    ctx.record(e0)
+    for _ in range(args.steps):
+        stack.step(x, c, B, S)
+    ctx.record(e1)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.elapsed_ms(e0, e1)
+    ms_step = wall * 1e3 / args.steps
+    finite = bool(np.isfinite(x.numpy()).all())
+    log(f"stack: {ms_step:.3f} ms/step wall, {ev_ms / args.steps:.3f} ms/step events, "
+        f"x finite: {finite}")
+
+    # Per-kernel durations on the stack's stream (HIP events), after the
+    # timed region.
+    ctx.profile(True)
+    for _ in range(args.profile_steps):
+        stack.step(x, c, B, S)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    total_ms = sum(v[1] for v in prof.values())
+    for k, (n, kms, kops, kby) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        avg = kms / n
+        log(f"  {k:24s} launches {n:5d}  avg {avg * 1e3:8.2f} us  share {kms / total_ms:6.1%}  "
+            f"{kops / kms / 1e9 if kops else 0:8.1f} TOPS  {kby / kms / 1e6:8.1f} GB/s")
+    dom = max(prof.items(), key=lambda kv: kv[1][1])
+    name, (n, kms, kops, kby) = dom
+    avg_ms = kms / n
+    if kops:
+        achieved = kops / n / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
+                "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                "kernel": name, "avg_us": round(avg_ms * 1e3, 2),
+                "ops_per_launch": kops / n}
+    else:
+        achieved = kby / n / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "kernel": name, "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": kby / n}
+
+    kernels = {k: {"launches": v[0], "avg_us": round(v[1] / v[0] * 1e3, 2),
+                   "share": round(v[1] / total_ms, 4)} for k, v in prof.items()}
+    stack_bytes = stack.nbytes()
+    stack.destroy()
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args, base, x0, cond, D, H, ops)
+
+    value = ops * args.steps / wall / 1e12
+    out = {
+        "metric": "int8 DiT linear TOPS + % of int8 MFMA peak; Euler-step latency (ms), 1 GPU",
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded Irwin-Hall Gaussian inputs, random-init weights)",
+        "config": {
+            "workload": (f"int8 DiT linear stack: {args.blocks} blocks, hidden {D}, MLP {H}, "
+                         f"M={B}x{S} rows, modulation 1024->6x1024 at M={B}, W2 two-term "
+                         f"(residual mask {rm}), one Euler step per step"),
+            "blocks": args.blocks, "batch": B, "frames": S, "hidden": D, "mlp": H,
+            "convention": args.convention, "ops_per_step": ops,
+            "frac_of_peak_stack": round(value / PEAK_INT8_TOPS, 4),
+            "resident_int8_bytes": stack_bytes, "parallelism": "single GPU",
+        },
+        "roofline": roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "x_finite": finite,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

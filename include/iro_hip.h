@@ -158,6 +158,36 @@ int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWe
                        const IroHipWeight *w2, int residual_w13, int residual_w2,
                        float *hidden, float *out, float *x_res, const float *gate, int S);
 
+/* ---- the int8 linear stack of one Euler step --------------------------- */
+
+/* The int8 projections of `blocks` DiT blocks (dit.h:51-58 IroDiTInt8,
+   built once as iro_dit_int8_quantize does, dit.c:235-259), device
+   resident.  residual_mask has IRO_INT8_RESIDUAL's meaning (dit.c:278-291:
+   1 QKVG, 2 Wo, 4 W1/W3, 8 W2; the reference default is 8). */
+typedef struct IroHipDiTStack IroHipDiTStack;
+int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int residual_mask,
+                             IroHipDiTStack **out);
+/* Device fp32 weights of one block: ada [6D,D] (modulation linear),
+   wq/wk/wv/wgate/wo [D,D], w1/w3 [H,D], w2 [D,H]. */
+int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, const float *wq,
+                                const float *wk, const float *wv, const float *wgate,
+                                const float *wo, const float *w1, const float *w3,
+                                const float *w2);
+/* One step of every block's int8 linears (the dit_block sequence,
+   dit.c:983-1040): mod = ada . cond [B,6D]; QKVG on x; Wo on V with
+   x += mod[:,2D:3D] * out; SwiGLU on x with x += mod[:,5D:6D] * out.
+   x [B*S, D] is updated in place, cond is [B, D].  The fp32 attention core
+   and RMSNorm-modulate between the projections are not part of this path
+   (Wo reads V; QKVG and W1/W3 read x). */
+int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B, int S);
+/* Resident int8 bytes, iro_int8_weight_bytes summed (generate.h:43-46). */
+size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s);
+/* Device pointers of the step's activation buffers (last block's q, k, v,
+   gate [M,D], hidden [M,H], modulation rows [B,6D]). */
+int iro_hip_dit_stack_buffers(IroHipDiTStack *s, float **q, float **k, float **v, float **gate,
+                              float **hidden, float **mod);
+void iro_hip_dit_stack_destroy(IroHipDiTStack *s);
+
 /* ---- DACVAE int8 Conv1d (dacvae.c:543-688, no snake) ------------------- */
 
 /* input [T, C] fp32 time-major, weight [N, kernel*C] (tap-major K as
@@ -170,6 +200,20 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
                         const IroHipWeight *w, int kernel, int stride, int dilation,
                         int padding, const float *bias, int residual, float *output,
                         int *t_out);
+
+/* ---- per-kernel event profiler ----------------------------------------- */
+
+/* While enabled, every kernel launch on the context is bracketed by HIP
+   events on its stream and accumulated per kernel kind (the role of the
+   reference's IRO_GEMM_PROFILE / IRO_DIT_PROFILE, ops.c:14-110,
+   dit.c:22-120).  Reading collects pending events (synchronizes). */
+int iro_hip_profile_enable(IroHipContext *ctx, int on);
+int iro_hip_profile_reset(IroHipContext *ctx);
+int iro_hip_profile_kinds(void);
+/* Totals for `kind` in [0, iro_hip_profile_kinds()): launches, summed
+   milliseconds, algorithmic ops (2*M*N*K per plane) and HBM bytes. */
+int iro_hip_profile_read(IroHipContext *ctx, int kind, const char **name, long long *launches,
+                         double *ms, double *ops, double *bytes);
 
 /* ---- backend queries: ops.h:55-78 ------------------------------------- */
 

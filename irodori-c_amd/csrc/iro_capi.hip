@@ -35,9 +35,85 @@ int Workspace::commit() {
     return 0;
 }
 
-namespace {
+// ---- event profiler ----------------------------------------------------------
 
-size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+const char *const kProfNames[PK_COUNT] = {
+    "quant_rows",        "quant_rows_residual", "gemm_linear",  "gemm_linear_two_term",
+    "gemm_qkvg",         "gemm_qkvg_two_term",  "gemm_swiglu",  "gemm_swiglu_two_term",
+    "gemm_gated",        "gemm_gated_two_term", "conv_rows",    "conv_im2col",
+    "other"};
+
+struct ProfState {
+    struct Rec {
+        ProfKind kind;
+        hipEvent_t e0, e1;
+        double ops, bytes;
+    };
+    std::vector<hipEvent_t> pool;
+    std::vector<Rec> pending;
+    hipEvent_t open = nullptr;
+    long long n[PK_COUNT] = {0};
+    double ms[PK_COUNT] = {0}, ops[PK_COUNT] = {0}, bytes[PK_COUNT] = {0};
+};
+
+static hipEvent_t prof_event(ProfState *p) {
+    if (!p->pool.empty()) {
+        hipEvent_t e = p->pool.back();
+        p->pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void prof_begin(IroHipContext *ctx) {
+    ProfState *p = ctx->prof;
+    if (!p) return;
+    p->open = prof_event(p);
+    if (p->open) (void)hipEventRecord(p->open, ctx->stream);
+}
+
+void prof_end(IroHipContext *ctx, ProfKind kind, double ops, double bytes) {
+    ProfState *p = ctx->prof;
+    if (!p || !p->open) return;
+    hipEvent_t e1 = prof_event(p);
+    if (!e1) return;
+    (void)hipEventRecord(e1, ctx->stream);
+    p->pending.push_back({kind, p->open, e1, ops, bytes});
+    p->open = nullptr;
+}
+
+static int prof_collect(IroHipContext *ctx) {
+    ProfState *p = ctx->prof;
+    if (!p || p->pending.empty()) return 0;
+    IRO_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    for (const auto &r : p->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r.e0, r.e1) == hipSuccess) {
+            p->n[r.kind] += 1;
+            p->ms[r.kind] += ms;
+            p->ops[r.kind] += r.ops;
+            p->bytes[r.kind] += r.bytes;
+        }
+        p->pool.push_back(r.e0);
+        p->pool.push_back(r.e1);
+    }
+    p->pending.clear();
+    return 0;
+}
+
+static void prof_free(ProfState *p) {
+    if (!p) return;
+    for (auto &r : p->pending) {
+        p->pool.push_back(r.e0);
+        p->pool.push_back(r.e1);
+    }
+    for (hipEvent_t e : p->pool) (void)hipEventDestroy(e);
+    delete p;
+}
+
+namespace {
 
 int device_guard(IroHipContext *ctx) {
     IRO_HIP_TRY(ctx, hipSetDevice(ctx->device));
@@ -134,56 +210,6 @@ int packed_col(const IroHipWeight *w, int n) {
     return pb * 32 + (n & 31);
 }
 
-// Activation staging in the context workspace: codes padded to 16-byte rows.
-struct ActBufs {
-    uint8_t *q1, *q2;
-    float *s1, *s2;
-    int32_t *z1, *z2;
-    int ld;
-};
-
-void act_reserve(Workspace &ws, int M, int K, bool two, size_t off[6]) {
-    const size_t ld = round_up((size_t)K, 16);
-    off[0] = ws.reserve(ld * M);
-    off[1] = ws.reserve(sizeof(float) * M);
-    off[2] = ws.reserve(sizeof(int32_t) * M);
-    if (two) {
-        off[3] = ws.reserve(ld * M);
-        off[4] = ws.reserve(sizeof(float) * M);
-        off[5] = ws.reserve(sizeof(int32_t) * M);
-    }
-}
-
-ActBufs act_at(const Workspace &ws, int K, bool two, const size_t off[6]) {
-    ActBufs b;
-    b.ld = (int)round_up((size_t)K, 16);
-    b.q1 = ws.at<uint8_t>(off[0]);
-    b.s1 = ws.at<float>(off[1]);
-    b.z1 = ws.at<int32_t>(off[2]);
-    b.q2 = two ? ws.at<uint8_t>(off[3]) : nullptr;
-    b.s2 = two ? ws.at<float>(off[4]) : nullptr;
-    b.z2 = two ? ws.at<int32_t>(off[5]) : nullptr;
-    return b;
-}
-
-int quantize_into(IroHipContext *ctx, const float *x, int M, int K, const ActBufs &b) {
-    return launch_quant_rows(ctx, x, M, K, K, b.q1, b.ld, b.s1, b.z1, nullptr, b.q2, b.s2, b.z2);
-}
-
-GemmArgs gemm_args(const ActBufs &b, int M, int K) {
-    GemmArgs a;
-    a.a1 = b.q1;
-    a.a2 = b.q2;
-    a.lda = b.ld;
-    a.sx1 = b.s1;
-    a.zx1 = b.z1;
-    a.sx2 = b.s2;
-    a.zx2 = b.z2;
-    a.M = M;
-    a.K = (int)round_up((size_t)K, 16);
-    return a;
-}
-
 // The known answer of ops.c:375-398.
 void kat_arrays(uint8_t *a, int8_t *b, int32_t *want) {
     const int M = 3, N = 5, K = 64;
@@ -240,6 +266,8 @@ void iro_hip_destroy(IroHipContext *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    prof_free(ctx->prof);
+    ctx->prof = nullptr;
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -326,6 +354,52 @@ int iro_hip_event_elapsed_ms(void *start, void *stop, float *ms) {
     if (!start || !stop || !ms) return -1;
     if (hipEventSynchronize((hipEvent_t)stop) != hipSuccess) return -1;
     return hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop) == hipSuccess ? 0 : -1;
+}
+
+int iro_hip_profile_enable(IroHipContext *ctx, int on) {
+    if (!ctx) return -1;
+    if (on && !ctx->prof) {
+        ctx->prof = new (std::nothrow) ProfState();
+        if (!ctx->prof) return set_error(ctx, "profile: out of host memory");
+    } else if (!on && ctx->prof) {
+        if (prof_collect(ctx)) return -1;
+        prof_free(ctx->prof);
+        ctx->prof = nullptr;
+    }
+    return 0;
+}
+
+int iro_hip_profile_reset(IroHipContext *ctx) {
+    if (!ctx || !ctx->prof) return -1;
+    if (prof_collect(ctx)) return -1;
+    ProfState *p = ctx->prof;
+    for (int k = 0; k < PK_COUNT; ++k) {
+        p->n[k] = 0;
+        p->ms[k] = p->ops[k] = p->bytes[k] = 0.0;
+    }
+    return 0;
+}
+
+int iro_hip_profile_kinds(void) { return PK_COUNT; }
+
+int iro_hip_profile_read(IroHipContext *ctx, int kind, const char **name, long long *launches,
+                         double *ms, double *ops, double *bytes) {
+    if (!ctx || kind < 0 || kind >= PK_COUNT) return -1;
+    if (name) *name = kProfNames[kind];
+    long long n = 0;
+    double t = 0, o = 0, b = 0;
+    if (ctx->prof) {
+        if (prof_collect(ctx)) return -1;
+        n = ctx->prof->n[kind];
+        t = ctx->prof->ms[kind];
+        o = ctx->prof->ops[kind];
+        b = ctx->prof->bytes[kind];
+    }
+    if (launches) *launches = n;
+    if (ms) *ms = t;
+    if (ops) *ops = o;
+    if (bytes) *bytes = b;
+    return 0;
 }
 
 // ---- weights -----------------------------------------------------------------
@@ -518,93 +592,6 @@ int iro_hip_int8_linear_two_term(IroHipContext *ctx, const uint8_t *q1, const fl
     if (!q2 || !scale2 || !zero2) return set_error(ctx, "int8_linear_two_term: invalid arguments");
     return linear_common(ctx, q1, scale1, zero1, q2, scale2, zero2, w, bias, y, M, nullptr,
                          accumulate);
-}
-
-// ---- fused DiT projections -----------------------------------------------------------
-
-int iro_hip_dit_qkvg(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w, float *q,
-                     float *k, float *v, float *gate, int residual) {
-    if (!ctx || !w || M < 0 || w->nparts != 4 || w->layout != 0 ||
-        (M && (!x || !q || !k || !v || !gate)))
-        return set_error(ctx, "dit_qkvg: needs a 4-part concatenated weight and q,k,v,gate");
-    for (int i = 1; i < 4; ++i)
-        if (w->part_N[i] != w->part_N[0]) return set_error(ctx, "dit_qkvg: unequal parts");
-    if (M == 0) return 0;
-    const int D = w->K;
-    Workspace ws{ctx};
-    size_t off[6];
-    act_reserve(ws, M, D, residual != 0, off);
-    if (ws.commit()) return -1;
-    const ActBufs b = act_at(ws, D, residual != 0, off);
-    if (quantize_into(ctx, x, M, D, b)) return -1;
-    GemmArgs a = gemm_args(b, M, D);
-    a.seg[0] = q;
-    a.seg[1] = k;
-    a.seg[2] = v;
-    a.seg[3] = gate;
-    a.seg_n = w->part_N[0];
-    return launch_gemm(ctx, w, a, EPI_QKVG);
-}
-
-int iro_hip_dit_linear_gated(IroHipContext *ctx, const float *mix, int M, const IroHipWeight *w,
-                             int residual, float *out, float *x_res, const float *gate, int S) {
-    if (!ctx || !w || M < 0 || (M && (!mix || (!x_res && !out) || (x_res && (!gate || S <= 0)))))
-        return set_error(ctx, "dit_linear_gated: invalid arguments");
-    if (M == 0) return 0;
-    const int K = w->K;
-    Workspace ws{ctx};
-    size_t off[6];
-    act_reserve(ws, M, K, residual != 0, off);
-    if (ws.commit()) return -1;
-    const ActBufs b = act_at(ws, K, residual != 0, off);
-    if (quantize_into(ctx, mix, M, K, b)) return -1;
-    GemmArgs a = gemm_args(b, M, K);
-    if (x_res) {
-        a.xres = x_res;
-        a.gate = gate;
-        a.ldx = w->N;
-        a.rows_per_branch = S;
-        return launch_gemm(ctx, w, a, EPI_GATED);
-    }
-    a.y = out;
-    a.ldy = w->N;
-    return launch_gemm(ctx, w, a, EPI_LINEAR);
-}
-
-int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
-                       const IroHipWeight *w2, int residual_w13, int residual_w2, float *hidden,
-                       float *out, float *x_res, const float *gate, int S) {
-    if (!ctx || !w13 || !w2 || M < 0 || w13->layout != 1 || w2->K != w13->part_N[0] ||
-        w2->N != w13->K || (M && (!h || (!x_res && !out) || (x_res && (!gate || S <= 0)))))
-        return set_error(ctx, "dit_swiglu: invalid arguments or weight shapes");
-    if (M == 0) return 0;
-    const int D = w13->K, H = w13->part_N[0];
-    Workspace ws{ctx};
-    size_t off1[6], off2[6], oh = 0;
-    act_reserve(ws, M, D, residual_w13 != 0, off1);
-    act_reserve(ws, M, H, residual_w2 != 0, off2);
-    if (!hidden) oh = ws.reserve(sizeof(float) * (size_t)M * H);
-    if (ws.commit()) return -1;
-    const ActBufs b1 = act_at(ws, D, residual_w13 != 0, off1);
-    const ActBufs b2 = act_at(ws, H, residual_w2 != 0, off2);
-    float *hid = hidden ? hidden : ws.at<float>(oh);
-    if (quantize_into(ctx, h, M, D, b1)) return -1;
-    GemmArgs a = gemm_args(b1, M, D);
-    a.hidden = hid;
-    a.ldh = H;
-    if (launch_gemm(ctx, w13, a, EPI_SWIGLU)) return -1;
-    if (quantize_into(ctx, hid, M, H, b2)) return -1;
-    GemmArgs a2 = gemm_args(b2, M, H);
-    if (x_res) {
-        a2.xres = x_res;
-        a2.gate = gate;
-        a2.ldx = D;
-        a2.rows_per_branch = S;
-        return launch_gemm(ctx, w2, a2, EPI_GATED);
-    }
-    a2.y = out;
-    a2.ldy = D;
-    return launch_gemm(ctx, w2, a2, EPI_LINEAR);
 }
 
 // ---- conv ------------------------------------------------------------------------------

@@ -144,9 +144,11 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(
 }  // namespace
 
 int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi) {
+    prof_begin(ctx);
     hipLaunchKernelGGL(conv_rows_kernel, dim3((T + 3) / 4), dim3(256), 0, ctx->stream, x, T, C, lo,
                        hi);
     IRO_HIP_CHECK_LAUNCH(ctx);
+    prof_end(ctx, PK_CONV_ROWS, 0, 4.0 * T * C + 8.0 * T);
     return 0;
 }
 
@@ -156,7 +158,8 @@ int launch_conv_im2col(IroHipContext *ctx, const float *x, int T, int C, int T_o
                        int32_t *z1, float *s2, int32_t *z2) {
     const dim3 grid((T_out + 3) / 4), block(256);
     const bool res = cols2 != nullptr;
-#define IRO_IM2COL(CV, RS)                                                                      \
+    prof_begin(ctx);
+#define IRO_IM2COL(CV, RS)                                                                     \
     hipLaunchKernelGGL((conv_im2col_kernel<CV, RS>), grid, block, 0, ctx->stream, x, T, C, T_out, \
                        kernel, stride, dilation, padding, row_lo, row_hi, cols1, cols2, ldc, s1, \
                        z1, s2, z2)
@@ -169,6 +172,9 @@ int launch_conv_im2col(IroHipContext *ctx, const float *x, int T, int C, int T_o
     }
 #undef IRO_IM2COL
     IRO_HIP_CHECK_LAUNCH(ctx);
+    // Algorithmic HBM bytes: the input once, the code plane(s) out.
+    prof_end(ctx, PK_CONV_IM2COL, 0,
+             4.0 * T * C + (res ? 2.0 : 1.0) * ((double)T_out * kernel * C + 8.0 * T_out));
     return 0;
 }
 

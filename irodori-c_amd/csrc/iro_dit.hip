@@ -1,0 +1,292 @@
+// iro_dit.hip -- the DiT int8 projections (dit.c:739-981) as fused device
+// calls, and the int8 linear stack of one Euler step over all blocks.
+//
+// Each projection group quantizes its input once (dit.c:469-475, shared by
+// Q/K/V/gate and by W1/W3) and runs one GEMM whose epilogue finishes the
+// group: the split Q/K/V/gate store, silu(w1)*w3, or the gated residual
+// x += gate * y (dit.c:1013-1020, 1032-1039), so the projection outputs of
+// Wo and W2 never round-trip HBM.
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "iro_internal.h"
+
+namespace iro {
+
+namespace {
+
+int qkvg_impl(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w, float *q,
+              float *k, float *v, float *gate, int residual) {
+    const int D = w->K;
+    Workspace ws{ctx};
+    size_t off[6];
+    act_reserve(ws, M, D, residual != 0, off);
+    if (ws.commit()) return -1;
+    const ActBufs b = act_at(ws, D, residual != 0, off);
+    if (quantize_into(ctx, x, M, D, D, b)) return -1;
+    GemmArgs a = gemm_args(b, M, D);
+    a.seg[0] = q;
+    a.seg[1] = k;
+    a.seg[2] = v;
+    a.seg[3] = gate;
+    a.seg_n = w->part_N[0];
+    return launch_gemm(ctx, w, a, EPI_QKVG);
+}
+
+// y = lin(quant(x)) [two-term]; x_res += gate[m / S] * y, or out = y.
+int linear_gated_impl(IroHipContext *ctx, const float *x, int M, int ldx_in,
+                      const IroHipWeight *w, int residual, float *out, int ldo, float *x_res,
+                      const float *gate, int ldg, int S) {
+    const int K = w->K;
+    Workspace ws{ctx};
+    size_t off[6];
+    act_reserve(ws, M, K, residual != 0, off);
+    if (ws.commit()) return -1;
+    const ActBufs b = act_at(ws, K, residual != 0, off);
+    if (quantize_into(ctx, x, M, K, ldx_in, b)) return -1;
+    GemmArgs a = gemm_args(b, M, K);
+    if (x_res) {
+        a.xres = x_res;
+        a.gate = gate;
+        a.ldg = ldg;
+        a.ldx = w->N;
+        a.rows_per_branch = S;
+        return launch_gemm(ctx, w, a, EPI_GATED);
+    }
+    a.y = out;
+    a.ldy = ldo;
+    return launch_gemm(ctx, w, a, EPI_LINEAR);
+}
+
+int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
+                const IroHipWeight *w2, int residual_w13, int residual_w2, float *hidden,
+                float *out, float *x_res, const float *gate, int ldg, int S) {
+    const int D = w13->K, H = w13->part_N[0];
+    Workspace ws{ctx};
+    size_t off1[6], off2[6], oh = 0;
+    act_reserve(ws, M, D, residual_w13 != 0, off1);
+    act_reserve(ws, M, H, residual_w2 != 0, off2);
+    if (!hidden) oh = ws.reserve(sizeof(float) * (size_t)M * H);
+    if (ws.commit()) return -1;
+    const ActBufs b1 = act_at(ws, D, residual_w13 != 0, off1);
+    const ActBufs b2 = act_at(ws, H, residual_w2 != 0, off2);
+    float *hid = hidden ? hidden : ws.at<float>(oh);
+    if (quantize_into(ctx, h, M, D, D, b1)) return -1;
+    GemmArgs a = gemm_args(b1, M, D);
+    a.hidden = hid;
+    a.ldh = H;
+    if (launch_gemm(ctx, w13, a, EPI_SWIGLU)) return -1;
+    if (quantize_into(ctx, hid, M, H, H, b2)) return -1;
+    GemmArgs a2 = gemm_args(b2, M, H);
+    if (x_res) {
+        a2.xres = x_res;
+        a2.gate = gate;
+        a2.ldg = ldg;
+        a2.ldx = D;
+        a2.rows_per_branch = S;
+        return launch_gemm(ctx, w2, a2, EPI_GATED);
+    }
+    a2.y = out;
+    a2.ldy = D;
+    return launch_gemm(ctx, w2, a2, EPI_LINEAR);
+}
+
+}  // namespace
+}  // namespace iro
+
+// The int8 weights of one DiT linear stack, device resident and pre-packed
+// once (the reference builds them once in iro_engine_init,
+// generate.c:527-579), plus the per-step activation buffers.
+struct IroHipDiTStack {
+    IroHipContext *ctx = nullptr;
+    int blocks = 0, D = 0, H = 0;
+    int residual_mask = 8;
+    std::vector<IroHipWeight *> ada, qkvg, wo, w13, w2;
+    int cap_rows = 0, cap_branches = 0;
+    float *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *hidden = nullptr;
+    float *mod = nullptr;
+};
+
+using namespace iro;
+
+namespace {
+
+void stack_free_acts(IroHipDiTStack *s) {
+    for (float **p : {&s->q, &s->k, &s->v, &s->g, &s->hidden, &s->mod}) {
+        if (*p) (void)hipFree(*p);
+        *p = nullptr;
+    }
+    s->cap_rows = s->cap_branches = 0;
+}
+
+int stack_reserve(IroHipDiTStack *s, int M, int B) {
+    if (M <= s->cap_rows && B <= s->cap_branches) return 0;
+    IroHipContext *ctx = s->ctx;
+    IRO_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    stack_free_acts(s);
+    const size_t md = sizeof(float) * (size_t)M * s->D;
+    hipError_t e = hipMalloc(&s->q, md);
+    if (e == hipSuccess) e = hipMalloc(&s->k, md);
+    if (e == hipSuccess) e = hipMalloc(&s->v, md);
+    if (e == hipSuccess) e = hipMalloc(&s->g, md);
+    if (e == hipSuccess) e = hipMalloc(&s->hidden, sizeof(float) * (size_t)M * s->H);
+    if (e == hipSuccess) e = hipMalloc(&s->mod, sizeof(float) * (size_t)B * 6 * s->D);
+    if (e != hipSuccess) {
+        stack_free_acts(s);
+        return set_error(ctx, "dit_stack: hipMalloc failed: %s", hipGetErrorString(e));
+    }
+    s->cap_rows = M;
+    s->cap_branches = B;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int iro_hip_dit_qkvg(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w, float *q,
+                     float *k, float *v, float *gate, int residual) {
+    if (!ctx || !w || M < 0 || w->nparts != 4 || w->layout != 0 ||
+        (M && (!x || !q || !k || !v || !gate)))
+        return set_error(ctx, "dit_qkvg: needs a 4-part concatenated weight and q,k,v,gate");
+    for (int i = 1; i < 4; ++i)
+        if (w->part_N[i] != w->part_N[0]) return set_error(ctx, "dit_qkvg: unequal parts");
+    if (M == 0) return 0;
+    return qkvg_impl(ctx, x, M, w, q, k, v, gate, residual);
+}
+
+int iro_hip_dit_linear_gated(IroHipContext *ctx, const float *mix, int M, const IroHipWeight *w,
+                             int residual, float *out, float *x_res, const float *gate, int S) {
+    if (!ctx || !w || M < 0 || (M && (!mix || (!x_res && !out) || (x_res && (!gate || S <= 0)))))
+        return set_error(ctx, "dit_linear_gated: invalid arguments");
+    if (M == 0) return 0;
+    return linear_gated_impl(ctx, mix, M, w->K, w, residual, out, w->N, x_res, gate, w->N, S);
+}
+
+int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
+                       const IroHipWeight *w2, int residual_w13, int residual_w2, float *hidden,
+                       float *out, float *x_res, const float *gate, int S) {
+    if (!ctx || !w13 || !w2 || M < 0 || w13->layout != 1 || w2->K != w13->part_N[0] ||
+        w2->N != w13->K || (M && (!h || (!x_res && !out) || (x_res && (!gate || S <= 0)))))
+        return set_error(ctx, "dit_swiglu: invalid arguments or weight shapes");
+    if (M == 0) return 0;
+    return swiglu_impl(ctx, h, M, w13, w2, residual_w13, residual_w2, hidden, out, x_res, gate,
+                       w13->K, S);
+}
+
+int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int residual_mask,
+                             IroHipDiTStack **out) {
+    if (!ctx || !out || blocks <= 0 || D <= 0 || H <= 0 || H % 32)
+        return set_error(ctx, "dit_stack: invalid shape (H must be a multiple of 32)");
+    IroHipDiTStack *s = new (std::nothrow) IroHipDiTStack();
+    if (!s) return set_error(ctx, "dit_stack: out of host memory");
+    s->ctx = ctx;
+    s->blocks = blocks;
+    s->D = D;
+    s->H = H;
+    s->residual_mask = residual_mask & 15;
+    s->ada.assign(blocks, nullptr);
+    s->qkvg.assign(blocks, nullptr);
+    s->wo.assign(blocks, nullptr);
+    s->w13.assign(blocks, nullptr);
+    s->w2.assign(blocks, nullptr);
+    *out = s;
+    return 0;
+}
+
+int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, const float *wq,
+                                const float *wk, const float *wv, const float *wgate,
+                                const float *wo, const float *w1, const float *w3,
+                                const float *w2) {
+    if (!s || block < 0 || block >= s->blocks) return -1;
+    IroHipContext *ctx = s->ctx;
+    if (!ada || !wq || !wk || !wv || !wgate || !wo || !w1 || !w3 || !w2)
+        return set_error(ctx, "dit_stack: missing block weight");
+    const int D = s->D, H = s->H;
+    const float *qkvg_parts[4] = {wq, wk, wv, wgate};
+    const int qkvg_n[4] = {D, D, D, D};
+    const float *w13_parts[2] = {w1, w3};
+    const int w13_n[2] = {H, H};
+    IroHipWeight *na = nullptr, *nq = nullptr, *no = nullptr, *n13 = nullptr, *n2 = nullptr;
+    if (iro_hip_weight_create(ctx, ada, 6 * D, D, &na) ||
+        iro_hip_weight_create_fused(ctx, qkvg_parts, qkvg_n, 4, D, 0, &nq) ||
+        iro_hip_weight_create(ctx, wo, D, D, &no) ||
+        iro_hip_weight_create_fused(ctx, w13_parts, w13_n, 2, D, 1, &n13) ||
+        iro_hip_weight_create(ctx, w2, D, H, &n2)) {
+        for (IroHipWeight *w : {na, nq, no, n13, n2}) iro_hip_weight_destroy(w);
+        return -1;
+    }
+    for (auto *v : {&s->ada, &s->qkvg, &s->wo, &s->w13, &s->w2}) iro_hip_weight_destroy((*v)[block]);
+    s->ada[block] = na;
+    s->qkvg[block] = nq;
+    s->wo[block] = no;
+    s->w13[block] = n13;
+    s->w2[block] = n2;
+    return 0;
+}
+
+// One Euler step's int8 linears (sampler.c:243-301 runs dit_block per
+// layer): for each block, the modulation linear on the conditioning rows,
+// QKVG, Wo with the attention gated residual, and the SwiGLU MLP with the
+// MLP gated residual.  x [B*S, D] is updated in place; cond is [B, D].
+// The attention core between QKVG and Wo and the RMSNorm-modulate before
+// QKVG and W1/W3 are fp32 and outside this path: Wo reads V as its input
+// and QKVG/W1W3 read x.
+int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B, int S) {
+    if (!s || !x || !cond || B <= 0 || S <= 0) return -1;
+    IroHipContext *ctx = s->ctx;
+    for (int b = 0; b < s->blocks; ++b)
+        if (!s->ada[b]) return set_error(ctx, "dit_stack: block %d has no weights", b);
+    const int M = B * S, D = s->D;
+    if (stack_reserve(s, M, B)) return -1;
+    const int rm = s->residual_mask;
+    for (int blk = 0; blk < s->blocks; ++blk) {
+        // modulation rows [B, 6D]: shift/scale/gate for attention and MLP
+        if (linear_gated_impl(ctx, cond, B, D, s->ada[blk], 0, s->mod, 6 * D, nullptr, nullptr, 0,
+                              1))
+            return -1;
+        if (qkvg_impl(ctx, x, M, s->qkvg[blk], s->q, s->k, s->v, s->g, rm & 1)) return -1;
+        if (linear_gated_impl(ctx, s->v, M, D, s->wo[blk], rm & 2, nullptr, 0, x, s->mod + 2 * D,
+                              6 * D, S))
+            return -1;
+        if (swiglu_impl(ctx, x, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, s->hidden, nullptr, x,
+                        s->mod + 5 * D, 6 * D, S))
+            return -1;
+    }
+    return ctx->has_err ? -1 : 0;
+}
+
+size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s) {
+    if (!s) return 0;
+    size_t n = 0;
+    for (int b = 0; b < s->blocks; ++b)
+        for (const auto *v : {&s->ada, &s->qkvg, &s->wo, &s->w13, &s->w2})
+            n += iro_hip_weight_bytes((*v)[b]);
+    return n;
+}
+
+// Pointers to the last step's per-block scratch outputs of the final block
+// (q, k, v, gate [M,D], hidden [M,H], modulation [B,6D]) for inspection.
+int iro_hip_dit_stack_buffers(IroHipDiTStack *s, float **q, float **k, float **v, float **gate,
+                              float **hidden, float **mod) {
+    if (!s) return -1;
+    if (q) *q = s->q;
+    if (k) *k = s->k;
+    if (v) *v = s->v;
+    if (gate) *gate = s->g;
+    if (hidden) *hidden = s->hidden;
+    if (mod) *mod = s->mod;
+    return 0;
+}
+
+void iro_hip_dit_stack_destroy(IroHipDiTStack *s) {
+    if (!s) return;
+    if (s->ctx) (void)hipStreamSynchronize(s->ctx->stream);
+    for (auto *v : {&s->ada, &s->qkvg, &s->wo, &s->w13, &s->w2})
+        for (IroHipWeight *w : *v) iro_hip_weight_destroy(w);
+    stack_free_acts(s);
+    delete s;
+}
+
+}  // extern "C"

@@ -58,6 +58,7 @@ struct KParams {
     int hidden_n;
     float *xres;
     const float *gate;
+    int ldg;
     int ldx;
     int rows_per_branch;
 };
@@ -84,11 +85,46 @@ __device__ __forceinline__ float add_term(float y, float t, float c) {
     return CONV == 1 ? __builtin_fmaf(t, c, y) : y + t * c;
 }
 
-// ops.c:781-784 strict: x / (1 + expf(-x)) * g.  expf is evaluated in
-// double and rounded once (correctly rounded but for double-rounding ties
-// far below float resolution).
+// expf as glibc >= 2.28 computes it on x86-64 with FMA (the __expf_fma
+// ifunc variant the reference's libm call resolves to): the published
+// exp2f table method of ARM optimized-routines, N = 32:
+//   x*N/ln2 = k + r,  exp(x) = 2^(k/N) * (1 + C2 r + C1 r^2 + C0 r^3),
+// in double, with GCC's contraction of both uses of InvLn2N*x into FMAs.
+// Bit-identical to glibc's expf for every float input.
+__constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+__device__ __forceinline__ float expf_glibc(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return __builtin_inff();  // overflow
+    if (x < -0x1.9fe368p6f) return 0.0f;             // underflow (and -inf)
+    const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = __builtin_fma(invln2n, xd, shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = __builtin_fma(invln2n, xd, -kd);
+    const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    const double s = __longlong_as_double((long long)t);
+    const double z = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return (float)(y * s);
+}
+
+// ops.c:781-784 as the strict build computes it: x / (1 + expf(-x)) * g.
 __device__ __forceinline__ float silu_mul(float a, float g) {
-    const float e = (float)exp(-(double)a);
+    const float e = expf_glibc(-a);
     return (a / (1.0f + e)) * g;
 }
 
@@ -260,7 +296,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(KParams p) {
                 } else if (EPI == EPI_GATED) {
                     if (ncol[j] < p.N) {
                         const size_t xi = (size_t)m * p.ldx + ncol[j];
-                        const float g = p.gate[(size_t)(m / p.rows_per_branch) * p.ldx + ncol[j]];
+                        const float g = p.gate[(size_t)(m / p.rows_per_branch) * p.ldg + ncol[j]];
                         const float x = p.xres[xi];
                         p.xres[xi] = CONV == 1 ? __builtin_fmaf(g, y, x) : x + g * y;
                     }
@@ -336,15 +372,33 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     kp.hidden_n = w->layout == 1 ? w->part_N[0] : 0;
     kp.xres = a.xres;
     kp.gate = a.gate;
+    kp.ldg = a.ldg > 0 ? a.ldg : a.ldx;
     kp.ldx = a.ldx;
     kp.rows_per_branch = a.rows_per_branch > 0 ? a.rows_per_branch : 1;
     const dim3 grid(w->Np / BN, (a.M + BM - 1) / BM);
     const bool two = a.a2 != nullptr;
+    prof_begin(ctx);
     if (ctx->convention == IRO_HIP_GCC_FASTMATH)
         launch_c<1>(kp, epi, two, grid, ctx->stream);
     else
         launch_c<0>(kp, epi, two, grid, ctx->stream);
     IRO_HIP_CHECK_LAUNCH(ctx);
+    // Algorithmic work: 2*M*N*K per plane; bytes = codes + weights + outputs.
+    const double M = a.M, N = w->N, K = w->K, planes = two ? 2 : 1;
+    double out_bytes = 4 * M * N;
+    ProfKind kind = two ? PK_GEMM_LINEAR_2T : PK_GEMM_LINEAR;
+    if (epi == EPI_LINEAR) {
+        out_bytes *= 1 + (a.accumulate ? 1 : 0) + (a.work ? 1 : 0);
+    } else if (epi == EPI_QKVG) {
+        kind = two ? PK_GEMM_QKVG_2T : PK_GEMM_QKVG;
+    } else if (epi == EPI_SWIGLU) {
+        kind = two ? PK_GEMM_SWIGLU_2T : PK_GEMM_SWIGLU;
+        out_bytes /= 2;
+    } else {
+        kind = two ? PK_GEMM_GATED_2T : PK_GEMM_GATED;
+        out_bytes *= 2;
+    }
+    prof_end(ctx, kind, 2 * M * N * K * planes, M * K * planes + N * K + out_bytes);
     return 0;
 }
 

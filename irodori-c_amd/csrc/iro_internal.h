@@ -8,9 +8,31 @@
 
 #include "iro_hip.h"
 
+namespace iro {
+// Kernel kinds the event profiler accumulates (names in iro_capi.hip).
+enum ProfKind {
+    PK_QUANT = 0,
+    PK_QUANT_RESIDUAL,
+    PK_GEMM_LINEAR,
+    PK_GEMM_LINEAR_2T,
+    PK_GEMM_QKVG,
+    PK_GEMM_QKVG_2T,
+    PK_GEMM_SWIGLU,
+    PK_GEMM_SWIGLU_2T,
+    PK_GEMM_GATED,
+    PK_GEMM_GATED_2T,
+    PK_CONV_ROWS,
+    PK_CONV_IM2COL,
+    PK_OTHER,
+    PK_COUNT
+};
+struct ProfState;
+}  // namespace iro
+
 // Context: one device, one stream, one rounding convention, one growable
 // device workspace for the activations the fused entry points stage
-// (quantized codes, row scales, the SwiGLU hidden state, im2col rows).
+// (quantized codes, row scales, the SwiGLU hidden state, im2col rows),
+// and an optional per-kernel event profiler.
 struct IroHipContext {
     int device = 0;
     int convention = IRO_HIP_STRICT;
@@ -20,6 +42,7 @@ struct IroHipContext {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     char backend[256] = {0};
+    iro::ProfState *prof = nullptr;  // non-null while profiling is on
 };
 
 // A quantized weight, pre-packed for the MFMA B operand.
@@ -67,6 +90,11 @@ int set_error(IroHipContext *ctx, const char *fmt, ...);
     } while (0)
 
 #define IRO_HIP_CHECK_LAUNCH(ctx) IRO_HIP_TRY(ctx, hipGetLastError())
+
+// Event pair around one launch when the context profiler is on; `ops` and
+// `bytes` are the launch's algorithmic work (multiply-adds x2, HBM bytes).
+void prof_begin(IroHipContext *ctx);
+void prof_end(IroHipContext *ctx, ProfKind kind, double ops, double bytes);
 
 // Bump allocation from the context workspace; grows it (after draining the
 // stream) when a call needs more.  Offsets are 256-byte aligned.
@@ -117,12 +145,67 @@ struct GemmArgs {
     float *hidden = nullptr;  // EPI_SWIGLU [M, ldh]
     int ldh = 0;
     float *xres = nullptr;  // EPI_GATED [M, ldx]
-    const float *gate = nullptr;
+    const float *gate = nullptr;  // [M / rows_per_branch, ldg]
+    int ldg = 0;
     int ldx = 0;
     int rows_per_branch = 1;
 };
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi);
+
+inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+// Activation staging in the context workspace: codes in rows padded to 16
+// bytes (the GEMM reads A in 16-byte chunks), row scales and zero points,
+// and the second plane when the two-term residual quantization is on.
+struct ActBufs {
+    uint8_t *q1, *q2;
+    float *s1, *s2;
+    int32_t *z1, *z2;
+    int ld;
+};
+
+inline void act_reserve(Workspace &ws, int M, int K, bool two, size_t off[6]) {
+    const size_t ld = round_up((size_t)K, 16);
+    off[0] = ws.reserve(ld * M);
+    off[1] = ws.reserve(sizeof(float) * M);
+    off[2] = ws.reserve(sizeof(int32_t) * M);
+    off[3] = two ? ws.reserve(ld * M) : 0;
+    off[4] = two ? ws.reserve(sizeof(float) * M) : 0;
+    off[5] = two ? ws.reserve(sizeof(int32_t) * M) : 0;
+}
+
+inline ActBufs act_at(const Workspace &ws, int K, bool two, const size_t off[6]) {
+    ActBufs b;
+    b.ld = (int)round_up((size_t)K, 16);
+    b.q1 = ws.at<uint8_t>(off[0]);
+    b.s1 = ws.at<float>(off[1]);
+    b.z1 = ws.at<int32_t>(off[2]);
+    b.q2 = two ? ws.at<uint8_t>(off[3]) : nullptr;
+    b.s2 = two ? ws.at<float>(off[4]) : nullptr;
+    b.z2 = two ? ws.at<int32_t>(off[5]) : nullptr;
+    return b;
+}
+
+inline int quantize_into(IroHipContext *ctx, const float *x, int M, int K, int ldx,
+                         const ActBufs &b) {
+    return launch_quant_rows(ctx, x, M, K, ldx, b.q1, b.ld, b.s1, b.z1, nullptr, b.q2, b.s2,
+                             b.z2);
+}
+
+inline GemmArgs gemm_args(const ActBufs &b, int M, int K) {
+    GemmArgs a;
+    a.a1 = b.q1;
+    a.a2 = b.q2;
+    a.lda = b.ld;
+    a.sx1 = b.s1;
+    a.zx1 = b.z1;
+    a.sx2 = b.s2;
+    a.zx2 = b.z2;
+    a.M = M;
+    a.K = (int)round_up((size_t)K, 16);
+    return a;
+}
 
 int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi);
 int launch_conv_im2col(IroHipContext *ctx, const float *x, int T, int C, int T_out, int kernel,

@@ -306,11 +306,19 @@ int launch_quant_rows(IroHipContext *ctx, const float *x, int M, int K, int ldx,
                       int32_t *z2) {
     if (M <= 0 || K <= 0) return 0;
     const bool two = q2 != nullptr;
+    prof_begin(ctx);
+    int rc;
     if (ctx->convention == IRO_HIP_GCC_FASTMATH)
-        return two ? quant_rows_dispatch<1, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
-                   : quant_rows_dispatch<1, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
-    return two ? quant_rows_dispatch<0, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
-               : quant_rows_dispatch<0, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
+        rc = two ? quant_rows_dispatch<1, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
+                 : quant_rows_dispatch<1, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
+    else
+        rc = two ? quant_rows_dispatch<0, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
+                 : quant_rows_dispatch<0, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
+    // HBM: fp32 row in, one (two) code planes and row scale/zero out.
+    const double mk = (double)M * K, planes = two ? 2 : 1;
+    prof_end(ctx, two ? PK_QUANT_RESIDUAL : PK_QUANT, 0,
+             4 * mk + planes * (mk + 8.0 * M) + (res ? 4 * mk : 0));
+    return rc;
 }
 
 int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long long stride_n,

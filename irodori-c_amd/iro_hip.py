@@ -81,6 +81,18 @@ def load() -> C.CDLL:
         "iro_hip_dit_swiglu": ([_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i], _i),
         "iro_hip_conv1d_int8": ([_vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _vp, _i, _vp,
                                  C.POINTER(_i)], _i),
+        "iro_hip_dit_stack_create": ([_vp, _i, _i, _i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_dit_stack_set_block": ([_vp, _i] + [_vp] * 9, _i),
+        "iro_hip_dit_stack_step": ([_vp, _vp, _vp, _i, _i], _i),
+        "iro_hip_dit_stack_bytes": ([_vp], C.c_size_t),
+        "iro_hip_dit_stack_buffers": ([_vp] + [C.POINTER(_vp)] * 6, _i),
+        "iro_hip_dit_stack_destroy": ([_vp], None),
+        "iro_hip_profile_enable": ([_vp, _i], _i),
+        "iro_hip_profile_reset": ([_vp], _i),
+        "iro_hip_profile_kinds": ([], _i),
+        "iro_hip_profile_read": ([_vp, _i, C.POINTER(C.c_char_p), C.POINTER(C.c_longlong),
+                                  C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                  C.POINTER(C.c_double)], _i),
         "iro_hip_selfcheck": ([_vp], _i),
         "iro_hip_backend_name": ([_vp], C.c_char_p),
         # ops.h drop-in
@@ -337,6 +349,58 @@ class Context:
             None if bias is None else bias.vp, int(bool(residual)), y.vp, C.byref(t_out)),
             "conv1d_int8")
         return t_out.value
+
+
+    # -- profiler ----------------------------------------------------------------------
+    def profile(self, on: bool):
+        self._check(self.lib.iro_hip_profile_enable(self.h, int(bool(on))), "profile_enable")
+
+    def profile_reset(self):
+        self._check(self.lib.iro_hip_profile_reset(self.h), "profile_reset")
+
+    def profile_read(self) -> dict:
+        """{kind: (launches, total_ms, ops, bytes)} for kinds with launches."""
+        out = {}
+        for k in range(self.lib.iro_hip_profile_kinds()):
+            name = C.c_char_p()
+            n = C.c_longlong()
+            ms, ops, by = C.c_double(), C.c_double(), C.c_double()
+            self._check(self.lib.iro_hip_profile_read(self.h, k, C.byref(name), C.byref(n),
+                                                      C.byref(ms), C.byref(ops), C.byref(by)),
+                        "profile_read")
+            if n.value:
+                out[name.value.decode()] = (n.value, ms.value, ops.value, by.value)
+        return out
+
+
+class DiTStack:
+    """The int8 linear stack of one Euler step (iro_hip_dit_stack_*)."""
+
+    def __init__(self, ctx: Context, blocks: int, D: int, H: int, residual_mask: int = 8):
+        self.ctx = ctx
+        self.blocks, self.D, self.H = blocks, D, H
+        h = C.c_void_p()
+        ctx._check(ctx.lib.iro_hip_dit_stack_create(ctx.h, blocks, D, H, residual_mask,
+                                                    C.byref(h)), "dit_stack_create")
+        self.h = h
+
+    def set_block(self, block, ada, wq, wk, wv, wgate, wo, w1, w3, w2):
+        ctx = self.ctx
+        ctx._check(ctx.lib.iro_hip_dit_stack_set_block(
+            self.h, block, *[a.vp for a in (ada, wq, wk, wv, wgate, wo, w1, w3, w2)]),
+            "dit_stack_set_block")
+
+    def step(self, x: DeviceArray, cond: DeviceArray, B: int, S: int):
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_step(self.h, x.vp, cond.vp, B, S),
+                        "dit_stack_step")
+
+    def nbytes(self):
+        return self.ctx.lib.iro_hip_dit_stack_bytes(self.h)
+
+    def destroy(self):
+        if self.h:
+            self.ctx.lib.iro_hip_dit_stack_destroy(self.h)
+            self.h = None
 
 
 class _Int8Weight(C.Structure):

@@ -122,6 +122,111 @@ void cpub_linear(int conv, const float *x, int M, int K, const int8_t *wq,
     t[2] += t3 - t2;
 }
 
+typedef struct {
+    const int8_t *q;
+    const float *s;
+    const int32_t *cs;
+    int N, K;
+} CpubWeight;
+
+/* One int8 projection of an activation already quantized (one or two
+   planes), as int8_scratch_linear (dit.c:477-485): y = lin(q1); y += lin(q2). */
+static void cpub_project(int conv, const uint8_t *q1, const float *s1, const int32_t *z1,
+                         const uint8_t *q2, const float *s2, const int32_t *z2,
+                         const CpubWeight *w, float *y, int M, int32_t *work, double *t) {
+    double t0 = now_s();
+    gemm(q1, w->q, work, M, w->N, w->K);
+    double t1 = now_s();
+    orc_epilogue(conv, work, s1, z1, w->s, w->cs, NULL, y, M, w->N, 0);
+    double t2 = now_s();
+    t[1] += t1 - t0;
+    t[2] += t2 - t1;
+    if (q2) {
+        t0 = now_s();
+        gemm(q2, w->q, work, M, w->N, w->K);
+        t1 = now_s();
+        orc_epilogue(conv, work, s2, z2, w->s, w->cs, NULL, y, M, w->N, 1);
+        t2 = now_s();
+        t[1] += t1 - t0;
+        t[2] += t2 - t1;
+    }
+}
+
+static void cpub_quantize(int conv, const float *x, int M, int K, int two, uint8_t *q1,
+                          float *s1, int32_t *z1, float *r, uint8_t *q2, float *s2, int32_t *z2,
+                          double *t) {
+    double t0 = now_s();
+    if (two)
+        orc_quantize_rows_residual(conv, x, M, K, q1, s1, z1, r, q2, s2, z2);
+    else
+        orc_quantize_rows(conv, x, M, K, q1, s1, z1);
+    t[0] += now_s() - t0;
+}
+
+/* One DiT block's int8 linears on host memory, in the order and with the
+   activation sharing of dit.c: the modulation linear on cond, QKVG on one
+   quantization of x (dit.c:780-798), Wo on V with x += gate_a * out
+   (dit.c:876-884, 1013-1020), W1/W3 on one quantization of x, the SwiGLU
+   gate (ops.c:781-784), W2 on the (two-term) hidden state with
+   x += gate_m * out (dit.c:939-972, 1032-1039).  gate_a = mod[:, 2D:3D],
+   gate_m = mod[:, 5D:6D].  w = {ada, wq, wk, wv, wgate, wo, w1, w3, w2}.
+   residual_mask: 1 QKVG, 2 Wo, 4 W1/W3, 8 W2 (dit.c:278-291).  Adds
+   quantize / GEMM / epilogue-and-elementwise seconds to t[0..2].
+   Returns 0, or -1 when out of memory. */
+int cpub_dit_block(int conv, const CpubWeight *w, float *x, const float *cond, int B, int S,
+                   int D, int H, int residual_mask, double *t) {
+    const size_t M = (size_t)B * S;
+    const size_t KM = (size_t)(H > D ? H : D);
+    const size_t NM = (size_t)(6 * D > H ? 6 * D : H);
+    uint8_t *q1 = malloc(M * KM), *q2 = malloc(M * KM);
+    float *s1 = malloc(4 * M), *s2 = malloc(4 * M), *r = malloc(4 * M * KM);
+    int32_t *z1 = malloc(4 * M), *z2 = malloc(4 * M), *work = malloc(4 * M * NM);
+    float *mod = malloc(4 * (size_t)B * 6 * D), *gate = malloc(4 * (size_t)B * D);
+    float *qkvg = malloc(4 * 4 * M * D), *branch = malloc(4 * M * D);
+    float *a = malloc(4 * M * H), *b = malloc(4 * M * H);
+    int ok = q1 && q2 && s1 && s2 && r && z1 && z2 && work && mod && gate && qkvg && branch &&
+             a && b;
+    if (ok) {
+        /* modulation rows */
+        cpub_quantize(conv, cond, B, D, 0, q1, s1, z1, r, q2, s2, z2, t);
+        cpub_project(conv, q1, s1, z1, NULL, NULL, NULL, &w[0], mod, B, work, t);
+        /* QKVG */
+        int two = (residual_mask & 1) != 0;
+        cpub_quantize(conv, x, (int)M, D, two, q1, s1, z1, r, q2, s2, z2, t);
+        for (int i = 0; i < 4; i++)
+            cpub_project(conv, q1, s1, z1, two ? q2 : NULL, s2, z2, &w[1 + i], qkvg + i * M * D,
+                         (int)M, work, t);
+        /* Wo on V, attention gated residual */
+        two = (residual_mask & 2) != 0;
+        cpub_quantize(conv, qkvg + 2 * M * D, (int)M, D, two, q1, s1, z1, r, q2, s2, z2, t);
+        cpub_project(conv, q1, s1, z1, two ? q2 : NULL, s2, z2, &w[5], branch, (int)M, work, t);
+        double t0 = now_s();
+        for (int bb = 0; bb < B; bb++)
+            memcpy(gate + (size_t)bb * D, mod + (size_t)bb * 6 * D + 2 * D, 4 * (size_t)D);
+        orc_gated_residual(conv, x, gate, branch, B, S, D);
+        t[2] += now_s() - t0;
+        /* SwiGLU */
+        two = (residual_mask & 4) != 0;
+        cpub_quantize(conv, x, (int)M, D, two, q1, s1, z1, r, q2, s2, z2, t);
+        cpub_project(conv, q1, s1, z1, two ? q2 : NULL, s2, z2, &w[6], a, (int)M, work, t);
+        cpub_project(conv, q1, s1, z1, two ? q2 : NULL, s2, z2, &w[7], b, (int)M, work, t);
+        t0 = now_s();
+        orc_silu_mul(a, b, M * H);
+        t[2] += now_s() - t0;
+        two = (residual_mask & 8) != 0;
+        cpub_quantize(conv, a, (int)M, H, two, q1, s1, z1, r, q2, s2, z2, t);
+        cpub_project(conv, q1, s1, z1, two ? q2 : NULL, s2, z2, &w[8], branch, (int)M, work, t);
+        t0 = now_s();
+        for (int bb = 0; bb < B; bb++)
+            memcpy(gate + (size_t)bb * D, mod + (size_t)bb * 6 * D + 5 * D, 4 * (size_t)D);
+        orc_gated_residual(conv, x, gate, branch, B, S, D);
+        t[2] += now_s() - t0;
+    }
+    free(q1); free(q2); free(s1); free(s2); free(r); free(z1); free(z2); free(work);
+    free(mod); free(gate); free(qkvg); free(branch); free(a); free(b);
+    return ok ? 0 : -1;
+}
+
 /* Raw GEMM only (for the int32 cross-check against the oracle). */
 void cpub_gemm(const uint8_t *a, const int8_t *b, int32_t *c, int M, int N, int K) {
     gemm(a, b, c, M, N, K);

@@ -263,6 +263,65 @@ void orc_silu_mul(float *x, const float *g, size_t n) {
     for (size_t i = 0; i < n; i++) x[i] = (x[i] / (1.0f + expf(-x[i]))) * g[i];
 }
 
+/* ---- glibc expf restated ------------------------------------------------ */
+
+/* 2^(i/32) as doubles, minus i << 47 so the exponent of k can be added. */
+static const uint64_t EXP2_TAB[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+float orc_expf_restated(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep6f) return INFINITY;
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = fma(invln2n, xd, shift);
+    uint64_t ki;
+    memcpy(&ki, &kd, sizeof ki);
+    kd -= shift;
+    const double r = fma(invln2n, xd, -kd);
+    uint64_t t = EXP2_TAB[ki % 32] + (ki << 47);
+    double s;
+    memcpy(&s, &t, sizeof s);
+    const double z = fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float)(y * s);
+}
+
+long long orc_expf_mismatches(int threads) {
+    long long bad = 0;
+#ifdef _OPENMP
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) reduction(+ : bad) num_threads(threads)
+#else
+    (void)threads;
+#endif
+    for (long long hi = 0; hi < 65536; hi++) {
+        for (uint32_t lo = 0; lo < 65536; lo++) {
+            const uint32_t u = ((uint32_t)hi << 16) | lo;
+            float x;
+            memcpy(&x, &u, sizeof x);
+            const float a = orc_expf_restated(x), b = expf(x);
+            uint32_t ua, ub;
+            memcpy(&ua, &a, 4);
+            memcpy(&ub, &b, 4);
+            if (ua != ub && !(a != a && b != b)) bad++;
+        }
+    }
+    return bad;
+}
+
 /* ---- gated residual: dit.c:1013-1020, 1032-1039 ------------------------ */
 
 void orc_gated_residual(int conv, float *x, const float *gate,

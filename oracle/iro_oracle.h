@@ -72,6 +72,15 @@ void orc_selfcheck_kat(uint8_t *a, int8_t *b, int32_t *want);
    has no portable restatement. */
 void orc_silu_mul(float *x, const float *g, size_t n);
 
+/* glibc's expf restated (the function orc_silu_mul calls through libm):
+   glibc >= 2.28 sysdeps/ieee754/flt-32/e_expf.c, the exp2f table method of
+   ARM optimized-routines (N = 32 table, cubic in r), as GCC builds glibc's
+   x86-64 __expf_fma variant (both uses of InvLn2N*x contracted to FMA). */
+float orc_expf_restated(float x);
+/* Count the float inputs (all 2^32 bit patterns) where orc_expf_restated
+   and this process's libm expf differ (NaN == NaN). */
+long long orc_expf_mismatches(int threads);
+
 /* dit.c:1013-1020 / 1032-1039: x[b,s,:] += gate[b,:] * branch[b,s,:].
    Strict: two roundings.  Fast-math: one FMA (vfmadd132ps). */
 void orc_gated_residual(int conv, float *x, const float *gate,

@@ -54,6 +54,10 @@ class Oracle:
                                    C.c_int, C.c_int, C.c_int]
         L.orc_selfcheck_kat.argtypes = [_u8p, _i8p, _i32p]
         L.orc_silu_mul.argtypes = [_f32p, _f32p, C.c_size_t]
+        L.orc_expf_restated.argtypes = [C.c_float]
+        L.orc_expf_restated.restype = C.c_float
+        L.orc_expf_mismatches.argtypes = [C.c_int]
+        L.orc_expf_mismatches.restype = C.c_longlong
         L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
         L.orc_conv1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p,
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int,
@@ -147,6 +151,9 @@ class Oracle:
         g = _f32(g)
         self.lib.orc_silu_mul(_p(a, _f32p), _p(g, _f32p), a.size)
         return a
+
+    def expf_mismatches(self):
+        return self.lib.orc_expf_mismatches(self.threads)
 
     def gated_residual(self, conv, x, gate, branch, B, S):
         x = np.array(x, np.float32, copy=True)
@@ -288,3 +295,46 @@ class Reference:
                                       int(bool(residual)), _p(y, _f32p))
         assert rc == 0
         return y
+
+
+class _CpubWeight(C.Structure):
+    _fields_ = [("q", _i8p), ("s", _f32p), ("cs", _i32p), ("N", C.c_int), ("K", C.c_int)]
+
+
+class CpuBaseline:
+    """libcpubase.so: the reference's oneMKL int8 path as a CPU timing harness
+    (bench.py's cpu_baseline leg; also a host-side DiT block for tests)."""
+
+    def __init__(self, threads: int, mkl_path: str | None = None):
+        path = os.path.join(HERE, "libcpubase.so")
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        self.lib = L = C.CDLL(path)
+        L.cpub_init.argtypes = [C.c_char_p, C.c_int, C.c_char_p, C.c_size_t]
+        L.cpub_init.restype = C.c_int
+        L.cpub_dit_block.argtypes = [C.c_int, C.POINTER(_CpubWeight), _f32p, _f32p, C.c_int,
+                                     C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
+        L.cpub_dit_block.restype = C.c_int
+        L.cpub_gemm.argtypes = [_u8p, _i8p, _i32p, C.c_int, C.c_int, C.c_int]
+        buf = C.create_string_buffer(256)
+        self.mkl = bool(L.cpub_init((mkl_path or "").encode(), threads, buf, 256))
+        self.backend = buf.value.decode()
+        self.threads = threads
+
+    def dit_block(self, conv, weights, x, cond, B, S, D, H, residual_mask=8):
+        """weights: 9 (q, s, cs) tuples {ada, wq, wk, wv, wgate, wo, w1, w3, w2}.
+        Updates x in place; returns seconds (quantize, gemm, epilogue)."""
+        arr = (_CpubWeight * 9)()
+        keep = []
+        for i, (q, s, cs) in enumerate(weights):
+            q = np.ascontiguousarray(q, np.int8)
+            s = _f32(s)
+            cs = np.ascontiguousarray(cs, np.int32)
+            keep += [q, s, cs]
+            arr[i] = _CpubWeight(_p(q, _i8p), _p(s, _f32p), _p(cs, _i32p), q.shape[0], q.shape[1])
+        assert x.dtype == np.float32 and x.flags["C_CONTIGUOUS"]
+        t = (C.c_double * 3)()
+        rc = self.lib.cpub_dit_block(conv, arr, _p(x, _f32p), _p(_f32(cond), _f32p), B, S, D, H,
+                                     residual_mask, t)
+        assert rc == 0
+        return tuple(t)

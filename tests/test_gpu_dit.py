@@ -6,13 +6,14 @@ separate GEMMs (dit.c:786-792 QKVG, dit.c:944-947 W1/W3), the SwiGLU gate
 the gated residual (dit.c:1013-1020, 1032-1039).  The fused kernels must
 give the same bits.
 
-The SwiGLU gate uses expf.  The strict build calls glibc's scalar expf,
-which the kernel reproduces except where glibc misrounds; the fast-math
-build uses libmvec and an rcpps Newton step whose results depend on the
-host CPU.  The hidden state is therefore compared with a tolerance
-(max relative error 2e-7 with a floor, i.e. within one float ulp), and W2
-parity is pinned at its own boundary: the oracle re-runs the quantization
-and W2 from the GPU's hidden state and must match bit for bit.
+The SwiGLU gate calls expf.  The strict build calls glibc's scalar expf,
+which the kernel restates exactly (the restatement equals glibc's expf on
+all 2^32 inputs, see tests/test_oracle_pins.py), so the hidden state is
+bit-exact.  The fast-math build evaluates the gate with libmvec expf and an
+rcpps Newton step whose results depend on the host CPU, so that convention
+has no portable reference for the gate: the kernel keeps the strict gate
+there too ("parity unpinned" for the fast-math hidden state), and W2 is
+still pinned bit-exactly at its own boundary from the GPU's hidden state.
 """
 import numpy as np
 import pytest
@@ -99,7 +100,7 @@ def _swiglu_case(ctx, oracle, B, S, D, H, heavy, residual_w2):
     ctx.dit_swiglu(ctx.to_device(h), M, W13, W2, residual_w13=False, residual_w2=residual_w2,
                    hidden=hidden, x_res=xres, gate=ctx.to_device(gate), S=S)
     hid = hidden.numpy()
-    # W1, W3 on one shared quantization, then the gate (strict expf)
+    # W1, W3 on one shared quantization, then the gate (glibc expf)
     q, s, z = oracle.quantize_rows(conv, h)
     a, _ = oracle.linear(conv, q, s, z, *oracle.weight_quantize(conv, w1))
     b, _ = oracle.linear(conv, q, s, z, *oracle.weight_quantize(conv, w3))
@@ -122,14 +123,11 @@ def _swiglu_case(ctx, oracle, B, S, D, H, heavy, residual_w2):
 @pytest.mark.parametrize("heavy", [0, 1], ids=["gauss", "heavy-tail"])
 def test_swiglu_mlp(ctx, oracle, B, S, D, H, heavy):
     err, mism, n, got, want = _swiglu_case(ctx, oracle, B, S, D, H, heavy, residual_w2=True)
-    print(f"swiglu hidden: {mism}/{n} elements differ from glibc expf, max rel {err.max():.3g}")
-    assert err.max() <= 2.5e-7, "hidden state beyond one ulp of the strict reference"
-    if ctx.convention == 0:
-        assert mism <= max(2, n // 100000), "more gate mismatches than glibc misroundings explain"
+    assert mism == 0, f"hidden state: {mism}/{n} differ from silu(w1)*w3, max rel {err.max():.3g}"
     assert_bits_equal(got, want, "x += gate * W2(two-term)")
 
 
 def test_swiglu_mlp_single_term_w2(ctx, oracle):
     err, mism, n, got, want = _swiglu_case(ctx, oracle, 2, 40, 256, 320, 0, residual_w2=False)
-    assert err.max() <= 2.5e-7
+    assert mism == 0, f"hidden state: {mism}/{n} differ"
     assert_bits_equal(got, want, "x += gate * W2(one-term)")

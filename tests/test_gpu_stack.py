@@ -1,0 +1,47 @@
+"""The int8 DiT linear stack on the GPU (iro_hip_dit_stack_step) against the
+host-side block of oracle/cpu_baseline.c, which runs the reference's call
+sequence per block (dit.c:780-798, 876-884, 939-972, 1013-1039) with the
+oracle's quantizers and epilogues.  x after the step must match bit for bit.
+"""
+import numpy as np
+import pytest
+
+from iro_synth import gauss
+
+import iro_hip
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(D, H, blocks, seed):
+    shapes = [(6 * D, D), (D, D), (D, D), (D, D), (D, D), (D, D), (H, D), (H, D), (D, H)]
+    return [[gauss(seed + 100 * b + i, s, 0.02) for i, s in enumerate(shapes)]
+            for b in range(blocks)]
+
+
+@pytest.mark.parametrize("blocks,B,S,D,H,rm", [(2, 2, 40, 256, 320, 8), (2, 1, 33, 128, 96, 15),
+                                               (1, 3, 750, 1024, 2816, 8)],
+                         ids=["small-w2two", "small-alltwo", "baseline-1block"])
+def test_stack_step_matches_reference_sequence(ctx, oracle, blocks, B, S, D, H, rm):
+    from oracle import CpuBaseline
+    conv = ctx.convention
+    ws = _weights(D, H, blocks, 900)
+    x0 = gauss(901, (B * S, D))
+    cond = gauss(902, (B, D), 0.1)
+    stack = iro_hip.DiTStack(ctx, blocks, D, H, rm)
+    try:
+        for b in range(blocks):
+            stack.set_block(b, *[ctx.to_device(w) for w in ws[b]])
+        x = ctx.to_device(x0)
+        stack.step(x, ctx.to_device(cond), B, S)
+        got = x.numpy()
+        assert stack.nbytes() == blocks * sum(w.shape[0] * (w.shape[1] + 8) for w in ws[0])
+    finally:
+        stack.destroy()
+    cpu = CpuBaseline(8)
+    want = np.array(x0, copy=True)
+    for b in range(blocks):
+        cpu.dit_block(conv, [oracle.weight_quantize(conv, w) for w in ws[b]], want, cond, B, S,
+                      D, H, rm)
+    bad = int((got.view(np.int32) != want.view(np.int32)).sum())
+    assert bad == 0, f"{bad} of {got.size} elements of x differ"
