@@ -1,0 +1,199 @@
+"""Pins of the oracle (CPU, no GPU).
+
+1. Against the reference's own int8 path compiled from its sources
+   (oracle/_ref, both flag sets of the reference Makefile), on seeded inputs
+   with the edge cases of tests/test_int8_ops.c.  Skipped where the
+   reference sources were absent when the checker was built.
+2. Against what the reference's tests and the mathematics fix without any
+   build: the int16-saturation known answer (ops.c:375-398), the invariants
+   of tests/test_int8_ops.c:56-109 on the reference's own xorshift data,
+   closed forms of degenerate rows, brute-force int32 sums, and glibc's
+   expf on every float input.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from iro_synth import gauss, heavy_tail
+from oracle import GCC_FASTMATH, HERE, STRICT, Reference
+
+REF_DIR = os.path.join(HERE, "_ref")
+CONVS = [(STRICT, "strict"), (GCC_FASTMATH, "fast")]
+
+
+def _ref(flavour):
+    path = os.path.join(REF_DIR, f"libref_{flavour}.so")
+    if not os.path.exists(path):
+        pytest.skip("reference build absent (oracle/_ref needs the reference sources)")
+    return Reference(flavour)
+
+
+def _eq(a, b):
+    a, b = np.asarray(a), np.asarray(b)
+    if a.dtype == np.float32:
+        return np.array_equal(a.view(np.int32), b.view(np.int32))
+    return np.array_equal(a, b)
+
+
+# --- 1. against the reference build --------------------------------------------------
+
+CASES = [(7, 32, 64, 0), (23, 96, 128, 1), (112, 160, 1280, 0), (37, 184, 1280, 1),
+         (256, 1024, 1024, 0), (300, 256, 2816, 1), (5, 8, 100, 0)]
+
+
+def _inputs(M, N, K, heavy, seed):
+    x = gauss(seed, (M, K))
+    if heavy:
+        x = heavy_tail(x, seed + 1)
+    w = gauss(seed + 2, (N, K), 0.02)
+    w[min(3, N - 1)] = 0.0
+    if M > 4:
+        x[1] = 0.0
+        x[2] = 2.5
+        x[3] = -np.abs(x[3])
+        x[4, 17 % K] = 20.0
+    return x, w, gauss(seed + 3, (N,), 0.01), gauss(seed + 4, (M, N))
+
+
+@pytest.mark.parametrize("conv,flavour", CONVS, ids=["strict", "fastmath"])
+@pytest.mark.parametrize("M,N,K,heavy", CASES)
+def test_oracle_matches_reference_build(oracle, conv, flavour, M, N, K, heavy):
+    ref = _ref(flavour)
+    x, w, b, y0 = _inputs(M, N, K, heavy, 10 + M + N)
+    wq = ref.weight_quantize(w)
+    assert all(_eq(g, o) for g, o in zip(oracle.weight_quantize(conv, w), wq)), "weights"
+    q = ref.quantize_rows(x)
+    assert all(_eq(g, o) for g, o in zip(oracle.quantize_rows(conv, x), q)), "rows"
+    (r1, rr, r2) = ref.quantize_rows_residual(x)
+    (o1, orr, o2) = oracle.quantize_rows_residual(conv, x)
+    assert all(_eq(g, o) for g, o in zip(o1 + (orr,) + o2, r1 + (rr,) + r2)), "residual"
+    for bias in (None, b):
+        for acc in (False, True):
+            yr, wr = ref.linear(*q, *wq, bias=bias, y=y0, accumulate=acc)
+            yo, wo = oracle.linear(conv, *q, *wq, bias=bias, y=y0, accumulate=acc)
+            assert _eq(wo, wr) and _eq(yo, yr), f"linear bias={bias is not None} acc={acc}"
+
+
+def test_oracle_transposed_weight_matches_reference(oracle):
+    for conv, flavour in CONVS:
+        ref = _ref(flavour)
+        w_kn = gauss(5, (80, 96), 0.02)
+        got = oracle.weight_quantize_transposed(conv, w_kn, 96, 80)
+        want = ref.weight_quantize(w_kn, transposed_shape=(96, 80))
+        assert all(_eq(g, o) for g, o in zip(got, want))
+
+
+CONV_CASES = [(50, 16, 24, 7, 1, 1, 3), (50, 16, 24, 7, 1, 3, 9), (40, 8, 8, 7, 2, 1, 3),
+              (64, 32, 16, 3, 1, 9, 9), (33, 6, 10, 7, 1, 1, 3), (600, 64, 8, 7, 1, 3, 9)]
+
+
+@pytest.mark.parametrize("conv,flavour", CONVS, ids=["strict", "fastmath"])
+@pytest.mark.parametrize("T,C,N,k,st,dil,pad", CONV_CASES)
+@pytest.mark.parametrize("residual", [0, 1])
+def test_oracle_conv_matches_reference_build(oracle, conv, flavour, T, C, N, k, st, dil, pad,
+                                             residual):
+    ref = _ref(flavour)
+    x = gauss(70 + T + C, (T, C))
+    if T > 30:
+        x[10:30] = 0.0
+    w = gauss(71, (N, k * C), 0.02)
+    b = gauss(72, (N,), 0.01)
+    wq = oracle.weight_quantize(conv, w)
+    To = oracle.conv_out_len(T, k, st, dil, pad)
+    yr = ref.conv1d(x, *wq, k, st, dil, pad, bias=b, residual=residual, out_len=To)
+    yo, _, _, _ = oracle.conv1d(conv, x, *wq, k, st, dil, pad, bias=b, residual=residual)
+    assert _eq(yo, yr)
+
+
+def test_oracle_silu_matches_strict_reference_build(oracle):
+    ref = _ref("strict")
+    a = gauss(3, (200000,), 4.0)
+    g = gauss(4, (200000,))
+    assert _eq(oracle.silu_mul(a, g), ref.silu_mul(a, g))
+
+
+def test_reference_selfcheck_passes_on_both_builds():
+    for _, flavour in CONVS:
+        assert _ref(flavour).selfcheck() == 0
+
+
+# --- 2. pins that need no reference build ---------------------------------------------
+
+def test_known_answer_sums_exceed_int16(oracle):
+    # ops.c:375-398: extreme u8 x s8 sums must not saturate
+    a, b, want = oracle.selfcheck_kat()
+    brute = a.astype(np.int64) @ b.astype(np.int64).T
+    assert np.array_equal(want, brute)
+    assert brute.max() > 32767 or brute.min() < -32768
+    assert np.array_equal(oracle.gemm(a, b), want)
+
+
+def test_gemm_brute_force(oracle):
+    rng = np.random.default_rng(1)
+    a = rng.integers(0, 256, (37, 300), dtype=np.uint8)
+    b = rng.integers(-127, 128, (45, 300), dtype=np.int8)
+    assert np.array_equal(oracle.gemm(a, b), a.astype(np.int64) @ b.astype(np.int64).T)
+
+
+def _xorshift_data():
+    """The data generator of tests/test_int8_ops.c:12-16 (xorshift64, 24-bit
+    uniform in [-0.5, 0.5))."""
+    state = [0x9E3779B97F4A7C15]
+    mask = (1 << 64) - 1
+
+    def rnd():
+        r = state[0]
+        r ^= (r << 13) & mask
+        r ^= r >> 7
+        r ^= (r << 17) & mask
+        state[0] = r
+        return np.float32(((r >> 40) & 0xFFFFFF) / 16777216.0) - np.float32(0.5)
+
+    return rnd
+
+
+@pytest.mark.parametrize("conv", [STRICT, GCC_FASTMATH], ids=["strict", "fastmath"])
+def test_reference_test_int8_ops_invariants(oracle, conv):
+    # tests/test_int8_ops.c:118-125 cases with its own data and checks
+    rnd = _xorshift_data()
+    for (M, N, K, outlier) in [(7, 32, 64, 0), (23, 96, 128, 1), (112, 160, 1280, 0),
+                               (37, 184, 1280, 1)]:
+        w = np.array([rnd() * np.float32(0.08) for _ in range(N * K)], np.float32).reshape(N, K)
+        x = np.array([rnd() * np.float32(3.0) for _ in range(M * K)], np.float32).reshape(M, K)
+        if outlier:
+            for m in range(M):
+                x[m, 17] = np.float32(20.0) + rnd()
+        bias = np.array([rnd() for _ in range(N)], np.float32)
+        q, s, cs = oracle.weight_quantize(conv, w)
+        # |w - s q| <= s/2 and colsum (test_int8_ops.c:56-69)
+        assert (np.abs(w - s[:, None] * q) <= s[:, None] * 0.5 + 1e-7).all()
+        assert np.array_equal(cs, q.astype(np.int32).sum(1))
+        qa, sa, za = oracle.quantize_rows(conv, x)
+        # activation reconstruction bound (test_int8_ops.c:71-80)
+        assert ((za >= 0) & (za <= 255) & (sa > 0)).all()
+        rec = sa[:, None] * (qa.astype(np.float32) - za[:, None].astype(np.float32))
+        assert (np.abs(rec - x) <= sa[:, None] * 0.5 + 1e-5).all()
+        y, work = oracle.linear(conv, qa, sa, za, q, s, cs, bias=bias)
+        assert np.array_equal(work, qa.astype(np.int64) @ q.astype(np.int64).T)
+        # relative RMSE vs fp32 (test_int8_ops.c:99-109)
+        yref = x.astype(np.float64) @ w.astype(np.float64).T + bias
+        rel = np.sqrt(((y - yref) ** 2).sum() / (yref ** 2).sum())
+        assert rel < (0.05 if outlier else 0.02)
+
+
+@pytest.mark.parametrize("conv", [STRICT, GCC_FASTMATH], ids=["strict", "fastmath"])
+def test_degenerate_rows_closed_form(oracle, conv):
+    # tests/test_int8_ops.c:126-134 plus the closed forms of ops.c:321-348
+    x = np.zeros((3, 16), np.float32)
+    x[1] = 2.5
+    x[2] = -1.5
+    q, s, z = oracle.quantize_rows(conv, x)
+    assert s[0] == 1.0 and z[0] == 0 and not q[0].any()
+    assert z[1] == 0 and (q[1] == 255).all() and abs(s[1] - 2.5 / 255) < 1e-9
+    assert z[2] == 255 and not q[2].any()
+
+
+def test_expf_restatement_equals_libm_on_every_float(oracle):
+    # glibc's expf (the libm call of ops.c:783) restated: all 2^32 inputs
+    assert oracle.expf_mismatches() == 0
