@@ -53,6 +53,11 @@ void iro_hip_clear_error(IroHipContext *ctx);
 int iro_hip_sync(IroHipContext *ctx);
 /* The context's hipStream_t, for callers that share it. */
 void *iro_hip_stream(IroHipContext *ctx);
+/* GEMM tile shape of the context's M > 32 launches: 32*ti rows by 128*tj
+   columns (ti in {2,4}, tj in {1,2}); ti = tj = 0 restores the per-GEMM
+   choice.  A tuning knob: results are identical for every shape.  No
+   counterpart in the reference (oneMKL picks its own blocking). */
+int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj);
 
 int iro_hip_alloc(IroHipContext *ctx, size_t bytes, void **dptr);
 int iro_hip_free(IroHipContext *ctx, void *dptr);
@@ -61,6 +66,8 @@ int iro_hip_upload(IroHipContext *ctx, void *dst_device, const void *src_host, s
 int iro_hip_download(IroHipContext *ctx, void *dst_host, const void *src_device, size_t bytes);
 /* Byte fill with a kernel on the context stream (capture-safe). */
 int iro_hip_fill(IroHipContext *ctx, void *dst_device, int value, size_t bytes);
+/* Device-to-device copy queued on the context stream. */
+int iro_hip_copy(IroHipContext *ctx, void *dst_device, const void *src_device, size_t bytes);
 
 /* Stream-ordered timing on the context stream. */
 int iro_hip_event_create(void **event);
@@ -182,11 +189,16 @@ int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, 
 int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B, int S);
 /* Resident int8 bytes, iro_int8_weight_bytes summed (generate.h:43-46). */
 size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s);
-/* Device pointers of the step's activation buffers (last block's q, k, v,
-   gate [M,D], hidden [M,H], modulation rows [B,6D]). */
+/* Device pointers of the step's activation buffers: the last block's q, k,
+   v, gate [M,D] and hidden [M,H], and the modulation rows of every block
+   [B, blocks*P] with block b at column b*P, P = 6D rounded up to 256. */
 int iro_hip_dit_stack_buffers(IroHipDiTStack *s, float **q, float **k, float **v, float **gate,
                               float **hidden, float **mod);
 void iro_hip_dit_stack_destroy(IroHipDiTStack *s);
+/* Steps with the same x, cond, B and S as the previous step replay a HIP
+   graph of the whole step (default on); off runs every launch directly.
+   The profiler (iro_hip_profile_enable) always runs steps directly. */
+int iro_hip_dit_stack_use_graph(IroHipDiTStack *s, int on);
 
 /* ---- DACVAE int8 Conv1d (dacvae.c:543-688, no snake) ------------------- */
 

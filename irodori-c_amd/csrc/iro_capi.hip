@@ -32,6 +32,7 @@ int Workspace::commit() {
     size_t grow = need + need / 4;
     IRO_HIP_TRY(ctx, hipMalloc(&ctx->ws, grow));
     ctx->ws_bytes = grow;
+    ++ctx->ws_epoch;
     return 0;
 }
 
@@ -225,6 +226,40 @@ void kat_arrays(uint8_t *a, int8_t *b, int32_t *want) {
 }
 
 }  // namespace
+
+int weight_rows_alloc(IroHipContext *ctx, int N, int K, IroHipWeight **out) {
+    if (!ctx || !out || N <= 0 || K <= 0) return set_error(ctx, "weight: invalid arguments");
+    if (device_guard(ctx)) return -1;
+    const int pn[1] = {N};
+    IroHipWeight *w = nullptr;
+    if (weight_alloc(ctx, N, K, 0, 1, pn, false, &w)) return -1;
+    const size_t bytes = (size_t)w->Np * w->Kp;
+    if (launch_fill(ctx, w->packed, 0, bytes) || launch_fill(ctx, w->scale, 0, 4 * (size_t)w->Np) ||
+        launch_fill(ctx, w->colsum, 0, 4 * (size_t)w->Np)) {
+        iro_hip_weight_destroy(w);
+        return -1;
+    }
+    *out = w;
+    return 0;
+}
+
+int weight_rows_copy(IroHipContext *ctx, IroHipWeight *dst, int row0, const IroHipWeight *src) {
+    if (!ctx || !dst || !src || src->layout != 0 || dst->layout != 0 || src->Kp != dst->Kp ||
+        row0 % 32 || row0 < 0 || row0 + src->Np > dst->Np || src->rowsum != src->colsum ||
+        dst->rowsum != dst->colsum)
+        return set_error(ctx, "weight: rows do not fit the destination weight");
+    // Packed rows are 32-row blocks of Kp/32 fragments: rows row0.. start at
+    // byte row0 * Kp, and the source's Np rows are one contiguous run.
+    IRO_HIP_TRY(ctx, hipMemcpyAsync(dst->packed + (size_t)row0 * dst->Kp, src->packed,
+                                    (size_t)src->Np * src->Kp, hipMemcpyDeviceToDevice,
+                                    ctx->stream));
+    IRO_HIP_TRY(ctx, hipMemcpyAsync(dst->scale + row0, src->scale, sizeof(float) * src->Np,
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+    IRO_HIP_TRY(ctx, hipMemcpyAsync(dst->colsum + row0, src->colsum, sizeof(int32_t) * src->Np,
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+    return 0;
+}
+
 }  // namespace iro
 
 using namespace iro;
@@ -249,10 +284,11 @@ int iro_hip_create(int device, int convention, IroHipContext **out) {
         return -1;
     }
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, device) == hipSuccess)
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+        ctx->cus = prop.multiProcessorCount;
         snprintf(ctx->backend, sizeof(ctx->backend), "gfx950 MFMA i8 (%s, %d CUs)", prop.gcnArchName,
                  prop.multiProcessorCount);
-    else
+    } else
         snprintf(ctx->backend, sizeof(ctx->backend), "gfx950 MFMA i8");
     if (iro_hip_selfcheck(ctx) != 0) {
         iro_hip_destroy(ctx);
@@ -290,6 +326,18 @@ int iro_hip_sync(IroHipContext *ctx) {
 }
 
 void *iro_hip_stream(IroHipContext *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
+    if (!ctx) return -1;
+    if (ti == 0 && tj == 0) {
+        ctx->gemm_tile = 0;
+        return 0;
+    }
+    if ((ti != 2 && ti != 4) || (tj != 1 && tj != 2))
+        return set_error(ctx, "set_gemm_tile: tile must be TI in {2,4}, TJ in {1,2}");
+    ctx->gemm_tile = 10 * ti + tj;
+    return 0;
+}
 
 const char *iro_hip_backend_name(IroHipContext *ctx) {
     return ctx ? ctx->backend : "gfx950 MFMA i8";
@@ -330,6 +378,13 @@ int iro_hip_download(IroHipContext *ctx, void *dst, const void *src, size_t byte
 int iro_hip_fill(IroHipContext *ctx, void *dst, int value, size_t bytes) {
     if (!ctx) return -1;
     return launch_fill(ctx, dst, value, bytes);
+}
+
+int iro_hip_copy(IroHipContext *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (bytes && (!dst || !src))) return -1;
+    if (!bytes) return 0;
+    IRO_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return 0;
 }
 
 int iro_hip_event_create(void **event) {

@@ -98,14 +98,38 @@ int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w
 // The int8 weights of one DiT linear stack, device resident and pre-packed
 // once (the reference builds them once in iro_engine_init,
 // generate.c:527-579), plus the per-step activation buffers.
+//
+// The modulation linears of all blocks read the same conditioning rows, so
+// their weights are stacked into one [blocks * ada_np, D] weight (block b at
+// rows b * ada_np) and a step computes every block's modulation with one
+// quantization and one GEMM; block b's modulation is columns
+// b * ada_np .. + 6D of that output.  Integer sums and per-element
+// epilogues do not depend on the stacking, so the result is the one of
+// per-block linears.
+//
+// A step with the same buffers and shape as the previous one replays a HIP
+// graph of the whole step (captured on the second such call), so the
+// launch cost of its ~9 kernels per block is paid once.
 struct IroHipDiTStack {
     IroHipContext *ctx = nullptr;
     int blocks = 0, D = 0, H = 0;
     int residual_mask = 8;
-    std::vector<IroHipWeight *> ada, qkvg, wo, w13, w2;
+    IroHipWeight *ada_all = nullptr;
+    int ada_np = 0;
+    std::vector<char> ada_set;
+    std::vector<IroHipWeight *> qkvg, wo, w13, w2;
     int cap_rows = 0, cap_branches = 0;
     float *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *hidden = nullptr;
     float *mod = nullptr;
+    // graph of the last step's launches
+    int use_graph = 1;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    float *gx = nullptr;
+    const float *gcond = nullptr;
+    int gB = 0, gS = 0;
+    unsigned gepoch = 0;
+    int seen = 0;  // the last eager step had these arguments
 };
 
 using namespace iro;
@@ -120,10 +144,19 @@ void stack_free_acts(IroHipDiTStack *s) {
     s->cap_rows = s->cap_branches = 0;
 }
 
+void stack_drop_graph(IroHipDiTStack *s) {
+    if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    s->gexec = nullptr;
+    s->graph = nullptr;
+    s->seen = 0;
+}
+
 int stack_reserve(IroHipDiTStack *s, int M, int B) {
     if (M <= s->cap_rows && B <= s->cap_branches) return 0;
     IroHipContext *ctx = s->ctx;
     IRO_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    stack_drop_graph(s);
     stack_free_acts(s);
     const size_t md = sizeof(float) * (size_t)M * s->D;
     hipError_t e = hipMalloc(&s->q, md);
@@ -131,13 +164,37 @@ int stack_reserve(IroHipDiTStack *s, int M, int B) {
     if (e == hipSuccess) e = hipMalloc(&s->v, md);
     if (e == hipSuccess) e = hipMalloc(&s->g, md);
     if (e == hipSuccess) e = hipMalloc(&s->hidden, sizeof(float) * (size_t)M * s->H);
-    if (e == hipSuccess) e = hipMalloc(&s->mod, sizeof(float) * (size_t)B * 6 * s->D);
+    if (e == hipSuccess)
+        e = hipMalloc(&s->mod, sizeof(float) * (size_t)B * s->blocks * s->ada_np);
     if (e != hipSuccess) {
         stack_free_acts(s);
         return set_error(ctx, "dit_stack: hipMalloc failed: %s", hipGetErrorString(e));
     }
     s->cap_rows = M;
     s->cap_branches = B;
+    return 0;
+}
+
+// The launches of one step (sampler.c:243-301 runs dit_block per layer).
+int stack_launch(IroHipDiTStack *s, float *x, const float *cond, int B, int S) {
+    IroHipContext *ctx = s->ctx;
+    const int M = B * S, D = s->D;
+    const int rm = s->residual_mask;
+    const int ldm = s->blocks * s->ada_np;
+    // modulation rows of every block [B, blocks * ada_np]: shift/scale/gate
+    // for attention and MLP, 6D columns per block
+    if (linear_gated_impl(ctx, cond, B, D, s->ada_all, 0, s->mod, ldm, nullptr, nullptr, 0, 1))
+        return -1;
+    for (int blk = 0; blk < s->blocks; ++blk) {
+        const float *mod = s->mod + (size_t)blk * s->ada_np;
+        if (qkvg_impl(ctx, x, M, s->qkvg[blk], s->q, s->k, s->v, s->g, rm & 1)) return -1;
+        if (linear_gated_impl(ctx, s->v, M, D, s->wo[blk], rm & 2, nullptr, 0, x, mod + 2 * D,
+                              ldm, S))
+            return -1;
+        if (swiglu_impl(ctx, x, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, s->hidden, nullptr, x,
+                        mod + 5 * D, ldm, S))
+            return -1;
+    }
     return 0;
 }
 
@@ -186,7 +243,12 @@ int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int r
     s->D = D;
     s->H = H;
     s->residual_mask = residual_mask & 15;
-    s->ada.assign(blocks, nullptr);
+    s->ada_np = (int)round_up((size_t)6 * D, kNPad);
+    if (weight_rows_alloc(ctx, blocks * s->ada_np, D, &s->ada_all)) {
+        delete s;
+        return -1;
+    }
+    s->ada_set.assign(blocks, 0);
     s->qkvg.assign(blocks, nullptr);
     s->wo.assign(blocks, nullptr);
     s->w13.assign(blocks, nullptr);
@@ -213,61 +275,100 @@ int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, 
         iro_hip_weight_create_fused(ctx, qkvg_parts, qkvg_n, 4, D, 0, &nq) ||
         iro_hip_weight_create(ctx, wo, D, D, &no) ||
         iro_hip_weight_create_fused(ctx, w13_parts, w13_n, 2, D, 1, &n13) ||
-        iro_hip_weight_create(ctx, w2, D, H, &n2)) {
+        iro_hip_weight_create(ctx, w2, D, H, &n2) ||
+        weight_rows_copy(ctx, s->ada_all, block * s->ada_np, na)) {
         for (IroHipWeight *w : {na, nq, no, n13, n2}) iro_hip_weight_destroy(w);
         return -1;
     }
-    for (auto *v : {&s->ada, &s->qkvg, &s->wo, &s->w13, &s->w2}) iro_hip_weight_destroy((*v)[block]);
-    s->ada[block] = na;
+    iro_hip_weight_destroy(na);  // drains the stream: its rows are copied
+    for (auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2}) iro_hip_weight_destroy((*v)[block]);
     s->qkvg[block] = nq;
     s->wo[block] = no;
     s->w13[block] = n13;
     s->w2[block] = n2;
+    s->ada_set[block] = 1;
+    stack_drop_graph(s);
     return 0;
 }
 
-// One Euler step's int8 linears (sampler.c:243-301 runs dit_block per
-// layer): for each block, the modulation linear on the conditioning rows,
-// QKVG, Wo with the attention gated residual, and the SwiGLU MLP with the
-// MLP gated residual.  x [B*S, D] is updated in place; cond is [B, D].
-// The attention core between QKVG and Wo and the RMSNorm-modulate before
-// QKVG and W1/W3 are fp32 and outside this path: Wo reads V as its input
-// and QKVG/W1W3 read x.
+// One Euler step's int8 linears: the modulation linears of all blocks,
+// then per block QKVG, Wo with the attention gated residual, and the
+// SwiGLU MLP with the MLP gated residual.  x [B*S, D] is updated in place;
+// cond is [B, D].  The attention core between QKVG and Wo and the
+// RMSNorm-modulate before QKVG and W1/W3 are fp32 and outside this path:
+// Wo reads V as its input and QKVG/W1W3 read x.
 int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B, int S) {
     if (!s || !x || !cond || B <= 0 || S <= 0) return -1;
     IroHipContext *ctx = s->ctx;
     for (int b = 0; b < s->blocks; ++b)
-        if (!s->ada[b]) return set_error(ctx, "dit_stack: block %d has no weights", b);
-    const int M = B * S, D = s->D;
-    if (stack_reserve(s, M, B)) return -1;
-    const int rm = s->residual_mask;
-    for (int blk = 0; blk < s->blocks; ++blk) {
-        // modulation rows [B, 6D]: shift/scale/gate for attention and MLP
-        if (linear_gated_impl(ctx, cond, B, D, s->ada[blk], 0, s->mod, 6 * D, nullptr, nullptr, 0,
-                              1))
-            return -1;
-        if (qkvg_impl(ctx, x, M, s->qkvg[blk], s->q, s->k, s->v, s->g, rm & 1)) return -1;
-        if (linear_gated_impl(ctx, s->v, M, D, s->wo[blk], rm & 2, nullptr, 0, x, s->mod + 2 * D,
-                              6 * D, S))
-            return -1;
-        if (swiglu_impl(ctx, x, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, s->hidden, nullptr, x,
-                        s->mod + 5 * D, 6 * D, S))
-            return -1;
+        if (!s->ada_set[b]) return set_error(ctx, "dit_stack: block %d has no weights", b);
+    if (stack_reserve(s, B * S, B)) return -1;
+    const bool same = s->gx == x && s->gcond == cond && s->gB == B && s->gS == S &&
+                      s->gepoch == ctx->ws_epoch;
+    if (!s->use_graph || ctx->prof) {
+        stack_drop_graph(s);
+        return stack_launch(s, x, cond, B, S) || ctx->has_err ? -1 : 0;
     }
+    if (same && s->gexec) {
+        IRO_HIP_TRY(ctx, hipGraphLaunch(s->gexec, ctx->stream));
+        return ctx->has_err ? -1 : 0;
+    }
+    if (!same || !s->seen) {
+        // First step with these buffers: run it directly (this sizes the
+        // workspace), capture on the next one.
+        stack_drop_graph(s);
+        if (stack_launch(s, x, cond, B, S) || ctx->has_err) return -1;
+        s->gx = x;
+        s->gcond = cond;
+        s->gB = B;
+        s->gS = S;
+        s->gepoch = ctx->ws_epoch;
+        s->seen = 1;
+        return 0;
+    }
+    IRO_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = stack_launch(s, x, cond, B, S);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (rc || e != hipSuccess || !graph || s->gepoch != ctx->ws_epoch) {
+        if (graph) (void)hipGraphDestroy(graph);
+        stack_drop_graph(s);
+        return set_error(ctx, "dit_stack: graph capture failed (%s)",
+                         e != hipSuccess ? hipGetErrorString(e) : "a launch failed");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return set_error(ctx, "dit_stack: graph instantiate failed: %s", hipGetErrorString(ei));
+    }
+    s->graph = graph;
+    s->gexec = exec;
+    IRO_HIP_TRY(ctx, hipGraphLaunch(s->gexec, ctx->stream));
     return ctx->has_err ? -1 : 0;
+}
+
+int iro_hip_dit_stack_use_graph(IroHipDiTStack *s, int on) {
+    if (!s) return -1;
+    s->use_graph = on != 0;
+    if (!on) stack_drop_graph(s);
+    return 0;
 }
 
 size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s) {
     if (!s) return 0;
     size_t n = 0;
-    for (int b = 0; b < s->blocks; ++b)
-        for (const auto *v : {&s->ada, &s->qkvg, &s->wo, &s->w13, &s->w2})
-            n += iro_hip_weight_bytes((*v)[b]);
+    for (int b = 0; b < s->blocks; ++b) {
+        if (s->ada_set[b]) n += (size_t)6 * s->D * (s->D + sizeof(float) + sizeof(int32_t));
+        for (const auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2}) n += iro_hip_weight_bytes((*v)[b]);
+    }
     return n;
 }
 
-// Pointers to the last step's per-block scratch outputs of the final block
-// (q, k, v, gate [M,D], hidden [M,H], modulation [B,6D]) for inspection.
+// Pointers to the last step's scratch outputs: the final block's q, k, v,
+// gate [M,D] and hidden [M,H], and the modulation rows of every block
+// [B, blocks * ada_np] (block b at column b * ada_np, ada_np = 6D rounded
+// up to 256).
 int iro_hip_dit_stack_buffers(IroHipDiTStack *s, float **q, float **k, float **v, float **gate,
                               float **hidden, float **mod) {
     if (!s) return -1;
@@ -283,7 +384,9 @@ int iro_hip_dit_stack_buffers(IroHipDiTStack *s, float **q, float **k, float **v
 void iro_hip_dit_stack_destroy(IroHipDiTStack *s) {
     if (!s) return;
     if (s->ctx) (void)hipStreamSynchronize(s->ctx->stream);
-    for (auto *v : {&s->ada, &s->qkvg, &s->wo, &s->w13, &s->w2})
+    stack_drop_graph(s);
+    iro_hip_weight_destroy(s->ada_all);
+    for (auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2})
         for (IroHipWeight *w : *v) iro_hip_weight_destroy(w);
     stack_free_acts(s);
     delete s;

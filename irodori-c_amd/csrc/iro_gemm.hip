@@ -8,12 +8,28 @@
 // acc + 128 * rowsum[n], rowsum = sum over k of W[n,k]  (|acc| < 2^31 for
 // K < 66k).
 //
-// Tiling: 256 threads = 4 wavefronts in 2x2, block tile 128x128x64, wave
-// tile 64x64 = 2x2 v_mfma_i32_32x32x32_i8.  Both operands are staged in LDS
-// in fragment order (lane L reads 16 bytes at L*16), so every ds_read_b128
-// is conflict-free; LDS is double-buffered with one barrier per k-step.
+// Tile kernel: 256 threads = 4 wavefronts side by side along N.  Block tile
+// BM x BN = 32*TI x 128*TJ, wave tile 32*TI x 32*TJ of
+// v_mfma_i32_32x32x32_i8.  The activation tile is shared by the four waves
+// and staged through double-buffered LDS in fragment order (lane L reads
+// 16 bytes at L*16: conflict-free ds_read_b128).  Each weight fragment is
+// used by exactly one wave, so waves read their fragments straight from the
+// pre-packed buffer into registers (one contiguous 1 KiB per wave load),
+// one k-step ahead; weights never touch LDS.  Per k-step (BK = 64) a wave
+// issues 4*TI*TJ MFMAs against 2*TI LDS reads.
+//
+// Addresses never leave the operands: rows past M repeat row M-1 and k past
+// the activation's extent repeats its last 16 bytes; the packed weight is
+// zero for every k >= K, so those products vanish, and rows past M are
+// never stored.  The main loop therefore has no branches around its loads.
+//
+// Skinny kernel (M <= 32, e.g. the modulation linear on the conditioning
+// rows): one block per 64 weight rows, the four waves split K, their int32
+// partial sums meet in LDS (integer addition: exact in any order) and wave 0
+// runs the epilogue.  It is bound by the weight read.
+//
 // The two-term activation (ops.c:427-442 + dit.c:477-485) runs both planes
-// against the same W fragment, two accumulators, one pass over W.
+// against the same weight fragment: two accumulators, one pass over W.
 //
 // Epilogues (all per element, identical op order to the reference):
 //   EPI_LINEAR  ops.c:468-490 four branches (+ optional raw int32 `work`)
@@ -23,6 +39,8 @@
 #include "iro_internal.h"
 #include "iro_round.h"
 
+#include <type_traits>
+
 namespace iro {
 
 namespace {
@@ -30,9 +48,9 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int TILE_A = BM * BK;  // bytes per A plane per stage
-constexpr int TILE_B = BN * BK;
+using I0 = std::integral_constant<int, 0>;
+using I1 = std::integral_constant<int, 1>;
+
 
 struct KParams {
     const uint8_t *a1, *a2;
@@ -61,6 +79,8 @@ struct KParams {
     int ldg;
     int ldx;
     int rows_per_branch;
+    int tiles_n, tiles_m;  // tiles of the tile kernel along N and M
+    int tiles_per_xcd;     // ceil(tiles / 8)
 };
 
 // ops.c:468-490: y = t*c [+ b] or y += t*c [+ b] with the build's rounding.
@@ -90,7 +110,8 @@ __device__ __forceinline__ float add_term(float y, float t, float c) {
 // exp2f table method of ARM optimized-routines, N = 32:
 //   x*N/ln2 = k + r,  exp(x) = 2^(k/N) * (1 + C2 r + C1 r^2 + C0 r^3),
 // in double, with GCC's contraction of both uses of InvLn2N*x into FMAs.
-// Bit-identical to glibc's expf for every float input.
+// Bit-identical to glibc's expf for every float input.  The 2^(i/32)
+// table is copied into LDS by the kernels that use it.
 __constant__ uint64_t kExp2Tab[32] = {
     0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
     0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
@@ -101,7 +122,7 @@ __constant__ uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-__device__ __forceinline__ float expf_glibc(float x) {
+__device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     if (x != x) return x + x;
     if (x > 0x1.62e42ep6f) return __builtin_inff();  // overflow
     if (x < -0x1.9fe368p6f) return 0.0f;             // underflow (and -inf)
@@ -113,7 +134,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
     const double r = __builtin_fma(invln2n, xd, -kd);
-    const uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+    const uint64_t t = tab[ki % 32] + (ki << 47);
     const double s = __longlong_as_double((long long)t);
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
@@ -123,221 +144,513 @@ __device__ __forceinline__ float expf_glibc(float x) {
 }
 
 // ops.c:781-784 as the strict build computes it: x / (1 + expf(-x)) * g.
-__device__ __forceinline__ float silu_mul(float a, float g) {
-    const float e = expf_glibc(-a);
+__device__ __forceinline__ float silu_mul(float a, float g, const uint64_t *tab) {
+    const float e = expf_glibc(-a, tab);
     return (a / (1.0f + e)) * g;
 }
 
-template <int CONV, int EPI, bool TWO>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(KParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][(TWO ? 2 : 1) * TILE_A + TILE_B];
+// Per-row parameters of a block's rows, staged in LDS: scale and zero
+// point of each plane and the gate row offset of the gated epilogue.
+template <int BM, bool TWO>
+struct RowLds {
+    float sx[TWO ? 2 : 1][BM];
+    int zx[TWO ? 2 : 1][BM];
+    int goff[BM];
+};
 
+template <int EPI, bool TWO, int BM>
+__device__ __forceinline__ void stage_rows(const KParams &p, RowLds<BM, TWO> &r, int m0, int tid) {
+    if (tid < BM) {
+        int m = m0 + tid;
+        m = m < p.M ? m : p.M - 1;
+        r.sx[0][tid] = p.sx1[m];
+        r.zx[0][tid] = p.zx1[m];
+        if (TWO) {
+            r.sx[TWO ? 1 : 0][tid] = p.sx2[m];
+            r.zx[TWO ? 1 : 0][tid] = p.zx2[m];
+        }
+        if (EPI == EPI_GATED) r.goff[tid] = (m / p.rows_per_branch) * p.ldg;
+    }
+}
+
+// Per-column parameters of the TJ 32-column blocks of one wave (packed
+// column order), loaded before the main loop so their latency is hidden.
+template <int TJ>
+struct ColParams {
+    int cs[TJ], rs[TJ];
+    float sw[TJ], b[TJ];
+};
+
+template <int EPI, int TJ>
+__device__ __forceinline__ ColParams<TJ> load_cols(const KParams &p, int nb0, int lane) {
+    ColParams<TJ> c;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int pc = (nb0 + j) * 32 + (lane & 31);  // packed: padded to Np, in bounds
+        c.cs[j] = p.colsum[pc];
+        c.rs[j] = p.rowsum[pc];
+        c.sw[j] = p.sw[pc];
+        c.b[j] = (EPI == EPI_LINEAR && p.bias && pc < p.N) ? p.bias[pc] : 0.0f;
+    }
+    return c;
+}
+
+// Epilogue of one wave's TI x TJ accumulator tiles.  32x32 accumulator
+// layout: lane L, register r holds row 8*(r/4) + 4*(L/32) + r%4 and column
+// L%32 of the tile.  Loads use clamped rows so they can be issued together;
+// only stores are predicated on m < M.
+template <int CONV, int EPI, bool TWO, int TI, int TJ, int BM>
+__device__ __forceinline__ void epilogue(const KParams &p, const v16i (&acc)[TI][TJ],
+                                         const v16i (&acc2)[TI][TJ], const ColParams<TJ> &cp,
+                                         const RowLds<BM, TWO> &rl, const uint64_t *exptab,
+                                         int m0, int nb0, int lane) {
+    const bool has_bias = EPI == EPI_LINEAR && p.bias != nullptr;
+    const int half = lane >> 5;
+    // QKVG: destination segment of each column block.
+    float *segp[TJ];
+    int segc[TJ];
+    if (EPI == EPI_QKVG) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int pc = (nb0 + j) * 32 + (lane & 31);
+            const int sg = pc / p.seg_n;
+            segp[j] = sg == 0 ? p.seg0 : (sg == 1 ? p.seg1 : (sg == 2 ? p.seg2 : p.seg3));
+            segc[j] = pc - sg * p.seg_n;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        float sx[16], sx2[16];
+        int zx[16], zx2[16], mrow[16], mcl[16], goff[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int rb = i * 32 + g * 8 + half * 4;
+            const float4 s4 = *reinterpret_cast<const float4 *>(&rl.sx[0][rb]);
+            const int4 z4 = *reinterpret_cast<const int4 *>(&rl.zx[0][rb]);
+            sx[g * 4 + 0] = s4.x; sx[g * 4 + 1] = s4.y; sx[g * 4 + 2] = s4.z; sx[g * 4 + 3] = s4.w;
+            zx[g * 4 + 0] = z4.x; zx[g * 4 + 1] = z4.y; zx[g * 4 + 2] = z4.z; zx[g * 4 + 3] = z4.w;
+            if (TWO) {
+                const float4 t4 = *reinterpret_cast<const float4 *>(&rl.sx[TWO ? 1 : 0][rb]);
+                const int4 w4 = *reinterpret_cast<const int4 *>(&rl.zx[TWO ? 1 : 0][rb]);
+                sx2[g * 4 + 0] = t4.x; sx2[g * 4 + 1] = t4.y; sx2[g * 4 + 2] = t4.z; sx2[g * 4 + 3] = t4.w;
+                zx2[g * 4 + 0] = w4.x; zx2[g * 4 + 1] = w4.y; zx2[g * 4 + 2] = w4.z; zx2[g * 4 + 3] = w4.w;
+            }
+            if (EPI == EPI_GATED) {
+                const int4 o4 = *reinterpret_cast<const int4 *>(&rl.goff[rb]);
+                goff[g * 4 + 0] = o4.x; goff[g * 4 + 1] = o4.y; goff[g * 4 + 2] = o4.z; goff[g * 4 + 3] = o4.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + rb + e;
+                mrow[g * 4 + e] = m;
+                mcl[g * 4 + e] = m < p.M ? m : p.M - 1;
+            }
+        }
+        float yv[TJ][16];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int pc = (nb0 + j) * 32 + (lane & 31);
+            float old[16], gv[16];
+            if (EPI == EPI_LINEAR && p.accumulate) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    old[r] = pc < p.N ? p.y[(size_t)mcl[r] * p.ldy + pc] : 0.0f;
+            }
+            if (EPI == EPI_GATED) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    old[r] = pc < p.N ? p.xres[(size_t)mcl[r] * p.ldx + pc] : 0.0f;
+                    gv[r] = pc < p.N ? p.gate[goff[r] + pc] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int raw = acc[i][j][r] + 128 * cp.rs[j];
+                const float t = (float)(raw - zx[r] * cp.cs[j]);
+                const float c = sx[r] * cp.sw[j];
+                float y;
+                if (EPI == EPI_LINEAR)
+                    y = lin_out<CONV>(t, c, cp.b[j], has_bias, p.accumulate != 0,
+                                      p.accumulate ? old[r] : 0.0f);
+                else
+                    y = t * c;
+                if (TWO) {
+                    const int raw2 = acc2[i][j][r] + 128 * cp.rs[j];
+                    const float t2 = (float)(raw2 - zx2[r] * cp.cs[j]);
+                    const float c2 = sx2[r] * cp.sw[j];
+                    y = add_term<CONV>(y, t2, c2);
+                }
+                yv[j][r] = y;
+                const bool ok = mrow[r] < p.M && pc < p.N;
+                if (EPI == EPI_LINEAR) {
+                    if (ok) {
+                        p.y[(size_t)mrow[r] * p.ldy + pc] = y;
+                        if (p.work) p.work[(size_t)mrow[r] * p.ldw + pc] = raw;
+                    }
+                } else if (EPI == EPI_QKVG) {
+                    if (ok) segp[j][(size_t)mrow[r] * p.seg_n + segc[j]] = y;
+                } else if (EPI == EPI_GATED) {
+                    if (ok)
+                        p.xres[(size_t)mrow[r] * p.ldx + pc] =
+                            CONV == 1 ? __builtin_fmaf(gv[r], y, old[r]) : old[r] + gv[r] * y;
+                }
+            }
+        }
+        if (EPI == EPI_SWIGLU) {
+            // Interleaved W1/W3: column block nb0+j (j even) is W1 block
+            // (nb0+j)/2, block nb0+j+1 the matching W3 block.
+#pragma unroll
+            for (int j = 0; j + 1 < TJ; j += 2) {
+                const int hcol = ((nb0 + j) >> 1) * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    if (mrow[r] < p.M && hcol < p.hidden_n)
+                        p.hidden[(size_t)mrow[r] * p.ldh + hcol] =
+                            silu_mul(yv[j][r], yv[j + 1][r], exptab);
+                }
+            }
+        }
+    }
+}
+
+// Tile -> (column slab, row tile).  Workgroups are dealt to the eight XCDs
+// round-robin (workgroup w runs on XCD w % 8), so workgroup w takes tile
+// (w % 8) * per + w / 8 of the column-slab-major order: each XCD works
+// through a contiguous run of tiles, i.e. a few weight column slabs, which
+// then stay in that XCD's L2 while every row tile passes over them.
+__device__ __forceinline__ bool tile_of(int w, int tiles_m, int tiles_n, int per, int &bx,
+                                        int &by) {
+    const int t = (w & 7) * per + (w >> 3);
+    if (t >= tiles_m * tiles_n) return false;
+    bx = t / tiles_m;
+    by = t - bx * tiles_m;
+    return true;
+}
+
+// Main loop: the activation tile is staged through LDS in chunks of KC
+// bytes of k (double-buffered: chunk c+1 is fetched into registers while
+// chunk c is consumed, one barrier per chunk), and each wave streams its
+// own weight fragments through a ring of R register slots, R k-blocks of
+// 32 ahead of their use.
+template <int CONV, int EPI, bool TWO, int TI, int TJ>
+__global__ __launch_bounds__(256) void gemm_tile_kernel(KParams p) {
+    constexpr int BM = 32 * TI;
+    constexpr int PL = TWO ? 2 : 1;
+    constexpr int CP = 8;                               // 16-byte pieces per thread per chunk
+    constexpr int KC = CP * 256 * 16 / (BM * PL);       // chunk of k, bytes per row per plane
+    constexpr int KBC = KC / 32;                        // k blocks per chunk
+    constexpr int PLANE = BM * KC;                      // LDS bytes per plane per chunk
+    constexpr int R = 8 / TJ <= KBC ? 8 / TJ : KBC;     // weight ring depth in k blocks
+    static_assert(KC % 32 == 0 && KBC % R == 0, "chunk must hold whole rings");
+    __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][PL * PLANE];
+    __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
+    __shared__ uint64_t exptab[32];
+
+    int bx, by;
+    if (!tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.tiles_per_xcd, bx, by)) return;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
+    const int m0 = by * BM;
+    const int nb0 = bx * 4 * TJ + wave * TJ;  // first packed 32-row weight block of this wave
 
-    // Global sources of this thread's two 16-byte chunks per operand.
-    const uint8_t *pa1[2];
-    const uint8_t *pa2[2];
-    const int8_t *pb[2];
-    int kk_of[2];
+    stage_rows<EPI, TWO, BM>(p, rl, m0, tid);
+    if (EPI == EPI_SWIGLU && tid < 32) exptab[tid] = kExp2Tab[tid];
+    const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane);
+
+    // Activation pieces of this thread: piece q = tid + 256*i of a chunk is
+    // plane q / (PLANE/16), then fragment f = (q % (PLANE/16)) / 64 =
+    // [k block kbl][row block rb] and lane ln = q % 64 of that fragment.
+    const uint8_t *pa[CP];
+    int kof[CP];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = tid + 256 * i;
-        const int f = c >> 6, ln = c & 63;
-        const int row = (f & 3) * 32 + (ln & 31);
-        const int kk = (f >> 2) * 32 + (ln >> 5) * 16;
-        int gr = m0 + row;
+    for (int i = 0; i < CP; ++i) {
+        const int q = tid + 256 * i;
+        const int pl = q / (PLANE / 16);
+        const int qq = q % (PLANE / 16);
+        const int f = qq >> 6, ln = qq & 63;
+        const int kbl = f / TI, rb = f % TI;
+        int gr = m0 + rb * 32 + (ln & 31);
         gr = gr < p.M ? gr : p.M - 1;
-        kk_of[i] = kk;
-        pa1[i] = p.a1 + (size_t)gr * p.lda + kk;
-        pa2[i] = TWO ? p.a2 + (size_t)gr * p.lda + kk : nullptr;
-        pb[i] = p.bp + ((size_t)((n0 >> 5) + (f >> 1)) * p.kb_count + (f & 1)) * 1024 + ln * 16;
+        kof[i] = kbl * 32 + (ln >> 5) * 16;
+        pa[i] = (pl == 0 ? p.a1 : p.a2) + (size_t)gr * p.lda;
     }
+    const int8_t *pbw = p.bp + (size_t)nb0 * p.kb_count * 1024 + lane * 16;
+    const size_t jstride = (size_t)p.kb_count * 1024;
+    const int nkb = (p.K + 31) / 32;  // k blocks holding activation data
+    const int nc = (p.K + KC - 1) / KC;
 
-    v16i acc[2][2], acc2[2][2];
+    v16i acc[TI][TJ], acc2[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 acc[i][j][r] = 0;
                 acc2[i][j][r] = 0;
             }
-        }
 
-    v4i ra1[2], ra2[2], rb[2];
+    v4i ra[CP];
+    v4i rb[R][TJ];
     const v4i flip = {(int)0x80808080, (int)0x80808080, (int)0x80808080, (int)0x80808080};
-    const v4i zero4 = {0, 0, 0, 0};
 
-    auto gload = [&](int kt) {
-        const int k0 = kt * BK;
+    auto load_chunk = [&](int c) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const bool ok = k0 + kk_of[i] < p.K;
-            ra1[i] = (ok ? *reinterpret_cast<const v4i *>(pa1[i] + k0) : zero4) ^ flip;
-            if (TWO) ra2[i] = (ok ? *reinterpret_cast<const v4i *>(pa2[i] + k0) : zero4) ^ flip;
-            rb[i] = *reinterpret_cast<const v4i *>(pb[i] + (size_t)kt * 2048);
+        for (int i = 0; i < CP; ++i) {
+            int k = c * KC + kof[i];
+            k = k < p.K - 16 ? k : p.K - 16;  // past the extent: any bytes, W is zero there
+            ra[i] = *reinterpret_cast<const v4i *>(pa[i] + k);
         }
     };
-    auto sstore = [&](int buf) {
-        uint8_t *base = lds[buf];
+    auto store_chunk = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int off = (tid + 256 * i) * 16;
-            *reinterpret_cast<v4i *>(base + off) = ra1[i];
-            if (TWO) *reinterpret_cast<v4i *>(base + TILE_A + off) = ra2[i];
-            *reinterpret_cast<v4i *>(base + (TWO ? 2 : 1) * TILE_A + off) = rb[i];
-        }
+        for (int i = 0; i < CP; ++i)
+            *reinterpret_cast<v4i *>(&lds_a[buf][(tid + 256 * i) * 16]) = ra[i] ^ flip;
     };
-
-    const int nk = (p.K + BK - 1) / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
-        const uint8_t *A1 = lds[cur];
-        const uint8_t *A2 = A1 + TILE_A;
-        const uint8_t *B = A1 + (TWO ? 2 : 1) * TILE_A;
+    auto load_b = [&](auto slot, int kb) {
+        constexpr int S = decltype(slot)::value;
+        kb = kb < nkb ? kb : nkb - 1;  // past the end: a harmless repeat
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            v4i a[2], a2[2], b[2];
+        for (int j = 0; j < TJ; ++j)
+            rb[S][j] = *reinterpret_cast<const v4i *>(pbw + j * jstride + (size_t)kb * 1024);
+    };
+    auto mma = [&](auto slot, const uint8_t *abuf, int kbl) {
+        constexpr int S = decltype(slot)::value;
+        v4i a[PL][TI];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int off = ((s * 4 + wm * 2 + i) * 64 + lane) * 16;
-                a[i] = *reinterpret_cast<const v4i *>(A1 + off);
-                if (TWO) a2[i] = *reinterpret_cast<const v4i *>(A2 + off);
+        for (int pl = 0; pl < PL; ++pl)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+                a[pl][i] = *reinterpret_cast<const v4i *>(
+                    abuf + pl * PLANE + ((kbl * TI + i) * 64 + lane) * 16);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], rb[S][j], acc[i][j],
+                                                                  0, 0, 0);
+                if (TWO)
+                    acc2[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[PL - 1][i], rb[S][j],
+                                                                       acc2[i][j], 0, 0, 0);
             }
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                b[j] = *reinterpret_cast<const v4i *>(B + (((wn * 2 + j) * 2 + s) * 64 + lane) * 16);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-                    if (TWO)
-                        acc2[i][j] =
-                            __builtin_amdgcn_mfma_i32_32x32x32_i8(a2[i], b[j], acc2[i][j], 0, 0, 0);
-                }
+    };
+    // One ring turn: k blocks g .. g+R-1 from LDS offsets kbl .. kbl+R-1.
+    // Blocks at or past nkb (only in the last turn of an extent that is not
+    // a whole number of turns) are skipped: their weight slot holds a repeat.
+    auto ring = [&](const uint8_t *abuf, int kbl, int g) {
+        static_assert(R == 4 || R == 8, "ring depth");
+        const int lim = nkb - g;
+#define IRO_RING_STEP(U)                                                  \
+    if ((U) < lim) mma(std::integral_constant<int, (U)>{}, abuf, kbl + (U)); \
+    load_b(std::integral_constant<int, (U)>{}, g + R + (U));
+        IRO_RING_STEP(0)
+        IRO_RING_STEP(1)
+        IRO_RING_STEP(2)
+        IRO_RING_STEP(3)
+        if constexpr (R == 8) {
+            IRO_RING_STEP(4)
+            IRO_RING_STEP(5)
+            IRO_RING_STEP(6)
+            IRO_RING_STEP(7)
         }
-        if (kt + 1 < nk) sstore(cur ^ 1);
+#undef IRO_RING_STEP
+    };
+
+    // Prologue: chunk 0 and the first R weight k blocks in flight together.
+    load_chunk(0);
+    load_b(std::integral_constant<int, 0>{}, 0);
+    load_b(std::integral_constant<int, 1>{}, 1);
+    load_b(std::integral_constant<int, 2>{}, 2);
+    load_b(std::integral_constant<int, 3>{}, 3);
+    if constexpr (R == 8) {
+        load_b(std::integral_constant<int, 4>{}, 4);
+        load_b(std::integral_constant<int, 5>{}, 5);
+        load_b(std::integral_constant<int, 6>{}, 6);
+        load_b(std::integral_constant<int, 7>{}, 7);
+    }
+    store_chunk(0);
+    __syncthreads();
+    for (int c = 0; c < nc; ++c) {
+        const uint8_t *abuf = lds_a[c & 1];
+        if (c + 1 < nc) load_chunk(c + 1);
+        // k blocks of this chunk that hold data; the ring runs whole turns
+        // (blocks past nkb multiply zero weights).
+        const int kb_end = (c + 1) * KBC < nkb ? KBC : nkb - c * KBC;
+        for (int kbl = 0; kbl < kb_end; kbl += R) ring(abuf, kbl, c * KBC + kbl);
+        if (c + 1 < nc) store_chunk((c + 1) & 1);
         __syncthreads();
     }
 
-    // ---- epilogue ----------------------------------------------------------
-    // 32x32 accumulator layout: lane L, register r holds
-    // row 8*(r/4) + 4*(L/32) + r%4, column L%32.
-    int ncol[2], cs[2], rs[2];
-    float swv[2], bv[2];
+    epilogue<CONV, EPI, TWO, TI, TJ, BM>(p, acc, acc2, cp, rl, exptab, m0, nb0, lane);
+}
+
+// M <= 32: block = 64 weight rows (two packed blocks), four waves split the
+// k blocks, int32 partials summed in LDS, wave 0 runs the epilogue.
+template <int CONV, int EPI, bool TWO>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(KParams p) {
+    constexpr int TJ = 2, PL = TWO ? 2 : 1, U = 4;
+    __shared__ int red[3][PL][TJ][16][64];
+    __shared__ __attribute__((aligned(16))) RowLds<32, TWO> rl;
+    __shared__ uint64_t exptab[32];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int nb0 = blockIdx.x * TJ;
+    stage_rows<EPI, TWO, 32>(p, rl, 0, tid);
+    if (EPI == EPI_SWIGLU && tid < 32) exptab[tid] = kExp2Tab[tid];
+
+    const int kbn = (p.K + 31) / 32;           // k blocks holding activation data
+    const int per = (kbn + 3) / 4;
+    const int kb_lo = wave * per;
+    const int kb_hi = kb_lo + per < kbn ? kb_lo + per : kbn;
+
+    int row = lane & 31;
+    row = row < p.M ? row : p.M - 1;
+    const int kk = (lane >> 5) * 16;
+    const uint8_t *pa1 = p.a1 + (size_t)row * p.lda + kk;
+    const uint8_t *pa2 = TWO ? p.a2 + (size_t)row * p.lda + kk : nullptr;
+    const int8_t *pbw = p.bp + (size_t)nb0 * p.kb_count * 1024 + lane * 16;
+    const size_t jstride = (size_t)p.kb_count * 1024;
+    const int lim = p.K - 16 - kk;
+    const v4i flip = {(int)0x80808080, (int)0x80808080, (int)0x80808080, (int)0x80808080};
+
+    v16i acc[1][TJ], acc2[1][TJ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        ncol[j] = n0 + wn * 64 + j * 32 + (lane & 31);
-        cs[j] = p.colsum[ncol[j]];  // padded to Np: always in bounds
-        rs[j] = p.rowsum[ncol[j]];
-        swv[j] = p.sw[ncol[j]];
-        bv[j] = (EPI == EPI_LINEAR && p.bias && ncol[j] < p.N) ? p.bias[ncol[j]] : 0.0f;
-    }
-    const bool has_bias = EPI == EPI_LINEAR && p.bias != nullptr;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            if (m >= p.M) continue;
-            const float sx1 = p.sx1[m];
-            const int zx1 = p.zx1[m];
-            float sx2 = 0.0f;
-            int zx2 = 0;
-            if (TWO) {
-                sx2 = p.sx2[m];
-                zx2 = p.zx2[m];
-            }
-            float yv[2];
+            acc[0][j][r] = 0;
+            acc2[0][j][r] = 0;
+        }
+    for (int kb = kb_lo; kb < kb_hi; kb += U) {
+        v4i a[U], a2[U], b[U][TJ];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int raw = acc[i][j][r] + 128 * rs[j];
-                const float t = (float)(raw - zx1 * cs[j]);
-                const float c = sx1 * swv[j];
-                float y;
-                if (EPI == EPI_LINEAR) {
-                    if (ncol[j] >= p.N) {
-                        yv[j] = 0.0f;
-                        continue;
-                    }
-                    const size_t yi = (size_t)m * p.ldy + ncol[j];
-                    const float yold = p.accumulate ? p.y[yi] : 0.0f;
-                    y = lin_out<CONV>(t, c, bv[j], has_bias, p.accumulate != 0, yold);
-                    if (p.work) p.work[(size_t)m * p.ldw + ncol[j]] = raw;
-                } else {
-                    y = t * c;
-                }
-                if (TWO) {
-                    const int raw2 = acc2[i][j][r] + 128 * rs[j];
-                    const float t2 = (float)(raw2 - zx2 * cs[j]);
-                    const float c2 = sx2 * swv[j];
-                    y = add_term<CONV>(y, t2, c2);
-                }
-                yv[j] = y;
-                if (EPI == EPI_LINEAR) {
-                    p.y[(size_t)m * p.ldy + ncol[j]] = y;
-                } else if (EPI == EPI_QKVG) {
-                    if (ncol[j] < p.N) {
-                        const int sg = ncol[j] / p.seg_n;
-                        float *dst = sg == 0 ? p.seg0 : (sg == 1 ? p.seg1 : (sg == 2 ? p.seg2 : p.seg3));
-                        dst[(size_t)m * p.seg_n + (ncol[j] - sg * p.seg_n)] = y;
-                    }
-                } else if (EPI == EPI_GATED) {
-                    if (ncol[j] < p.N) {
-                        const size_t xi = (size_t)m * p.ldx + ncol[j];
-                        const float g = p.gate[(size_t)(m / p.rows_per_branch) * p.ldg + ncol[j]];
-                        const float x = p.xres[xi];
-                        p.xres[xi] = CONV == 1 ? __builtin_fmaf(g, y, x) : x + g * y;
-                    }
-                }
-            }
-            if (EPI == EPI_SWIGLU) {
-                const int hcol = ((n0 + wn * 64) >> 6) * 32 + (lane & 31);
-                if (hcol < p.hidden_n) p.hidden[(size_t)m * p.ldh + hcol] = silu_mul(yv[0], yv[1]);
+        for (int u = 0; u < U; ++u) {
+            const int k = kb + u < kb_hi ? kb + u : kb_lo;  // repeats stay in bounds
+            int koff = k * 32;
+            koff = koff < lim ? koff : lim;
+            a[u] = *reinterpret_cast<const v4i *>(pa1 + koff);
+            if (TWO) a2[u] = *reinterpret_cast<const v4i *>(pa2 + koff);
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                b[u][j] = *reinterpret_cast<const v4i *>(pbw + j * jstride + (size_t)k * 1024);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (kb + u >= kb_hi) break;
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                acc[0][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[u] ^ flip, b[u][j], acc[0][j],
+                                                                  0, 0, 0);
+                if (TWO)
+                    acc2[0][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a2[u] ^ flip, b[u][j],
+                                                                       acc2[0][j], 0, 0, 0);
             }
         }
     }
+    if (wave > 0) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                red[wave - 1][0][j][r][lane] = acc[0][j][r];
+                if (TWO) red[wave - 1][PL - 1][j][r][lane] = acc2[0][j][r];
+            }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[0][j][r] += red[w][0][j][r][lane];
+                if (TWO) acc2[0][j][r] += red[w][PL - 1][j][r][lane];
+            }
+    const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane);
+    epilogue<CONV, EPI, TWO, 1, TJ, 32>(p, acc, acc2, cp, rl, exptab, 0, nb0, lane);
+}
+
+// ---- launch ------------------------------------------------------------------
+
+struct TileCfg {
+    int ti, tj;
+};
+
+template <int CONV, int EPI, bool TWO>
+void launch_tile(const KParams &kp, TileCfg t, unsigned grid, hipStream_t st) {
+#define IRO_TILE(TI_, TJ_)                                                                  \
+    hipLaunchKernelGGL((gemm_tile_kernel<CONV, EPI, TWO, TI_, TJ_>), dim3(grid), dim3(256), 0, \
+                       st, kp)
+    // Two planes of a 128 x 256 tile would hold 256 accumulator registers
+    // per lane and spill: that shape runs as 128 x 128.
+    if (t.ti == 2 && t.tj == 1) IRO_TILE(2, 1);
+    else if (t.ti == 2 && t.tj == 2) IRO_TILE(2, 2);
+    else if (t.ti == 4 && (t.tj == 1 || TWO)) IRO_TILE(4, 1);
+    else IRO_TILE(4, (TWO ? 1 : 2));
+#undef IRO_TILE
 }
 
 template <int CONV, int EPI>
-void launch_t(const KParams &kp, bool two, dim3 grid, hipStream_t st) {
-    if (two)
-        hipLaunchKernelGGL((gemm_i8_kernel<CONV, EPI, true>), grid, dim3(256), 0, st, kp);
-    else
-        hipLaunchKernelGGL((gemm_i8_kernel<CONV, EPI, false>), grid, dim3(256), 0, st, kp);
+void launch_e(const KParams &kp, bool two, bool skinny, TileCfg t, unsigned grid,
+              hipStream_t st) {
+    if (skinny) {
+        if (two)
+            hipLaunchKernelGGL((gemm_skinny_kernel<CONV, EPI, true>), dim3(grid), dim3(256), 0, st,
+                               kp);
+        else
+            hipLaunchKernelGGL((gemm_skinny_kernel<CONV, EPI, false>), dim3(grid), dim3(256), 0,
+                               st, kp);
+    } else if (two) {
+        launch_tile<CONV, EPI, true>(kp, t, grid, st);
+    } else {
+        launch_tile<CONV, EPI, false>(kp, t, grid, st);
+    }
 }
 
 template <int CONV>
-void launch_c(const KParams &kp, Epi epi, bool two, dim3 grid, hipStream_t st) {
+void launch_c(const KParams &kp, Epi epi, bool two, bool skinny, TileCfg t, unsigned grid,
+              hipStream_t st) {
     switch (epi) {
-        case EPI_LINEAR: launch_t<CONV, EPI_LINEAR>(kp, two, grid, st); break;
-        case EPI_QKVG: launch_t<CONV, EPI_QKVG>(kp, two, grid, st); break;
-        case EPI_SWIGLU: launch_t<CONV, EPI_SWIGLU>(kp, two, grid, st); break;
-        case EPI_GATED: launch_t<CONV, EPI_GATED>(kp, two, grid, st); break;
+        case EPI_LINEAR: launch_e<CONV, EPI_LINEAR>(kp, two, skinny, t, grid, st); break;
+        case EPI_QKVG: launch_e<CONV, EPI_QKVG>(kp, two, skinny, t, grid, st); break;
+        case EPI_SWIGLU: launch_e<CONV, EPI_SWIGLU>(kp, two, skinny, t, grid, st); break;
+        case EPI_GATED: launch_e<CONV, EPI_GATED>(kp, two, skinny, t, grid, st); break;
     }
+}
+
+// Tile choice (measured on MI355X at the DiT shapes): 64-row tiles keep
+// two blocks resident per CU; 256 columns per block halve the activation
+// re-reads of 128, so they win whenever they still give every CU a tile.
+// The SwiGLU epilogue needs an even number of 32-column blocks per wave.
+TileCfg choose_tile(int M, int Np, int cus, bool two, Epi epi, int forced) {
+    if (forced) {
+        TileCfg t{forced / 10, forced % 10};
+        if (epi == EPI_SWIGLU && t.tj % 2) t.tj = 2;
+        if (two && t.ti * t.tj > 4) t.tj = 1;
+        if (epi == EPI_SWIGLU && two && t.ti * t.tj > 4) t.ti = 2;
+        return t;
+    }
+    if (epi == EPI_SWIGLU || two) return TileCfg{2, 2};
+    const long long tiles22 = (long long)((M + 63) / 64) * (Np / 256);
+    return tiles22 >= cus ? TileCfg{2, 2} : TileCfg{2, 1};
 }
 
 }  // namespace
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi) {
     if (a.M <= 0) return 0;
-    if (a.K <= 0 || a.K % 16 || a.K > w->Kp || a.lda % 16 || (((uintptr_t)a.a1) & 15) ||
-        (a.a2 && (((uintptr_t)a.a2) & 15)) || w->Np % BN)
+    if (a.K <= 0 || a.K % 16 || a.K > w->Kp || a.K < w->K || a.lda < a.K || a.lda % 16 ||
+        (((uintptr_t)a.a1) & 15) || (a.a2 && (((uintptr_t)a.a2) & 15)) || w->Np % 256)
         return set_error(ctx, "gemm: unsupported operand shape (K=%d lda=%d Kp=%d Np=%d)", a.K,
                          a.lda, w->Kp, w->Np);
     if (epi == EPI_SWIGLU && (w->layout != 1 || w->part_N[0] % 32))
         return set_error(ctx, "gemm: SwiGLU epilogue needs an interleaved W1/W3 weight");
+    if (epi != EPI_SWIGLU && w->layout != 0)
+        return set_error(ctx, "gemm: an interleaved weight needs the SwiGLU epilogue");
     if (epi == EPI_QKVG && (a.seg_n <= 0 || w->N > 4 * a.seg_n))
         return set_error(ctx, "gemm: QKVG epilogue needs N <= 4 * segment width");
     KParams kp;
@@ -375,13 +688,29 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     kp.ldg = a.ldg > 0 ? a.ldg : a.ldx;
     kp.ldx = a.ldx;
     kp.rows_per_branch = a.rows_per_branch > 0 ? a.rows_per_branch : 1;
-    const dim3 grid(w->Np / BN, (a.M + BM - 1) / BM);
     const bool two = a.a2 != nullptr;
+    const bool skinny = a.M <= 32;
+    TileCfg t{0, 0};
+    unsigned grid;
+    if (skinny) {
+        grid = (unsigned)(w->Np / 64);
+        kp.tiles_n = grid;
+        kp.tiles_m = 1;
+        kp.tiles_per_xcd = 0;
+    } else {
+        t = choose_tile(a.M, w->Np, ctx->cus > 0 ? ctx->cus : 256, two, epi, ctx->gemm_tile);
+        if (two && t.ti * t.tj > 4) t.tj = 1;  // as launch_tile runs it
+        kp.tiles_n = w->Np / (128 * t.tj);
+        kp.tiles_m = (a.M + 32 * t.ti - 1) / (32 * t.ti);
+        const int tiles = kp.tiles_n * kp.tiles_m;
+        kp.tiles_per_xcd = (tiles + 7) / 8;
+        grid = (unsigned)(8 * kp.tiles_per_xcd);
+    }
     prof_begin(ctx);
     if (ctx->convention == IRO_HIP_GCC_FASTMATH)
-        launch_c<1>(kp, epi, two, grid, ctx->stream);
+        launch_c<1>(kp, epi, two, skinny, t, grid, ctx->stream);
     else
-        launch_c<0>(kp, epi, two, grid, ctx->stream);
+        launch_c<0>(kp, epi, two, skinny, t, grid, ctx->stream);
     IRO_HIP_CHECK_LAUNCH(ctx);
     // Algorithmic work: 2*M*N*K per plane; bytes = codes + weights + outputs.
     const double M = a.M, N = w->N, K = w->K, planes = two ? 2 : 1;

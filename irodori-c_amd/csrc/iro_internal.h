@@ -41,7 +41,10 @@ struct IroHipContext {
     int has_err = 0;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    unsigned ws_epoch = 0;  // bumped whenever ws is reallocated
     char backend[256] = {0};
+    int cus = 0;        // compute units of the device
+    int gemm_tile = 0;  // 0: tile shape chosen per GEMM; else 10*TI + TJ
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
 };
 
@@ -123,6 +126,12 @@ int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long l
 int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const int32_t *colsum,
                 const int32_t *rowsum, IroHipWeight *w);
 int launch_fill(IroHipContext *ctx, void *dst, int value, size_t bytes);
+
+// A zeroed layout-0 weight of N x K, and a copy of a whole layout-0 weight
+// into its rows row0 .. row0 + src->Np (row0 a multiple of 32): several
+// weights that share one activation become one GEMM.
+int weight_rows_alloc(IroHipContext *ctx, int N, int K, IroHipWeight **out);
+int weight_rows_copy(IroHipContext *ctx, IroHipWeight *dst, int row0, const IroHipWeight *src);
 
 enum Epi { EPI_LINEAR = 0, EPI_QKVG = 1, EPI_SWIGLU = 2, EPI_GATED = 3 };
 

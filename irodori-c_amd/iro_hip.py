@@ -52,11 +52,13 @@ def load() -> C.CDLL:
         "iro_hip_clear_error": ([_vp], None),
         "iro_hip_sync": ([_vp], _i),
         "iro_hip_stream": ([_vp], _vp),
+        "iro_hip_set_gemm_tile": ([_vp, _i, _i], _i),
         "iro_hip_alloc": ([_vp, C.c_size_t, C.POINTER(_vp)], _i),
         "iro_hip_free": ([_vp, _vp], _i),
         "iro_hip_upload": ([_vp, _vp, _vp, C.c_size_t], _i),
         "iro_hip_download": ([_vp, _vp, _vp, C.c_size_t], _i),
         "iro_hip_fill": ([_vp, _vp, _i, C.c_size_t], _i),
+        "iro_hip_copy": ([_vp, _vp, _vp, C.c_size_t], _i),
         "iro_hip_event_create": ([C.POINTER(_vp)], _i),
         "iro_hip_event_destroy": ([_vp], None),
         "iro_hip_event_record": ([_vp, _vp], _i),
@@ -87,6 +89,7 @@ def load() -> C.CDLL:
         "iro_hip_dit_stack_bytes": ([_vp], C.c_size_t),
         "iro_hip_dit_stack_buffers": ([_vp] + [C.POINTER(_vp)] * 6, _i),
         "iro_hip_dit_stack_destroy": ([_vp], None),
+        "iro_hip_dit_stack_use_graph": ([_vp, _i], _i),
         "iro_hip_profile_enable": ([_vp, _i], _i),
         "iro_hip_profile_reset": ([_vp], _i),
         "iro_hip_profile_kinds": ([], _i),
@@ -237,6 +240,9 @@ class Context:
     def sync(self):
         self._check(self.lib.iro_hip_sync(self.h), "sync")
 
+    def set_gemm_tile(self, ti: int, tj: int):
+        self._check(self.lib.iro_hip_set_gemm_tile(self.h, ti, tj), "set_gemm_tile")
+
     def backend(self) -> str:
         return self.lib.iro_hip_backend_name(self.h).decode()
 
@@ -249,6 +255,11 @@ class Context:
 
     def fill(self, arr: DeviceArray, value: int = 0):
         self._check(self.lib.iro_hip_fill(self.h, arr.vp, value, arr.nbytes), "fill")
+
+    def copy(self, dst: DeviceArray, src: DeviceArray):
+        if dst.nbytes != src.nbytes:
+            raise ValueError("copy: size mismatch")
+        self._check(self.lib.iro_hip_copy(self.h, dst.vp, src.vp, src.nbytes), "copy")
 
     def selfcheck(self) -> int:
         return self.lib.iro_hip_selfcheck(self.h)
@@ -393,6 +404,10 @@ class DiTStack:
     def step(self, x: DeviceArray, cond: DeviceArray, B: int, S: int):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_step(self.h, x.vp, cond.vp, B, S),
                         "dit_stack_step")
+
+    def use_graph(self, on: bool):
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_use_graph(self.h, int(bool(on))),
+                        "dit_stack_use_graph")
 
     def nbytes(self):
         return self.ctx.lib.iro_hip_dit_stack_bytes(self.h)

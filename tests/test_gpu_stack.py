@@ -45,3 +45,35 @@ def test_stack_step_matches_reference_sequence(ctx, oracle, blocks, B, S, D, H, 
                       D, H, rm)
     bad = int((got.view(np.int32) != want.view(np.int32)).sum())
     assert bad == 0, f"{bad} of {got.size} elements of x differ"
+
+
+def test_stack_graph_replays_match_direct_steps(ctx):
+    """The step replayed from its HIP graph equals the directly launched step
+    on every replay, with other eager work and synchronizations between the
+    replays."""
+    D, H, B, S, blocks = 256, 320, 2, 40, 2
+    ws = _weights(D, H, blocks, 910)
+    x0 = gauss(911, (B * S, D))
+    cond = ctx.to_device(gauss(912, (B, D), 0.1))
+    stack = iro_hip.DiTStack(ctx, blocks, D, H, 8)
+    try:
+        for b in range(blocks):
+            stack.set_block(b, *[ctx.to_device(w) for w in ws[b]])
+        x_init = ctx.to_device(x0)
+        x = ctx.to_device(x0)
+        stack.use_graph(False)
+        stack.step(x, cond, B, S)
+        want = x.numpy()
+        stack.use_graph(True)
+        other = ctx.to_device(gauss(913, (64, D)))
+        q = ctx.empty((64, D), np.uint8)
+        s_, z_ = ctx.empty(64, np.float32), ctx.empty(64, np.int32)
+        for i in range(5):  # direct, capture, then three replays
+            ctx.copy(x, x_init)
+            stack.step(x, cond, B, S)
+            got = x.numpy()
+            assert np.array_equal(got.view(np.int32), want.view(np.int32)), f"step {i} differs"
+            ctx.quantize_rows(other, q, s_, z_)
+            ctx.sync()
+    finally:
+        stack.destroy()
