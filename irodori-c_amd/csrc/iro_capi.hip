@@ -290,7 +290,8 @@ int iro_hip_create(int device, int convention, IroHipContext **out) {
                  prop.multiProcessorCount);
     } else
         snprintf(ctx->backend, sizeof(ctx->backend), "gfx950 MFMA i8");
-    if (iro_hip_selfcheck(ctx) != 0) {
+    if (hipMalloc(&ctx->zero16, 256) != hipSuccess || launch_fill(ctx, ctx->zero16, 0, 256) ||
+        iro_hip_selfcheck(ctx) != 0) {
         iro_hip_destroy(ctx);
         return -1;
     }
@@ -305,6 +306,7 @@ void iro_hip_destroy(IroHipContext *ctx) {
     prof_free(ctx->prof);
     ctx->prof = nullptr;
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->zero16) (void)hipFree(ctx->zero16);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -329,6 +331,21 @@ void *iro_hip_stream(IroHipContext *ctx) { return ctx ? (void *)ctx->stream : nu
 
 int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
     if (!ctx) return -1;
+    if (ti == -1) {  // tj selects the tile order: -1 per GEMM, 0 columns, 1 rows
+        if (tj < -1 || tj > 1) return set_error(ctx, "set_gemm_tile: unknown tile order");
+        ctx->tile_order = tj;
+        return 0;
+    }
+    if (ti == -2) {  // tj: weight ring depth of the whole-tile kernel, 0 default, 4 or 8
+        if (tj != 0 && tj != 4 && tj != 8) return set_error(ctx, "set_gemm_tile: ring 0, 4 or 8");
+        ctx->gemm_ring = tj;
+        return 0;
+    }
+    if (ti == -3) {  // tj: column slabs per whole-tile block, 0 chosen per GEMM
+        if (tj < 0 || tj > 64) return set_error(ctx, "set_gemm_tile: slabs per block 0..64");
+        ctx->gemm_spb = tj;
+        return 0;
+    }
     if (ti == 0 && tj == 0) {
         ctx->gemm_tile = 0;
         return 0;

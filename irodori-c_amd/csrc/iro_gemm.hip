@@ -81,6 +81,10 @@ struct KParams {
     int rows_per_branch;
     int tiles_n, tiles_m;  // tiles of the tile kernel along N and M
     int tiles_per_xcd;     // ceil(tiles / 8)
+    int row_major;         // tile order, see tile_of
+    int aflip;             // XOR applied to stored codes: 0x80808080 for u8 codes, 0 if signed
+    int spb, groups_n;     // whole-tile kernel: column slabs per block, slab groups per row
+    const uint8_t *zero16; // 256 zero bytes
 };
 
 // ops.c:468-490: y = t*c [+ b] or y += t*c [+ b] with the build's rounding.
@@ -197,31 +201,44 @@ __device__ __forceinline__ ColParams<TJ> load_cols(const KParams &p, int nb0, in
 
 // Epilogue of one wave's TI x TJ accumulator tiles.  32x32 accumulator
 // layout: lane L, register r holds row 8*(r/4) + 4*(L/32) + r%4 and column
-// L%32 of the tile.  Loads use clamped rows so they can be issued together;
-// only stores are predicated on m < M.
-template <int CONV, int EPI, bool TWO, int TI, int TJ, int BM>
-__device__ __forceinline__ void epilogue(const KParams &p, const v16i (&acc)[TI][TJ],
-                                         const v16i (&acc2)[TI][TJ], const ColParams<TJ> &cp,
-                                         const RowLds<BM, TWO> &rl, const uint64_t *exptab,
-                                         int m0, int nb0, int lane) {
+// L%32 of the tile.  Row (m0 + i*32 + 8*g + e) is wave-uniform, so every
+// store address is a scalar row base plus one per-lane offset fixed per
+// column block.  FULL tiles (all rows < M, all columns < N) store without
+// predicates; the others clamp their loads to row M-1 and predicate stores.
+template <int CONV, int EPI, bool TWO, int TI, int TJ, int BM, bool FULL, bool RAW>
+__device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc)[TI][TJ],
+                                              const v16i (&acc2)[TI][TJ],
+                                              const ColParams<TJ> &cp, const RowLds<BM, TWO> &rl,
+                                              const uint64_t *exptab, int m0, int nb0, int lane) {
     const bool has_bias = EPI == EPI_LINEAR && p.bias != nullptr;
     const int half = lane >> 5;
-    // QKVG: destination segment of each column block.
+    int pc[TJ], c128[TJ];
+    unsigned off[TJ];  // element offset of (row m0-relative half*4, column) from a row base
     float *segp[TJ];
-    int segc[TJ];
-    if (EPI == EPI_QKVG) {
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int pc = (nb0 + j) * 32 + (lane & 31);
-            const int sg = pc / p.seg_n;
+    for (int j = 0; j < TJ; ++j) {
+        pc[j] = (nb0 + j) * 32 + (lane & 31);
+        c128[j] = RAW ? 0 : 128 * cp.rs[j];
+        if (EPI == EPI_QKVG) {
+            const int sg = pc[j] / p.seg_n;
             segp[j] = sg == 0 ? p.seg0 : (sg == 1 ? p.seg1 : (sg == 2 ? p.seg2 : p.seg3));
-            segc[j] = pc - sg * p.seg_n;
+            segp[j] += pc[j] - sg * p.seg_n + (size_t)half * 4 * p.seg_n;
+        } else if (EPI == EPI_LINEAR) {
+            off[j] = (unsigned)(half * 4 * p.ldy + pc[j]);
+        } else if (EPI == EPI_GATED) {
+            off[j] = (unsigned)(half * 4 * p.ldx + pc[j]);
         }
+    }
+    unsigned offh[TJ / 2 > 0 ? TJ / 2 : 1];
+    if (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int j = 0; j + 1 < TJ; j += 2)
+            offh[j / 2] = (unsigned)(half * 4 * p.ldh + ((nb0 + j) >> 1) * 32 + (lane & 31));
     }
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         float sx[16], sx2[16];
-        int zx[16], zx2[16], mrow[16], mcl[16], goff[16];
+        int zx[16], zx2[16], goff[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int rb = i * 32 + g * 8 + half * 4;
@@ -239,34 +256,39 @@ __device__ __forceinline__ void epilogue(const KParams &p, const v16i (&acc)[TI]
                 const int4 o4 = *reinterpret_cast<const int4 *>(&rl.goff[rb]);
                 goff[g * 4 + 0] = o4.x; goff[g * 4 + 1] = o4.y; goff[g * 4 + 2] = o4.z; goff[g * 4 + 3] = o4.w;
             }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int m = m0 + rb + e;
-                mrow[g * 4 + e] = m;
-                mcl[g * 4 + e] = m < p.M ? m : p.M - 1;
-            }
         }
+        // Row of register r is rowu(r) + half*4; rowu is wave-uniform.
+        auto rowu = [&](int r) { return m0 + i * 32 + (r >> 2) * 8 + (r & 3); };
+        auto row_ok = [&](int r) { return FULL || rowu(r) + half * 4 < p.M; };
+        // Uniform row base used for loads: in partial tiles it is pulled back
+        // so the lane's row base + half*4 is at most M-1 (it may be negative
+        // when M < 5; base + per-lane offset is then still a valid row).
+        auto row_ld = [&](int r) {
+            int m = rowu(r);
+            if (!FULL) m = m + half * 4 < p.M ? m : p.M - 1 - half * 4;
+            return m;
+        };
         float yv[TJ][16];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const int pc = (nb0 + j) * 32 + (lane & 31);
+            const bool col_ok = FULL || pc[j] < p.N;
             float old[16], gv[16];
             if (EPI == EPI_LINEAR && p.accumulate) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    old[r] = pc < p.N ? p.y[(size_t)mcl[r] * p.ldy + pc] : 0.0f;
+                    old[r] = col_ok ? p.y[(long long)row_ld(r) * p.ldy + off[j]] : 0.0f;
             }
             if (EPI == EPI_GATED) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    old[r] = pc < p.N ? p.xres[(size_t)mcl[r] * p.ldx + pc] : 0.0f;
-                    gv[r] = pc < p.N ? p.gate[goff[r] + pc] : 0.0f;
+                    old[r] = col_ok ? p.xres[(long long)row_ld(r) * p.ldx + off[j]] : 0.0f;
+                    gv[r] = col_ok ? p.gate[goff[r] + pc[j]] : 0.0f;
                 }
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int raw = acc[i][j][r] + 128 * cp.rs[j];
-                const float t = (float)(raw - zx[r] * cp.cs[j]);
+                const int raw = acc[i][j][r] + c128[j];
+                const float t = (float)(raw - __mul24(zx[r], cp.cs[j]));
                 const float c = sx[r] * cp.sw[j];
                 float y;
                 if (EPI == EPI_LINEAR)
@@ -275,23 +297,24 @@ __device__ __forceinline__ void epilogue(const KParams &p, const v16i (&acc)[TI]
                 else
                     y = t * c;
                 if (TWO) {
-                    const int raw2 = acc2[i][j][r] + 128 * cp.rs[j];
-                    const float t2 = (float)(raw2 - zx2[r] * cp.cs[j]);
+                    const int raw2 = acc2[i][j][r] + c128[j];
+                    const float t2 = (float)(raw2 - __mul24(zx2[r], cp.cs[j]));
                     const float c2 = sx2[r] * cp.sw[j];
                     y = add_term<CONV>(y, t2, c2);
                 }
                 yv[j][r] = y;
-                const bool ok = mrow[r] < p.M && pc < p.N;
+                const bool ok = row_ok(r) && col_ok;
+                const size_t ru = (size_t)rowu(r);
                 if (EPI == EPI_LINEAR) {
                     if (ok) {
-                        p.y[(size_t)mrow[r] * p.ldy + pc] = y;
-                        if (p.work) p.work[(size_t)mrow[r] * p.ldw + pc] = raw;
+                        p.y[ru * p.ldy + off[j]] = y;
+                        if (p.work) p.work[(ru + half * 4) * p.ldw + pc[j]] = raw;
                     }
                 } else if (EPI == EPI_QKVG) {
-                    if (ok) segp[j][(size_t)mrow[r] * p.seg_n + segc[j]] = y;
+                    if (ok) segp[j][ru * p.seg_n] = y;
                 } else if (EPI == EPI_GATED) {
                     if (ok)
-                        p.xres[(size_t)mrow[r] * p.ldx + pc] =
+                        p.xres[ru * p.ldx + off[j]] =
                             CONV == 1 ? __builtin_fmaf(gv[r], y, old[r]) : old[r] + gv[r] * y;
                 }
             }
@@ -301,29 +324,49 @@ __device__ __forceinline__ void epilogue(const KParams &p, const v16i (&acc)[TI]
             // (nb0+j)/2, block nb0+j+1 the matching W3 block.
 #pragma unroll
             for (int j = 0; j + 1 < TJ; j += 2) {
-                const int hcol = ((nb0 + j) >> 1) * 32 + (lane & 31);
+                const bool hok = FULL || ((nb0 + j) >> 1) * 32 + (lane & 31) < p.hidden_n;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    if (mrow[r] < p.M && hcol < p.hidden_n)
-                        p.hidden[(size_t)mrow[r] * p.ldh + hcol] =
-                            silu_mul(yv[j][r], yv[j + 1][r], exptab);
+                    const float h = silu_mul(yv[j][r], yv[j + 1][r], exptab);
+                    if (row_ok(r) && hok) p.hidden[(size_t)rowu(r) * p.ldh + offh[j / 2]] = h;
                 }
             }
         }
     }
 }
 
+template <int CONV, int EPI, bool TWO, int TI, int TJ, int BM, bool RAW = false>
+__device__ __forceinline__ void epilogue(const KParams &p, const v16i (&acc)[TI][TJ],
+                                         const v16i (&acc2)[TI][TJ], const ColParams<TJ> &cp,
+                                         const RowLds<BM, TWO> &rl, const uint64_t *exptab,
+                                         int m0, int nb0, int lane) {
+    const int ncols = EPI == EPI_SWIGLU ? 2 * p.hidden_n : p.N;
+    if (m0 + BM <= p.M && (nb0 + TJ) * 32 <= ncols)
+        epilogue_body<CONV, EPI, TWO, TI, TJ, BM, true, RAW>(p, acc, acc2, cp, rl, exptab, m0,
+                                                             nb0, lane);
+    else
+        epilogue_body<CONV, EPI, TWO, TI, TJ, BM, false, RAW>(p, acc, acc2, cp, rl, exptab, m0,
+                                                              nb0, lane);
+}
+
 // Tile -> (column slab, row tile).  Workgroups are dealt to the eight XCDs
 // round-robin (workgroup w runs on XCD w % 8), so workgroup w takes tile
-// (w % 8) * per + w / 8 of the column-slab-major order: each XCD works
-// through a contiguous run of tiles, i.e. a few weight column slabs, which
-// then stay in that XCD's L2 while every row tile passes over them.
-__device__ __forceinline__ bool tile_of(int w, int tiles_m, int tiles_n, int per, int &bx,
-                                        int &by) {
+// (w % 8) * per + w / 8 of a fixed order: each XCD works through one
+// contiguous run of it.  Column-slab-major order (row_major = 0) gives each
+// XCD a few weight slabs that stay in its L2 while all row tiles pass; it
+// suits GEMMs whose weight outweighs the activation.  Row-tile-major order
+// gives each XCD a band of activation rows read once, against all slabs.
+__device__ __forceinline__ bool tile_of(int w, int tiles_m, int tiles_n, int per, int row_major,
+                                        int &bx, int &by) {
     const int t = (w & 7) * per + (w >> 3);
     if (t >= tiles_m * tiles_n) return false;
-    bx = t / tiles_m;
-    by = t - bx * tiles_m;
+    if (row_major) {
+        by = t / tiles_n;
+        bx = t - by * tiles_n;
+    } else {
+        bx = t / tiles_m;
+        by = t - bx * tiles_m;
+    }
     return true;
 }
 
@@ -341,13 +384,13 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(KParams p) {
     constexpr int KBC = KC / 32;                        // k blocks per chunk
     constexpr int PLANE = BM * KC;                      // LDS bytes per plane per chunk
     constexpr int R = 8 / TJ <= KBC ? 8 / TJ : KBC;     // weight ring depth in k blocks
-    static_assert(KC % 32 == 0 && KBC % R == 0, "chunk must hold whole rings");
+    static_assert(KC % 32 == 0 && KBC % R == 0 && R % 2 == 0 && KBC >= 2, "chunk must hold whole rings");
     __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][PL * PLANE];
     __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
     __shared__ uint64_t exptab[32];
 
     int bx, by;
-    if (!tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.tiles_per_xcd, bx, by)) return;
+    if (!tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.tiles_per_xcd, p.row_major, bx, by)) return;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -393,96 +436,219 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(KParams p) {
 
     v4i ra[CP];
     v4i rb[R][TJ];
-    const v4i flip = {(int)0x80808080, (int)0x80808080, (int)0x80808080, (int)0x80808080};
+    const v4i flip = {p.aflip, p.aflip, p.aflip, p.aflip};
+    const v4i zero4 = {0, 0, 0, 0};
 
     auto load_chunk = [&](int c) {
 #pragma unroll
         for (int i = 0; i < CP; ++i) {
             int k = c * KC + kof[i];
-            k = k < p.K - 16 ? k : p.K - 16;  // past the extent: any bytes, W is zero there
+            k = k < p.K - 16 ? k : p.K - 16;  // past the extent: any in-bounds bytes
             ra[i] = *reinterpret_cast<const v4i *>(pa[i] + k);
         }
     };
-    auto store_chunk = [&](int buf) {
+    // Codes enter LDS as a - 128; bytes at k >= K enter as 0, so every MFMA
+    // of a chunk can run unconditionally (zero times any weight is zero).
+    auto store_chunk = [&](int buf, int c) {
 #pragma unroll
         for (int i = 0; i < CP; ++i)
-            *reinterpret_cast<v4i *>(&lds_a[buf][(tid + 256 * i) * 16]) = ra[i] ^ flip;
+            *reinterpret_cast<v4i *>(&lds_a[buf][(tid + 256 * i) * 16]) =
+                c * KC + kof[i] < p.K ? (ra[i] ^ flip) : zero4;
     };
-    auto load_b = [&](auto slot, int kb) {
-        constexpr int S = decltype(slot)::value;
-        kb = kb < nkb ? kb : nkb - 1;  // past the end: a harmless repeat
+    auto load_b = [&](int slot_unused, v4i (&dst)[TJ], int kb) {
+        (void)slot_unused;
+        kb = kb < nkb ? kb : nkb - 1;  // past the end: a repeat, multiplied by zero codes
 #pragma unroll
         for (int j = 0; j < TJ; ++j)
-            rb[S][j] = *reinterpret_cast<const v4i *>(pbw + j * jstride + (size_t)kb * 1024);
+            dst[j] = *reinterpret_cast<const v4i *>(pbw + j * jstride + (size_t)kb * 1024);
     };
-    auto mma = [&](auto slot, const uint8_t *abuf, int kbl) {
-        constexpr int S = decltype(slot)::value;
-        v4i a[PL][TI];
+    auto read_a = [&](v4i (&a)[PL][TI], const uint8_t *abuf, int kbl) {
 #pragma unroll
         for (int pl = 0; pl < PL; ++pl)
 #pragma unroll
             for (int i = 0; i < TI; ++i)
                 a[pl][i] = *reinterpret_cast<const v4i *>(
                     abuf + pl * PLANE + ((kbl * TI + i) * 64 + lane) * 16);
+    };
+    auto mma = [&](const v4i (&a)[PL][TI], const v4i (&b)[TJ]) {
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], rb[S][j], acc[i][j],
-                                                                  0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], b[j], acc[i][j], 0, 0, 0);
                 if (TWO)
-                    acc2[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[PL - 1][i], rb[S][j],
+                    acc2[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[PL - 1][i], b[j],
                                                                        acc2[i][j], 0, 0, 0);
             }
-    };
-    // One ring turn: k blocks g .. g+R-1 from LDS offsets kbl .. kbl+R-1.
-    // Blocks at or past nkb (only in the last turn of an extent that is not
-    // a whole number of turns) are skipped: their weight slot holds a repeat.
-    auto ring = [&](const uint8_t *abuf, int kbl, int g) {
-        static_assert(R == 4 || R == 8, "ring depth");
-        const int lim = nkb - g;
-#define IRO_RING_STEP(U)                                                  \
-    if ((U) < lim) mma(std::integral_constant<int, (U)>{}, abuf, kbl + (U)); \
-    load_b(std::integral_constant<int, (U)>{}, g + R + (U));
-        IRO_RING_STEP(0)
-        IRO_RING_STEP(1)
-        IRO_RING_STEP(2)
-        IRO_RING_STEP(3)
-        if constexpr (R == 8) {
-            IRO_RING_STEP(4)
-            IRO_RING_STEP(5)
-            IRO_RING_STEP(6)
-            IRO_RING_STEP(7)
-        }
-#undef IRO_RING_STEP
     };
 
     // Prologue: chunk 0 and the first R weight k blocks in flight together.
     load_chunk(0);
-    load_b(std::integral_constant<int, 0>{}, 0);
-    load_b(std::integral_constant<int, 1>{}, 1);
-    load_b(std::integral_constant<int, 2>{}, 2);
-    load_b(std::integral_constant<int, 3>{}, 3);
-    if constexpr (R == 8) {
-        load_b(std::integral_constant<int, 4>{}, 4);
-        load_b(std::integral_constant<int, 5>{}, 5);
-        load_b(std::integral_constant<int, 6>{}, 6);
-        load_b(std::integral_constant<int, 7>{}, 7);
-    }
-    store_chunk(0);
+#pragma unroll
+    for (int u = 0; u < R; ++u) load_b(u, rb[u], u);
+    store_chunk(0, 0);
     __syncthreads();
+    // Each chunk is one straight run of KBC k steps (fully unrolled, no
+    // branches): step u reads the activation fragments of step u+1 from
+    // LDS, issues its MFMAs on slot u % R, and refills that slot with the
+    // weights of step u + R.  The next chunk's activation loads go out after
+    // the first ring turn: loads complete in issue order, so weight
+    // fragments issued after them are consumed a full turn later.  In the
+    // last chunk they reload in-bounds bytes into the idle buffer.
     for (int c = 0; c < nc; ++c) {
         const uint8_t *abuf = lds_a[c & 1];
-        if (c + 1 < nc) load_chunk(c + 1);
-        // k blocks of this chunk that hold data; the ring runs whole turns
-        // (blocks past nkb multiply zero weights).
-        const int kb_end = (c + 1) * KBC < nkb ? KBC : nkb - c * KBC;
-        for (int kbl = 0; kbl < kb_end; kbl += R) ring(abuf, kbl, c * KBC + kbl);
-        if (c + 1 < nc) store_chunk((c + 1) & 1);
+        const int g0 = c * KBC;
+        v4i a0[PL][TI], a1[PL][TI];
+        read_a(a0, abuf, 0);
+#pragma unroll
+        for (int u = 0; u < KBC; u += 2) {
+            // sched_barrier keeps each step's loads where they are written:
+            // the scheduler would otherwise sink them below later MFMAs and
+            // drain the ring.
+            read_a(a1, abuf, u + 1);
+            mma(a0, rb[u % R]);
+            load_b(u % R, rb[u % R], g0 + u + R);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + 2 < KBC) read_a(a0, abuf, u + 2);
+            mma(a1, rb[(u + 1) % R]);
+            load_b((u + 1) % R, rb[(u + 1) % R], g0 + u + 1 + R);
+            if (u + 2 == R) load_chunk(c + 1 < nc ? c + 1 : c);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        store_chunk((c + 1) & 1, c + 1);
         __syncthreads();
     }
 
     epilogue<CONV, EPI, TWO, TI, TJ, BM>(p, acc, acc2, cp, rl, exptab, m0, nb0, lane);
+}
+
+// Whole-tile kernel (one activation plane, K <= 1024, codes stored signed):
+// the block's entire 64-row activation tile, 64 x K bytes, is copied into
+// LDS once by direct global-to-LDS loads (global_load_lds_dwordx4: lane L
+// of a wave writes 16 bytes at the wave's LDS base + 16 L, which is the
+// fragment order), so it needs no staging registers and one barrier.  The
+// block then sweeps `spb` consecutive weight column slabs against that
+// stationary tile.  The main loop has no barriers: each wave streams its
+// weight fragments through an R-deep register ring, and the stream runs on
+// across slabs, so the next slab's first R k blocks are in flight while
+// this slab's epilogue runs.  k past K is copied from a zero page.  The
+// accumulators start at 128 * rowsum[n] (the signed-operand correction), so
+// they end as the reference's raw u8 x s8 sums.
+template <int CONV, int EPI, int TJ, int R>
+__global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
+    constexpr int TI = 2, BM = 64, KMAX = 1024;
+    // Sweeping several slabs pays for the projections with the largest N
+    // (QKVG, W1/W3); the others run one slab per block, which keeps their
+    // epilogues' registers out of a loop.
+    constexpr bool MULTI = EPI == EPI_QKVG || EPI == EPI_SWIGLU;
+    __shared__ __attribute__((aligned(16))) uint8_t lds_a[BM * KMAX];
+    __shared__ __attribute__((aligned(16))) RowLds<BM, false> rl;
+    __shared__ uint64_t exptab[32];
+
+    // Work item = (row tile, group of spb slabs), row-tile-major.
+    int gx, by;
+    if (!tile_of(blockIdx.x, p.tiles_m, p.groups_n, p.tiles_per_xcd, 1, gx, by)) return;
+    const int bx0 = gx * p.spb;
+    const int nslab = !MULTI ? 1 : (p.tiles_n - bx0 < p.spb ? p.tiles_n - bx0 : p.spb);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int m0 = by * BM;
+
+    stage_rows<EPI, false, BM>(p, rl, m0, tid);
+    if (EPI == EPI_SWIGLU && tid < 32) exptab[tid] = kExp2Tab[tid];
+
+    const int nkb = (p.K + 31) / 32;             // k blocks holding activation data
+    const int nkr = (nkb + R - 1) / R * R;       // whole ring turns (<= KMAX / 32)
+    // Piece q = tid + 256 i of the tile: fragment f = q / 64 = (k block,
+    // row block) = (f / 2, f % 2), lane q % 64.  For this thread the row is
+    // fixed and k advances by 64 per piece.
+    {
+        int row = m0 + (wave & 1) * 32 + (lane & 31);
+        row = row < p.M ? row : p.M - 1;
+        const uint8_t *arow = p.a1 + (size_t)row * p.lda;
+        const int k0 = (wave >> 1) * 32 + (lane >> 5) * 16;
+        const int pieces = nkr / 2;
+        for (int i = 0; i < pieces; ++i) {
+            const int k = k0 + 64 * i;
+            const uint8_t *src = k < p.K ? arow + k : p.zero16;
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)src,
+                (__attribute__((address_space(3))) void *)(lds_a + (size_t)(tid - lane + 256 * i) * 16),
+                16, 0, 0);
+        }
+    }
+    const size_t jstride = (size_t)p.kb_count * 1024;
+    const size_t slab_stride = (size_t)4 * TJ * jstride;  // bytes between column slabs
+    const int8_t *pb0 = p.bp + (size_t)(bx0 * 4 * TJ + wave * TJ) * jstride + lane * 16;
+
+    v16i acc[TI][TJ], acc2[TI][TJ];
+    v4i rb[R][TJ];
+    // Weight stream: k block kk of the current slab, or, for kk >= nkr, k
+    // block kk - nkr of the next slab (the last slab repeats itself); k
+    // blocks are clamped to nkb - 1 (repeats meet zero codes or are never
+    // consumed).
+    auto load_b = [&](v4i (&dst)[TJ], const int8_t *cur, const int8_t *nxt, int kk) {
+        const bool next = kk >= nkr;
+        int kb = next ? kk - nkr : kk;
+        kb = kb < nkb ? kb : nkb - 1;
+        const int8_t *src = (next ? nxt : cur) + (size_t)kb * 1024;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) dst[j] = *reinterpret_cast<const v4i *>(src + j * jstride);
+    };
+    auto read_a = [&](v4i (&a)[TI], int kb) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+            a[i] = *reinterpret_cast<const v4i *>(lds_a + ((kb * TI + i) * 64 + lane) * 16);
+    };
+    auto mma = [&](const v4i (&a)[TI], const v4i (&b)[TJ]) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    };
+
+#pragma unroll
+    for (int u = 0; u < R; ++u) load_b(rb[u], pb0, pb0, u);
+    // This wave's copies are done once at most the R*TJ weight loads issued
+    // after them are outstanding (loads complete in issue order); the
+    // barrier then publishes every wave's part of the tile.
+    constexpr int VM = R * TJ;
+    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
+    __syncthreads();
+
+    for (int sl = 0; sl < nslab; ++sl) {
+        const int8_t *pcur = pb0 + sl * slab_stride;
+        const int8_t *pnxt = sl + 1 < nslab ? pcur + slab_stride : pcur;
+        const int nb0 = (bx0 + sl) * 4 * TJ + wave * TJ;
+        const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc[i][j][r] = 128 * cp.rs[j];
+                    acc2[i][j][r] = 0;
+                }
+        v4i a0[TI], a1[TI];
+        read_a(a0, 0);
+        for (int g = 0; g < nkr; g += R) {
+#pragma unroll
+            for (int u = 0; u < R; u += 2) {
+                read_a(a1, g + u + 1);
+                mma(a0, rb[u]);
+                load_b(rb[u], pcur, pnxt, g + u + R);
+                __builtin_amdgcn_sched_barrier(0);
+                read_a(a0, g + u + 2 < nkr ? g + u + 2 : nkr - 1);
+                mma(a1, rb[u + 1]);
+                load_b(rb[u + 1], pcur, pnxt, g + u + 1 + R);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        epilogue<CONV, EPI, false, TI, TJ, BM, true>(p, acc, acc2, cp, rl, exptab, m0, nb0, lane);
+    }
 }
 
 // M <= 32: block = 64 weight rows (two packed blocks), four waves split the
@@ -514,7 +680,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(KParams p) {
     const int8_t *pbw = p.bp + (size_t)nb0 * p.kb_count * 1024 + lane * 16;
     const size_t jstride = (size_t)p.kb_count * 1024;
     const int lim = p.K - 16 - kk;
-    const v4i flip = {(int)0x80808080, (int)0x80808080, (int)0x80808080, (int)0x80808080};
+    const v4i flip = {p.aflip, p.aflip, p.aflip, p.aflip};
 
     v16i acc[1][TJ], acc2[1][TJ];
 #pragma unroll
@@ -594,16 +760,30 @@ void launch_tile(const KParams &kp, TileCfg t, unsigned grid, hipStream_t st) {
 #undef IRO_TILE
 }
 
+enum Mode { MODE_TILE = 0, MODE_SKINNY = 1, MODE_WHOLE = 2 };
+
 template <int CONV, int EPI>
-void launch_e(const KParams &kp, bool two, bool skinny, TileCfg t, unsigned grid,
+void launch_wt(const KParams &kp, int tj, int ring, unsigned grid, hipStream_t st) {
+    if (tj == 1)
+        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 1, 8>), dim3(grid), dim3(256), 0, st, kp);
+    else if (ring == 8)
+        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 8>), dim3(grid), dim3(256), 0, st, kp);
+    else
+        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 4>), dim3(grid), dim3(256), 0, st, kp);
+}
+
+template <int CONV, int EPI>
+void launch_e(const KParams &kp, bool two, Mode mode, TileCfg t, int ring, unsigned grid,
               hipStream_t st) {
-    if (skinny) {
+    if (mode == MODE_SKINNY) {
         if (two)
             hipLaunchKernelGGL((gemm_skinny_kernel<CONV, EPI, true>), dim3(grid), dim3(256), 0, st,
                                kp);
         else
             hipLaunchKernelGGL((gemm_skinny_kernel<CONV, EPI, false>), dim3(grid), dim3(256), 0,
                                st, kp);
+    } else if (mode == MODE_WHOLE) {
+        launch_wt<CONV, EPI>(kp, t.tj, ring, grid, st);
     } else if (two) {
         launch_tile<CONV, EPI, true>(kp, t, grid, st);
     } else {
@@ -612,13 +792,13 @@ void launch_e(const KParams &kp, bool two, bool skinny, TileCfg t, unsigned grid
 }
 
 template <int CONV>
-void launch_c(const KParams &kp, Epi epi, bool two, bool skinny, TileCfg t, unsigned grid,
+void launch_c(const KParams &kp, Epi epi, bool two, Mode mode, TileCfg t, int ring, unsigned grid,
               hipStream_t st) {
     switch (epi) {
-        case EPI_LINEAR: launch_e<CONV, EPI_LINEAR>(kp, two, skinny, t, grid, st); break;
-        case EPI_QKVG: launch_e<CONV, EPI_QKVG>(kp, two, skinny, t, grid, st); break;
-        case EPI_SWIGLU: launch_e<CONV, EPI_SWIGLU>(kp, two, skinny, t, grid, st); break;
-        case EPI_GATED: launch_e<CONV, EPI_GATED>(kp, two, skinny, t, grid, st); break;
+        case EPI_LINEAR: launch_e<CONV, EPI_LINEAR>(kp, two, mode, t, ring, grid, st); break;
+        case EPI_QKVG: launch_e<CONV, EPI_QKVG>(kp, two, mode, t, ring, grid, st); break;
+        case EPI_SWIGLU: launch_e<CONV, EPI_SWIGLU>(kp, two, mode, t, ring, grid, st); break;
+        case EPI_GATED: launch_e<CONV, EPI_GATED>(kp, two, mode, t, ring, grid, st); break;
     }
 }
 
@@ -643,7 +823,8 @@ TileCfg choose_tile(int M, int Np, int cus, bool two, Epi epi, int forced) {
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi) {
     if (a.M <= 0) return 0;
-    if (a.K <= 0 || a.K % 16 || a.K > w->Kp || a.K < w->K || a.lda < a.K || a.lda % 16 ||
+    if (a.K <= 0 || a.K % 16 || a.K > w->Kp || a.K < w->K || a.K > 65536 || a.lda < a.K ||
+        a.lda % 16 ||
         (((uintptr_t)a.a1) & 15) || (a.a2 && (((uintptr_t)a.a2) & 15)) || w->Np % 256)
         return set_error(ctx, "gemm: unsupported operand shape (K=%d lda=%d Kp=%d Np=%d)", a.K,
                          a.lda, w->Kp, w->Np);
@@ -690,27 +871,57 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     kp.rows_per_branch = a.rows_per_branch > 0 ? a.rows_per_branch : 1;
     const bool two = a.a2 != nullptr;
     const bool skinny = a.M <= 32;
+    kp.aflip = a.a_signed ? 0 : (int)0x80808080;
+    kp.zero16 = static_cast<const uint8_t *>(ctx->zero16);
     TileCfg t{0, 0};
+    Mode mode = MODE_TILE;
+    int ring = ctx->gemm_ring ? ctx->gemm_ring : 4;
     unsigned grid;
     if (skinny) {
+        mode = MODE_SKINNY;
         grid = (unsigned)(w->Np / 64);
         kp.tiles_n = grid;
         kp.tiles_m = 1;
         kp.tiles_per_xcd = 0;
+        kp.row_major = 0;
     } else {
         t = choose_tile(a.M, w->Np, ctx->cus > 0 ? ctx->cus : 256, two, epi, ctx->gemm_tile);
         if (two && t.ti * t.tj > 4) t.tj = 1;  // as launch_tile runs it
+        // Signed single-plane codes with K <= 1024 fit a whole 64-row tile
+        // in LDS: the barrier-free whole-tile kernel.
+        if (a.a_signed && !two && a.K <= 1024 && t.ti == 2) mode = MODE_WHOLE;
         kp.tiles_n = w->Np / (128 * t.tj);
         kp.tiles_m = (a.M + 32 * t.ti - 1) / (32 * t.ti);
         const int tiles = kp.tiles_n * kp.tiles_m;
         kp.tiles_per_xcd = (tiles + 7) / 8;
+        // Each XCD reads its share of one operand once and all of the other:
+        // keep the larger operand split.
+        const double abytes = (double)a.M * a.K * (two ? 2 : 1), wbytes = (double)w->Np * a.K;
+        kp.row_major = ctx->tile_order >= 0 ? ctx->tile_order : (abytes > wbytes ? 1 : 0);
         grid = (unsigned)(8 * kp.tiles_per_xcd);
+        if (mode == MODE_WHOLE) {
+            // Slabs per block: the fewest that still leave about one block
+            // per CU per resident slot pair, so the stationary tile serves
+            // as many slabs as the grid allows.
+            int spb = (epi == EPI_QKVG || epi == EPI_SWIGLU) ? ctx->gemm_spb : 1;
+            if (spb <= 0) {
+                const int cus = ctx->cus > 0 ? ctx->cus : 256;
+                spb = 1;
+                while (spb < kp.tiles_n && (long long)kp.tiles_m * ((kp.tiles_n + 2 * spb - 1) / (2 * spb)) >= cus)
+                    spb *= 2;
+            }
+            kp.spb = spb;
+            kp.groups_n = (kp.tiles_n + spb - 1) / spb;
+            const int items = kp.groups_n * kp.tiles_m;
+            kp.tiles_per_xcd = (items + 7) / 8;
+            grid = (unsigned)(8 * kp.tiles_per_xcd);
+        }
     }
     prof_begin(ctx);
     if (ctx->convention == IRO_HIP_GCC_FASTMATH)
-        launch_c<1>(kp, epi, two, skinny, t, grid, ctx->stream);
+        launch_c<1>(kp, epi, two, mode, t, ring, grid, ctx->stream);
     else
-        launch_c<0>(kp, epi, two, skinny, t, grid, ctx->stream);
+        launch_c<0>(kp, epi, two, mode, t, ring, grid, ctx->stream);
     IRO_HIP_CHECK_LAUNCH(ctx);
     // Algorithmic work: 2*M*N*K per plane; bytes = codes + weights + outputs.
     const double M = a.M, N = w->N, K = w->K, planes = two ? 2 : 1;

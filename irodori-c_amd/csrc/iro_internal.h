@@ -44,7 +44,11 @@ struct IroHipContext {
     unsigned ws_epoch = 0;  // bumped whenever ws is reallocated
     char backend[256] = {0};
     int cus = 0;        // compute units of the device
+    void *zero16 = nullptr;  // 256 zero bytes: the source of padding k pieces
     int gemm_tile = 0;  // 0: tile shape chosen per GEMM; else 10*TI + TJ
+    int tile_order = -1;  // -1: per GEMM; 0 column-slab-major; 1 row-major
+    int gemm_ring = 0;    // weight ring depth of the whole-tile kernel (0: default)
+    int gemm_spb = 0;     // column slabs per whole-tile block (0: chosen per GEMM)
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
 };
 
@@ -120,7 +124,7 @@ struct Workspace {
 
 int launch_quant_rows(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
                       int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
-                      int32_t *z2);
+                      int32_t *z2, bool signed_codes = false);
 int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long long stride_n,
                         long long stride_k, int8_t *q, float *scale, int32_t *colsum);
 int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const int32_t *colsum,
@@ -158,6 +162,7 @@ struct GemmArgs {
     int ldg = 0;
     int ldx = 0;
     int rows_per_branch = 1;
+    int a_signed = 0;  // codes already stored as a ^ 0x80 (quantize_into)
 };
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi);
@@ -199,7 +204,7 @@ inline ActBufs act_at(const Workspace &ws, int K, bool two, const size_t off[6])
 inline int quantize_into(IroHipContext *ctx, const float *x, int M, int K, int ldx,
                          const ActBufs &b) {
     return launch_quant_rows(ctx, x, M, K, ldx, b.q1, b.ld, b.s1, b.z1, nullptr, b.q2, b.s2,
-                             b.z2);
+                             b.z2, true);
 }
 
 inline GemmArgs gemm_args(const ActBufs &b, int M, int K) {
@@ -213,6 +218,7 @@ inline GemmArgs gemm_args(const ActBufs &b, int M, int K) {
     a.zx2 = b.z2;
     a.M = M;
     a.K = (int)round_up((size_t)K, 16);
+    a.a_signed = 1;
     return a;
 }
 

@@ -2,7 +2,9 @@
 // quantization and MFMA pre-packing for gfx950.
 //
 // Activations (ops.c:321-348, ops.c:427-442): one 64-lane wavefront per
-// row.  The row is read once into registers (CH float4 per lane, coalesced
+// row.  Codes are u8 as the reference stores them, or, for buffers only the
+// GEMM reads, the same codes with the top bit flipped (a ^ 0x80 = a - 128
+// as s8), the operand form of the signed int8 MFMA.  The row is read once into registers (CH float4 per lane, coalesced
 // 1 KiB per wave instruction), min/max are wave reductions, and the codes
 // are written as one u32 (4 codes) per lane per chunk.  The two-term
 // variant keeps the row in registers, forms the remainder in place and
@@ -32,7 +34,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
                                                       float *__restrict__ res,
                                                       uint8_t *__restrict__ q2,
                                                       float *__restrict__ s2,
-                                                      int32_t *__restrict__ z2) {
+                                                      int32_t *__restrict__ z2, uint32_t sflip) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= M) return;
@@ -62,7 +64,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
         const int col = (c * 64 + lane) * 4;
         float4 qv;
         const uint32_t packed = codes4<CONV>(v[c], r, RES ? &qv : nullptr);
-        if (col < K) *reinterpret_cast<uint32_t *>(qr + col) = packed;
+        if (col < K) *reinterpret_cast<uint32_t *>(qr + col) = packed ^ sflip;
         if (RES) {
             if (col < K) {
                 v[c].x = residual_value<CONV>(v[c].x, qv.x, r);
@@ -91,7 +93,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
             const int col = (c * 64 + lane) * 4;
             const uint32_t packed = codes4<CONV>(v[c], r2, nullptr);
             if (col < K) {
-                *reinterpret_cast<uint32_t *>(q2r + col) = packed;
+                *reinterpret_cast<uint32_t *>(q2r + col) = packed ^ sflip;
                 if (rr) *reinterpret_cast<float4 *>(rr + col) = v[c];
             }
         }
@@ -111,11 +113,12 @@ __global__ __launch_bounds__(256) void quant_rows_any(const float *__restrict__ 
                                                       float *__restrict__ res,
                                                       uint8_t *__restrict__ q2,
                                                       float *__restrict__ s2,
-                                                      int32_t *__restrict__ z2) {
+                                                      int32_t *__restrict__ z2, uint32_t sflip) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= M) return;
     const float *xr = x + (size_t)row * ldx;
+    const uint8_t fb = (uint8_t)(sflip & 0xff);
     float lo = 0.0f, hi = 0.0f;
     for (int k = lane; k < K; k += 64) {
         lo = sel_min(lo, xr[k]);
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(256) void quant_rows_any(const float *__restrict__ 
     float lo2 = 0.0f, hi2 = 0.0f;
     for (int k = lane; k < K; k += 64) {
         const float v = quant_value<CONV>(xr[k], r);
-        qr[k] = (uint8_t)v;
+        qr[k] = (uint8_t)v ^ fb;
         if (RES) {
             const float rv = residual_value<CONV>(xr[k], v, r);
             lo2 = sel_min(lo2, rv);
@@ -145,8 +148,8 @@ __global__ __launch_bounds__(256) void quant_rows_any(const float *__restrict__ 
         const RowQ r2 = row_params<CONV>(lo2, hi2);
         uint8_t *q2r = q2 + (size_t)row * ldq;
         for (int k = lane; k < K; k += 64) {
-            const float rv = residual_value<CONV>(xr[k], (float)qr[k], r);
-            q2r[k] = (uint8_t)quant_value<CONV>(rv, r2);
+            const float rv = residual_value<CONV>(xr[k], (float)(uint8_t)(qr[k] ^ fb), r);
+            q2r[k] = (uint8_t)quant_value<CONV>(rv, r2) ^ fb;
             if (res) res[(size_t)row * K + k] = rv;
         }
         if (lane == 0) {
@@ -274,7 +277,7 @@ __global__ __launch_bounds__(256) void fill_kernel(uint8_t *__restrict__ dst, ui
 template <int CONV, bool RES>
 int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
                         int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
-                        int32_t *z2) {
+                        int32_t *z2, uint32_t sflip) {
     const dim3 grid((M + 3) / 4), block(256);
     const bool vec = (K % 4 == 0) && (ldx % 4 == 0) && (ldq % 4 == 0) &&
                      (((uintptr_t)x) & 15) == 0 && (((uintptr_t)q1) & 3) == 0 &&
@@ -284,7 +287,7 @@ int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ld
     hipStream_t st = ctx->stream;
 #define IRO_QR(CH)                                                                               \
     hipLaunchKernelGGL((quant_rows_vec<CONV, CH, RES>), grid, block, 0, st, x, M, K, ldx, q1, ldq, \
-                       s1, z1, res, q2, s2, z2)
+                       s1, z1, res, q2, s2, z2, sflip)
     if (vec && ch <= 1) IRO_QR(1);
     else if (vec && ch <= 2) IRO_QR(2);
     else if (vec && ch <= 4) IRO_QR(4);
@@ -293,7 +296,7 @@ int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ld
     else if (vec && ch <= 16) IRO_QR(16);
     else
         hipLaunchKernelGGL((quant_rows_any<CONV, RES>), grid, block, 0, st, x, M, K, ldx, q1, ldq,
-                           s1, z1, res, q2, s2, z2);
+                           s1, z1, res, q2, s2, z2, sflip);
 #undef IRO_QR
     IRO_HIP_CHECK_LAUNCH(ctx);
     return 0;
@@ -303,17 +306,18 @@ int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ld
 
 int launch_quant_rows(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
                       int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
-                      int32_t *z2) {
+                      int32_t *z2, bool signed_codes) {
+    const uint32_t sflip = signed_codes ? 0x80808080u : 0u;
     if (M <= 0 || K <= 0) return 0;
     const bool two = q2 != nullptr;
     prof_begin(ctx);
     int rc;
     if (ctx->convention == IRO_HIP_GCC_FASTMATH)
-        rc = two ? quant_rows_dispatch<1, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
-                 : quant_rows_dispatch<1, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
+        rc = two ? quant_rows_dispatch<1, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2, sflip)
+                 : quant_rows_dispatch<1, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
     else
-        rc = two ? quant_rows_dispatch<0, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2)
-                 : quant_rows_dispatch<0, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2);
+        rc = two ? quant_rows_dispatch<0, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2, sflip)
+                 : quant_rows_dispatch<0, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
     // HBM: fp32 row in, one (two) code planes and row scale/zero out.
     const double mk = (double)M * K, planes = two ? 2 : 1;
     prof_end(ctx, two ? PK_QUANT_RESIDUAL : PK_QUANT, 0,
