@@ -54,7 +54,7 @@ int iro_hip_sync(IroHipContext *ctx);
 /* The context's hipStream_t, for callers that share it. */
 void *iro_hip_stream(IroHipContext *ctx);
 /* GEMM tile shape of the context's M > 32 launches: 32*ti rows by 128*tj
-   columns (ti in {2,4}, tj in {1,2}); ti = tj = 0 restores the per-GEMM
+   columns (ti in {1,2,4}, tj in {1,2}; ti = 1 implies tj = 2); ti = tj = 0 restores the per-GEMM
    choice.  A tuning knob: results are identical for every shape.  No
    counterpart in the reference (oneMKL picks its own blocking). */
 int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj);

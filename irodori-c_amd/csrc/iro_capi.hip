@@ -350,8 +350,8 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
         ctx->gemm_tile = 0;
         return 0;
     }
-    if ((ti != 2 && ti != 4) || (tj != 1 && tj != 2))
-        return set_error(ctx, "set_gemm_tile: tile must be TI in {2,4}, TJ in {1,2}");
+    if ((ti != 1 && ti != 2 && ti != 4) || (tj != 1 && tj != 2))
+        return set_error(ctx, "set_gemm_tile: tile must be TI in {1,2,4}, TJ in {1,2}");
     ctx->gemm_tile = 10 * ti + tj;
     return 0;
 }

@@ -376,7 +376,7 @@ __device__ __forceinline__ bool tile_of(int w, int tiles_m, int tiles_n, int per
 // own weight fragments through a ring of R register slots, R k-blocks of
 // 32 ahead of their use.
 template <int CONV, int EPI, bool TWO, int TI, int TJ>
-__global__ __launch_bounds__(256) void gemm_tile_kernel(KParams p) {
+__device__ __forceinline__ void gemm_tile_body(const KParams &p) {
     constexpr int BM = 32 * TI;
     constexpr int PL = TWO ? 2 : 1;
     constexpr int CP = 8;                               // 16-byte pieces per thread per chunk
@@ -520,6 +520,18 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(KParams p) {
     }
 
     epilogue<CONV, EPI, TWO, TI, TJ, BM>(p, acc, acc2, cp, rl, exptab, m0, nb0, lane);
+}
+
+template <int CONV, int EPI, bool TWO, int TI, int TJ>
+__global__ __launch_bounds__(256) void gemm_tile_kernel(KParams p) {
+    gemm_tile_body<CONV, EPI, TWO, TI, TJ>(p);
+}
+
+// The 32-row tile exists to put two blocks on every CU: hold its register
+// budget to two waves per SIMD.
+template <int CONV, int EPI, bool TWO, int TI, int TJ>
+__global__ __launch_bounds__(256, 2) void gemm_tile_kernel_o2(KParams p) {
+    gemm_tile_body<CONV, EPI, TWO, TI, TJ>(p);
 }
 
 // Whole-tile kernel (one activation plane, K <= 1024, codes stored signed):
@@ -753,7 +765,10 @@ void launch_tile(const KParams &kp, TileCfg t, unsigned grid, hipStream_t st) {
                        st, kp)
     // Two planes of a 128 x 256 tile would hold 256 accumulator registers
     // per lane and spill: that shape runs as 128 x 128.
-    if (t.ti == 2 && t.tj == 1) IRO_TILE(2, 1);
+    if (t.ti == 1)
+        hipLaunchKernelGGL((gemm_tile_kernel_o2<CONV, EPI, TWO, 1, 2>), dim3(grid), dim3(256), 0,
+                           st, kp);
+    else if (t.ti == 2 && t.tj == 1) IRO_TILE(2, 1);
     else if (t.ti == 2 && t.tj == 2) IRO_TILE(2, 2);
     else if (t.ti == 4 && (t.tj == 1 || TWO)) IRO_TILE(4, 1);
     else IRO_TILE(4, (TWO ? 1 : 2));
@@ -805,17 +820,22 @@ void launch_c(const KParams &kp, Epi epi, bool two, Mode mode, TileCfg t, int ri
 // Tile choice (measured on MI355X at the DiT shapes): 64-row tiles keep
 // two blocks resident per CU; 256 columns per block halve the activation
 // re-reads of 128, so they win whenever they still give every CU a tile.
-// The SwiGLU epilogue needs an even number of 32-column blocks per wave.
+// Two planes of a 64 x 256 tile need 128 accumulator registers per lane
+// (one block per CU); 32-row tiles (ti = 1) double the tile count at 64
+// registers, measured no faster at the W2 shape.  The SwiGLU epilogue
+// needs an even number of 32-column blocks per wave.
 TileCfg choose_tile(int M, int Np, int cus, bool two, Epi epi, int forced) {
     if (forced) {
         TileCfg t{forced / 10, forced % 10};
         if (epi == EPI_SWIGLU && t.tj % 2) t.tj = 2;
+        if (t.ti == 1) t.tj = 2;
         if (two && t.ti * t.tj > 4) t.tj = 1;
         if (epi == EPI_SWIGLU && two && t.ti * t.tj > 4) t.ti = 2;
         return t;
     }
-    if (epi == EPI_SWIGLU || two) return TileCfg{2, 2};
     const long long tiles22 = (long long)((M + 63) / 64) * (Np / 256);
+    if (two) return TileCfg{2, 2};
+    if (epi == EPI_SWIGLU) return TileCfg{2, 2};
     return tiles22 >= cus ? TileCfg{2, 2} : TileCfg{2, 1};
 }
 
