@@ -31,6 +31,21 @@ from iro_synth import gauss  # noqa: E402
 PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA
 PEAK_HBM_GBS = 8000.0
 
+# HBM bytes per launch of each kernel kind at this workload, from two
+# rocprofv3 --pmc runs of this script (FETCH_SIZE, then WRITE_SIZE, per
+# dispatch), scaled by what the same counters read for a 64 MiB device copy
+# (--copy-calibration 64: FETCH_SIZE x 1.999, WRITE_SIZE x 1.000); summary
+# and commands in profiles/dit_stack_M2250_hbm_traffic.md.  Counters cannot
+# be read from inside the process, so the figure is the last profile's.
+MEASURED_TRAFFIC = {
+    "gemm_swiglu": 76.2e6,
+    "gemm_gated_two_term": 56.0e6,
+    "gemm_qkvg": 74.5e6,
+    "gemm_gated": 29.6e6,
+    "quant_rows_residual": 38.3e6,
+    "quant_rows": 11.3e6,
+}
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -105,7 +120,22 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run three device-to-device copies of MIB MiB (the known-size "
+                         "copy that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
+
+    if args.copy_calibration > 0:
+        ctx = iro_hip.Context(0, iro_hip.STRICT)
+        n = args.copy_calibration << 18  # float32 elements
+        a, b = ctx.empty(n, np.float32), ctx.empty(n, np.float32)
+        ctx.fill(a, 1)
+        for _ in range(3):
+            ctx.copy(b, a)
+        ctx.sync()
+        log(f"copied {args.copy_calibration} MiB x3")
+        ctx.close()
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -167,25 +197,30 @@ def main():
         step()
     prof = ctx.profile_read()
     ctx.profile(False)
-    total_ms = sum(v[1] for v in prof.values())
+    total_ms = sum(v[1] for v in prof.values()) or 1.0
     for k, (n, kms, kops, kby) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
         avg = kms / n
         log(f"  {k:24s} launches {n:5d}  avg {avg * 1e3:8.2f} us  share {kms / total_ms:6.1%}  "
             f"{kops / kms / 1e9 if kops else 0:8.1f} TOPS  {kby / kms / 1e6:8.1f} GB/s")
-    dom = max(prof.items(), key=lambda kv: kv[1][1])
-    name, (n, kms, kops, kby) = dom
-    avg_ms = kms / n
-    if kops:
-        achieved = kops / n / (avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
-                "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                "kernel": name, "avg_us": round(avg_ms * 1e3, 2),
-                "ops_per_launch": kops / n}
-    else:
-        achieved = kby / n / (avg_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                "kernel": name, "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": kby / n}
+    roof = None
+    if prof:
+        dom = max(prof.items(), key=lambda kv: kv[1][1])
+        name, (n, kms, kops, kby) = dom
+        avg_ms = kms / n
+        if kops:
+            achieved = kops / n / (avg_ms * 1e-3) / 1e12
+            roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
+                    "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                    "traffic": MEASURED_TRAFFIC.get(name),
+                    "kernel": name, "avg_us": round(avg_ms * 1e3, 2),
+                    "ops_per_launch": kops / n}
+        else:
+            achieved = kby / n / (avg_ms * 1e-3) / 1e9
+            roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": MEASURED_TRAFFIC.get(name),
+                    "kernel": name, "avg_us": round(avg_ms * 1e3, 2),
+                    "bytes_per_launch": kby / n}
 
     kernels = {k: {"launches": v[0], "avg_us": round(v[1] / v[0] * 1e3, 2),
                    "share": round(v[1] / total_ms, 4)} for k, v in prof.items()}

@@ -557,9 +557,10 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
     __shared__ __attribute__((aligned(16))) RowLds<BM, false> rl;
     __shared__ uint64_t exptab[32];
 
-    // Work item = (row tile, group of spb slabs), row-tile-major.
+    // Work item = (row tile, group of spb slabs), dealt to the XCDs in the
+    // order that splits the larger operand (see tile_of).
     int gx, by;
-    if (!tile_of(blockIdx.x, p.tiles_m, p.groups_n, p.tiles_per_xcd, 1, gx, by)) return;
+    if (!tile_of(blockIdx.x, p.tiles_m, p.groups_n, p.tiles_per_xcd, p.row_major, gx, by)) return;
     const int bx0 = gx * p.spb;
     const int nslab = !MULTI ? 1 : (p.tiles_n - bx0 < p.spb ? p.tiles_n - bx0 : p.spb);
     const int tid = threadIdx.x;
@@ -932,6 +933,12 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
             }
             kp.spb = spb;
             kp.groups_n = (kp.tiles_n + spb - 1) / spb;
+            // Row bands per XCD: the blocks of an XCD then share their
+            // stationary activation tiles in its L2, which shortens the
+            // latency-bound tile copy; the weight stream hides its latency
+            // in the ring (measured faster than slab order at the DiT
+            // shapes although it moves more bytes).
+            kp.row_major = ctx->tile_order >= 0 ? ctx->tile_order : 1;
             const int items = kp.groups_n * kp.tiles_m;
             kp.tiles_per_xcd = (items + 7) / 8;
             grid = (unsigned)(8 * kp.tiles_per_xcd);
