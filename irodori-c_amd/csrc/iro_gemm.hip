@@ -126,14 +126,16 @@ __constant__ uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
+// Branch-free: the table path runs on x clamped into its domain (the clamp
+// is the identity there; NaN becomes the lower bound) and the special cases
+// are selected afterwards, so a wavefront never splits on them.
 __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
-    if (x != x) return x + x;
-    if (x > 0x1.62e42ep6f) return __builtin_inff();  // overflow
-    if (x < -0x1.9fe368p6f) return 0.0f;             // underflow (and -inf)
+    constexpr float hi = 0x1.62e42ep6f, lo = -0x1.9fe368p6f;  // overflow / underflow bounds
+    const float xc = __builtin_fminf(__builtin_fmaxf(x, lo), hi);
     const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
-    const double xd = (double)x;
+    const double xd = (double)xc;
     double kd = __builtin_fma(invln2n, xd, shift);
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
@@ -144,7 +146,10 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
-    return (float)(y * s);
+    float e = (float)(y * s);
+    e = x > hi ? __builtin_inff() : e;  // overflow
+    e = x < lo ? 0.0f : e;              // underflow (and -inf)
+    return x != x ? x + x : e;
 }
 
 // ops.c:781-784 as the strict build computes it: x / (1 + expf(-x)) * g.
@@ -183,11 +188,26 @@ template <int TJ>
 struct ColParams {
     int cs[TJ], rs[TJ];
     float sw[TJ], b[TJ];
+    float glo[TJ], ghi[TJ];  // gated epilogue: gate of the tile's first and last branch
 };
 
+// Gate rows of the gated epilogue (dit.c:1013-1020): row m uses gate row
+// m / rows_per_branch.  A tile whose rows fall in at most two branches
+// takes both gate values per column up front and selects per row.
+__device__ __forceinline__ int gate_branch_lo(const KParams &p, int m0) {
+    return m0 / p.rows_per_branch;
+}
+__device__ __forceinline__ int gate_branch_hi(const KParams &p, int m0, int bm) {
+    const int last = (m0 + bm < p.M ? m0 + bm : p.M) - 1;
+    return last / p.rows_per_branch;
+}
+
 template <int EPI, int TJ>
-__device__ __forceinline__ ColParams<TJ> load_cols(const KParams &p, int nb0, int lane) {
+__device__ __forceinline__ ColParams<TJ> load_cols(const KParams &p, int nb0, int lane, int m0,
+                                                   int bm) {
     ColParams<TJ> c;
+    const int blo = EPI == EPI_GATED ? gate_branch_lo(p, m0) : 0;
+    const int bhi = EPI == EPI_GATED ? gate_branch_hi(p, m0, bm) : 0;
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int pc = (nb0 + j) * 32 + (lane & 31);  // packed: padded to Np, in bounds
@@ -195,6 +215,13 @@ __device__ __forceinline__ ColParams<TJ> load_cols(const KParams &p, int nb0, in
         c.rs[j] = p.rowsum[pc];
         c.sw[j] = p.sw[pc];
         c.b[j] = (EPI == EPI_LINEAR && p.bias && pc < p.N) ? p.bias[pc] : 0.0f;
+        if (EPI == EPI_GATED) {
+            const int gc = pc < p.N ? pc : p.N - 1;  // padded columns are never stored
+            c.glo[j] = p.gate[blo * p.ldg + gc];
+            c.ghi[j] = p.gate[bhi * p.ldg + gc];
+        } else {
+            c.glo[j] = c.ghi[j] = 0.0f;
+        }
     }
     return c;
 }
@@ -203,8 +230,10 @@ __device__ __forceinline__ ColParams<TJ> load_cols(const KParams &p, int nb0, in
 // layout: lane L, register r holds row 8*(r/4) + 4*(L/32) + r%4 and column
 // L%32 of the tile.  Row (m0 + i*32 + 8*g + e) is wave-uniform, so every
 // store address is a scalar row base plus one per-lane offset fixed per
-// column block.  FULL tiles (all rows < M, all columns < N) store without
-// predicates; the others clamp their loads to row M-1 and predicate stores.
+// column block.  FULL tiles (all rows < M, all columns < N, and for the
+// gated epilogue at most two gate branches) store without predicates; the
+// others clamp their loads to row M-1, predicate stores and gather the gate
+// per element.
 template <int CONV, int EPI, bool TWO, int TI, int TJ, int BM, bool FULL, bool RAW>
 __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc)[TI][TJ],
                                               const v16i (&acc2)[TI][TJ],
@@ -235,6 +264,26 @@ __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc
         for (int j = 0; j + 1 < TJ; j += 2)
             offh[j / 2] = (unsigned)(half * 4 * p.ldh + ((nb0 + j) >> 1) * 32 + (lane & 31));
     }
+    // Gated residual: every old x of the wave tile is loaded before the
+    // first store (the stores may alias later loads for the compiler, which
+    // would otherwise serialize one load round trip per 32x32 block).  Full
+    // tiles span at most two gate branches: rows below gbnd take glo.
+    constexpr int GI = EPI == EPI_GATED ? TI : 1, GJ = EPI == EPI_GATED ? TJ : 1;
+    float xold[GI][GJ][16];
+    const int gbnd = EPI == EPI_GATED ? (gate_branch_lo(p, m0) + 1) * p.rows_per_branch : 0;
+    if (EPI == EPI_GATED) {
+#pragma unroll
+        for (int i = 0; i < GI; ++i)
+#pragma unroll
+            for (int j = 0; j < GJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    int m = m0 + i * 32 + (r >> 2) * 8 + (r & 3);
+                    if (!FULL) m = m + half * 4 < p.M ? m : p.M - 1 - half * 4;
+                    xold[i][j][r] = (FULL || pc[j] < p.N)
+                                        ? p.xres[(long long)m * p.ldx + off[j]] : 0.0f;
+                }
+    }
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         float sx[16], sx2[16];
@@ -252,7 +301,7 @@ __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc
                 sx2[g * 4 + 0] = t4.x; sx2[g * 4 + 1] = t4.y; sx2[g * 4 + 2] = t4.z; sx2[g * 4 + 3] = t4.w;
                 zx2[g * 4 + 0] = w4.x; zx2[g * 4 + 1] = w4.y; zx2[g * 4 + 2] = w4.z; zx2[g * 4 + 3] = w4.w;
             }
-            if (EPI == EPI_GATED) {
+            if (EPI == EPI_GATED && !FULL) {
                 const int4 o4 = *reinterpret_cast<const int4 *>(&rl.goff[rb]);
                 goff[g * 4 + 0] = o4.x; goff[g * 4 + 1] = o4.y; goff[g * 4 + 2] = o4.z; goff[g * 4 + 3] = o4.w;
             }
@@ -281,8 +330,11 @@ __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc
             if (EPI == EPI_GATED) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    old[r] = col_ok ? p.xres[(long long)row_ld(r) * p.ldx + off[j]] : 0.0f;
-                    gv[r] = col_ok ? p.gate[goff[r] + pc[j]] : 0.0f;
+                    old[r] = xold[EPI == EPI_GATED ? i : 0][EPI == EPI_GATED ? j : 0][r];
+                    if (FULL)
+                        gv[r] = rowu(r) + half * 4 < gbnd ? cp.glo[j] : cp.ghi[j];
+                    else
+                        gv[r] = col_ok ? p.gate[goff[r] + pc[j]] : 0.0f;
                 }
             }
 #pragma unroll
@@ -341,12 +393,28 @@ __device__ __forceinline__ void epilogue(const KParams &p, const v16i (&acc)[TI]
                                          const RowLds<BM, TWO> &rl, const uint64_t *exptab,
                                          int m0, int nb0, int lane) {
     const int ncols = EPI == EPI_SWIGLU ? 2 * p.hidden_n : p.N;
-    if (m0 + BM <= p.M && (nb0 + TJ) * 32 <= ncols)
+    bool full = m0 + BM <= p.M && (nb0 + TJ) * 32 <= ncols;
+    if (EPI == EPI_GATED) full = full && gate_branch_hi(p, m0, BM) - gate_branch_lo(p, m0) <= 1;
+    if (full)
         epilogue_body<CONV, EPI, TWO, TI, TJ, BM, true, RAW>(p, acc, acc2, cp, rl, exptab, m0,
                                                              nb0, lane);
     else
         epilogue_body<CONV, EPI, TWO, TI, TJ, BM, false, RAW>(p, acc, acc2, cp, rl, exptab, m0,
                                                               nb0, lane);
+}
+
+// Direct global-to-LDS copy of 16 bytes per lane (global_load_lds_dwordx4:
+// lane L writes at the wave-uniform LDS address + 16 L).  Written as inline
+// assembly so that the compiler's wait-count insertion, which cannot tell
+// which LDS bytes a copy writes, does not drain every outstanding load
+// before each later LDS read; callers wait for the copies themselves.
+__device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *lds) {
+    const uint32_t a = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(a)
+                 : "memory", "m0");
 }
 
 // Tile -> (column slab, row tile).  Workgroups are dealt to the eight XCDs
@@ -399,7 +467,7 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
 
     stage_rows<EPI, TWO, BM>(p, rl, m0, tid);
     if (EPI == EPI_SWIGLU && tid < 32) exptab[tid] = kExp2Tab[tid];
-    const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane);
+    const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane, m0, BM);
 
     // Activation pieces of this thread: piece q = tid + 256*i of a chunk is
     // plane q / (PLANE/16), then fragment f = (q % (PLANE/16)) / 64 =
@@ -536,24 +604,30 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel_o2(KParams p) {
 
 // Whole-tile kernel (one activation plane, K <= 1024, codes stored signed):
 // the block's entire 64-row activation tile, 64 x K bytes, is copied into
-// LDS once by direct global-to-LDS loads (global_load_lds_dwordx4: lane L
-// of a wave writes 16 bytes at the wave's LDS base + 16 L, which is the
-// fragment order), so it needs no staging registers and one barrier.  The
-// block then sweeps `spb` consecutive weight column slabs against that
-// stationary tile.  The main loop has no barriers: each wave streams its
-// weight fragments through an R-deep register ring, and the stream runs on
-// across slabs, so the next slab's first R k blocks are in flight while
-// this slab's epilogue runs.  k past K is copied from a zero page.  The
-// accumulators start at 128 * rowsum[n] (the signed-operand correction), so
-// they end as the reference's raw u8 x s8 sums.
+// LDS by direct global-to-LDS loads (global_load_lds_dwordx4: lane L of a
+// wave writes 16 bytes at the wave's LDS base + 16 L, which is the fragment
+// order), so it needs no staging registers.  The copy runs two ring turns
+// ahead of the MFMAs of the first slab: the pieces of turn t+2 are issued at
+// the end of turn t, and turn t waits only for its own pieces (loads
+// complete in issue order, so "at most R*TJ + P loads outstanding" means
+// this wave's pieces of turn t have landed) and one barrier.  The block
+// then sweeps `spb` consecutive weight column slabs against the stationary
+// tile, barrier-free: each wave streams its weight fragments through an
+// R-deep register ring, and the stream runs on across slabs, so the next
+// slab's first R k blocks are in flight while this slab's epilogue runs.
+// k past K is copied from a zero page.  The accumulators start at
+// 128 * rowsum[n] (the signed-operand correction), so they end as the
+// reference's raw u8 x s8 sums.
 template <int CONV, int EPI, int TJ, int R>
 __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
     constexpr int TI = 2, BM = 64, KMAX = 1024;
+    constexpr int P = R / 2;  // activation pieces per thread per ring turn (a piece spans 2 k blocks)
     // Sweeping several slabs pays for the projections with the largest N
     // (QKVG, W1/W3); the others run one slab per block, which keeps their
     // epilogues' registers out of a loop.
     constexpr bool MULTI = EPI == EPI_QKVG || EPI == EPI_SWIGLU;
     __shared__ __attribute__((aligned(16))) uint8_t lds_a[BM * KMAX];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_sink[1024];  // never read
     __shared__ __attribute__((aligned(16))) RowLds<BM, false> rl;
     __shared__ uint64_t exptab[32];
 
@@ -573,24 +647,28 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
 
     const int nkb = (p.K + 31) / 32;             // k blocks holding activation data
     const int nkr = (nkb + R - 1) / R * R;       // whole ring turns (<= KMAX / 32)
+    const int nturn = nkr / R;
     // Piece q = tid + 256 i of the tile: fragment f = q / 64 = (k block,
     // row block) = (f / 2, f % 2), lane q % 64.  For this thread the row is
-    // fixed and k advances by 64 per piece.
-    {
-        int row = m0 + (wave & 1) * 32 + (lane & 31);
-        row = row < p.M ? row : p.M - 1;
-        const uint8_t *arow = p.a1 + (size_t)row * p.lda;
-        const int k0 = (wave >> 1) * 32 + (lane >> 5) * 16;
-        const int pieces = nkr / 2;
-        for (int i = 0; i < pieces; ++i) {
+    // fixed and k advances by 64 per piece, so pieces t*P .. t*P+P-1 hold
+    // ring turn t's k blocks.  Turns past the last one load the zero page
+    // into a sink, which keeps the count of loads behind every turn's pieces
+    // the same.
+    int arow_i = m0 + (wave & 1) * 32 + (lane & 31);
+    arow_i = arow_i < p.M ? arow_i : p.M - 1;
+    const uint8_t *arow = p.a1 + (size_t)arow_i * p.lda;
+    const int k0 = (wave >> 1) * 32 + (lane >> 5) * 16;
+    auto copy_turn = [&](int t) {
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+            const int i = t * P + q;
             const int k = k0 + 64 * i;
-            const uint8_t *src = k < p.K ? arow + k : p.zero16;
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)src,
-                (__attribute__((address_space(3))) void *)(lds_a + (size_t)(tid - lane + 256 * i) * 16),
-                16, 0, 0);
+            const bool real = t < nturn;
+            const uint8_t *src = real && k < p.K ? arow + k : p.zero16;
+            uint8_t *dst = real ? lds_a + (size_t)(tid - lane + 256 * i) * 16 : lds_sink;
+            dma16(src, dst);
         }
-    }
+    };
     const size_t jstride = (size_t)p.kb_count * 1024;
     const size_t slab_stride = (size_t)4 * TJ * jstride;  // bytes between column slabs
     const int8_t *pb0 = p.bp + (size_t)(bx0 * 4 * TJ + wave * TJ) * jstride + lane * 16;
@@ -622,20 +700,22 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
     };
 
+    // Issue order: pieces of turn 0, the first R weight k blocks, pieces of
+    // turn 1; every later turn t issues R*TJ weight loads and then the
+    // pieces of turn t+2.  Behind the pieces of any turn t there are thus at
+    // least R*TJ + P loads when turn t begins.
+    copy_turn(0);
 #pragma unroll
     for (int u = 0; u < R; ++u) load_b(rb[u], pb0, pb0, u);
-    // This wave's copies are done once at most the R*TJ weight loads issued
-    // after them are outstanding (loads complete in issue order); the
-    // barrier then publishes every wave's part of the tile.
-    constexpr int VM = R * TJ;
-    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
-    __syncthreads();
+    copy_turn(1);
+    constexpr int VM = R * TJ + P;
+    static_assert(VM < 64, "vmcnt holds 6 bits");
 
     for (int sl = 0; sl < nslab; ++sl) {
         const int8_t *pcur = pb0 + sl * slab_stride;
         const int8_t *pnxt = sl + 1 < nslab ? pcur + slab_stride : pcur;
         const int nb0 = (bx0 + sl) * 4 * TJ + wave * TJ;
-        const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane);
+        const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane, m0, BM);
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -645,23 +725,34 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
                     acc[i][j][r] = 128 * cp.rs[j];
                     acc2[i][j][r] = 0;
                 }
+        // In the first slab each turn waits for its own pieces, then a
+        // barrier publishes the other waves' pieces (and, at turn 0, the row
+        // parameters); later slabs find the whole tile in LDS.
         v4i a0[TI], a1[TI];
-        read_a(a0, 0);
-        for (int g = 0; g < nkr; g += R) {
+        for (int t = 0; t < nturn; ++t) {
+            const int g = t * R;
+            if (sl == 0) {
+                __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
+                __syncthreads();
+            }
+            read_a(a0, g);
 #pragma unroll
             for (int u = 0; u < R; u += 2) {
                 read_a(a1, g + u + 1);
                 mma(a0, rb[u]);
                 load_b(rb[u], pcur, pnxt, g + u + R);
                 __builtin_amdgcn_sched_barrier(0);
-                read_a(a0, g + u + 2 < nkr ? g + u + 2 : nkr - 1);
+                if (u + 2 < R) read_a(a0, g + u + 2);
                 mma(a1, rb[u + 1]);
                 load_b(rb[u + 1], pcur, pnxt, g + u + 1 + R);
                 __builtin_amdgcn_sched_barrier(0);
             }
+            if (sl == 0) copy_turn(t + 2);
         }
         epilogue<CONV, EPI, false, TI, TJ, BM, true>(p, acc, acc2, cp, rl, exptab, m0, nb0, lane);
     }
+    // No copy into this block's LDS may still be in flight when it exits.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 }
 
 // M <= 32: block = 64 weight rows (two packed blocks), four waves split the
@@ -749,7 +840,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(KParams p) {
                 acc[0][j][r] += red[w][0][j][r][lane];
                 if (TWO) acc2[0][j][r] += red[w][PL - 1][j][r][lane];
             }
-    const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane);
+    const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane, 0, 32);
     epilogue<CONV, EPI, TWO, 1, TJ, 32>(p, acc, acc2, cp, rl, exptab, 0, nb0, lane);
 }
 
