@@ -11,6 +11,10 @@ Every quantization, int8 GEMM and epilogue of the step runs on the GPU
 through the C ABI; inputs and weights are resident in HBM before timing.
 The fp32 attention core and RMSNorm-modulate are not part of the stack.
 
+`--workload conv7` (T=24000, 512->512, kernel 7, padding 3) and
+`--workload conv7-dil3` (T=6000, 1024->256, dilation 3, padding 9) measure
+the codec's int8 Conv1d instead: one conv per step, same JSON line.
+
 Prints one JSON line on stdout; diagnostics go to stderr.
 """
 import argparse
@@ -105,6 +109,137 @@ def cpu_baseline(args, base, x0, cond, D, H, ops_per_step):
     }
 
 
+CONV_WORKLOADS = {  # T, C_in, C_out, kernel, stride, dilation, padding
+    "conv7": (24000, 512, 512, 7, 1, 1, 3),
+    "conv7-dil3": (6000, 1024, 256, 7, 1, 3, 9),
+}
+
+
+def roofline_of(prof):
+    """Dominant kernel kind (largest share of profiled time) against its
+    roofline: int8 MFMA peak when it does MFMA work, else HBM."""
+    if not prof:
+        return None
+    name, (n, kms, kops, kby) = max(prof.items(), key=lambda kv: kv[1][1])
+    avg_ms = kms / n
+    if kops:
+        achieved = kops / n / (avg_ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
+                "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4),
+                "traffic": MEASURED_TRAFFIC.get(name), "kernel": name,
+                "avg_us": round(avg_ms * 1e3, 2), "ops_per_launch": kops / n}
+    achieved = kby / n / (avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": MEASURED_TRAFFIC.get(name),
+            "kernel": name, "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": kby / n}
+
+
+def log_profile(prof):
+    total_ms = sum(v[1] for v in prof.values()) or 1.0
+    for k, (n, kms, kops, kby) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
+        log(f"  {k:24s} launches {n:5d}  avg {kms / n * 1e3:8.2f} us  share {kms / total_ms:6.1%}  "
+            f"{kops / kms / 1e9 if kops else 0:8.1f} TOPS  {kby / kms / 1e6:8.1f} GB/s")
+    return {k: {"launches": v[0], "avg_us": round(v[1] / v[0] * 1e3, 2),
+                "share": round(v[1] / total_ms, 4)} for k, v in prof.items()}
+
+
+def conv_main(args):
+    """The codec's int8 Conv1d (dacvae.c:543-688) at its measured shapes:
+    one step = one conv (input ranges, quantized im2col, int8 GEMM with the
+    bias epilogue) with input and weights resident in HBM."""
+    T, Cin, N, k, st, dil, pad = CONV_WORKLOADS[args.workload]
+    To = (T + 2 * pad - dil * (k - 1) - 1) // st + 1
+    planes = 2 if args.conv_residual else 1
+    ops = 2 * To * N * k * Cin * planes
+    conv = iro_hip.STRICT if args.convention == "strict" else iro_hip.GCC_FASTMATH
+    x = gauss(42, (T, Cin))
+    w = gauss(43, (N, k * Cin), 0.02)
+    b = gauss(44, (N,), 0.01)
+    ctx = iro_hip.Context(0, conv)
+    log("backend:", ctx.backend())
+    wd = ctx.to_device(w)
+    W = ctx.weight(wd, N, k * Cin)
+    wd.free()
+    xd, bd = ctx.to_device(x), ctx.to_device(b)
+    y = ctx.empty((To, N), np.float32)
+
+    def step():
+        ctx.conv1d(xd, T, Cin, W, k, st, dil, pad, bd, args.conv_residual, y)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    t0 = time.perf_counter()
+    ctx.record(e0)
+    for _ in range(args.steps):
+        step()
+    ctx.record(e1)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.elapsed_ms(e0, e1)
+    ms_step = wall * 1e3 / args.steps
+    log(f"{args.workload}: {ms_step:.3f} ms/conv wall, {ev_ms / args.steps:.3f} ms/conv events")
+    ctx.profile(True)
+    for _ in range(args.profile_steps):
+        step()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    kernels = log_profile(prof)
+    roof = roofline_of(prof)
+    ygpu = y.numpy()
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import CpuBaseline, Oracle
+        threads = min(16, len(os.sched_getaffinity(0)))
+        cb = CpuBaseline(threads)
+        wq = Oracle().weight_quantize(0 if conv == iro_hip.STRICT else 1, w)
+        times = []
+        start = time.perf_counter()
+        while len(times) < 5 and time.perf_counter() - start < args.cpu_seconds:
+            t1 = time.perf_counter()
+            ycpu, parts = cb.conv1d(0 if conv == iro_hip.STRICT else 1, x, *wq, k, st, dil, pad,
+                                    bias=b, residual=args.conv_residual)
+            times.append(time.perf_counter() - t1)
+        med = sorted(times)[len(times) // 2]
+        same = bool(np.array_equal(ycpu.view(np.uint32), ygpu.view(np.uint32)))
+        log(f"cpu baseline: {len(times)} convs, median {med * 1e3:.1f} ms on {threads} threads "
+            f"({cb.backend}); last: quantize {parts[0]:.3f}s gemm {parts[1]:.3f}s "
+            f"epilogue {parts[2]:.3f}s; GPU output bit-identical: {same}")
+        cpu = {"value": round(ops / med / 1e12, 4), "unit": "TOPS", "cores": threads,
+               "kind": "port", "ms_per_step": round(med * 1e3, 2), "backend": cb.backend,
+               "sample": (f"the full conv ({len(times)} runs, median): im2col quantization on one "
+                          f"thread as dacvae.c, GEMM on {threads} threads, epilogue on one thread"),
+               "gpu_output_bit_identical": same}
+
+    out = {
+        "metric": f"int8 Conv1d TOPS ({args.workload}), 1 GPU",
+        "value": round(ops * args.steps / wall / 1e12, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded Irwin-Hall Gaussian input, random-init weights)",
+        "config": {"workload": (f"int8 Conv1d T={T}, {Cin}->{N}, kernel {k}, stride {st}, "
+                                f"dilation {dil}, padding {pad}, {planes} plane(s), bias; one conv "
+                                f"per step"),
+                   "T": T, "c_in": Cin, "c_out": N, "kernel": k, "dilation": dil,
+                   "padding": pad, "planes": planes, "ops_per_step": ops,
+                   "convention": args.convention, "parallelism": "single GPU"},
+        "roofline": roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +255,10 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=["stack"] + sorted(CONV_WORKLOADS), default="stack",
+                    help="stack (default): the DiT linear stack; conv7*: the codec int8 Conv1d")
+    ap.add_argument("--conv-residual", action="store_true",
+                    help="conv workloads: add the fixed-scale second plane")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run three device-to-device copies of MIB MiB (the known-size "
                          "copy that scales rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -142,6 +281,9 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
+    if args.workload != "stack":
+        conv_main(args)
+        return
 
     B, S, D, H = args.batch, args.frames, args.hidden, args.mlp
     M = B * S
@@ -197,33 +339,8 @@ def main():
         step()
     prof = ctx.profile_read()
     ctx.profile(False)
-    total_ms = sum(v[1] for v in prof.values()) or 1.0
-    for k, (n, kms, kops, kby) in sorted(prof.items(), key=lambda kv: -kv[1][1]):
-        avg = kms / n
-        log(f"  {k:24s} launches {n:5d}  avg {avg * 1e3:8.2f} us  share {kms / total_ms:6.1%}  "
-            f"{kops / kms / 1e9 if kops else 0:8.1f} TOPS  {kby / kms / 1e6:8.1f} GB/s")
-    roof = None
-    if prof:
-        dom = max(prof.items(), key=lambda kv: kv[1][1])
-        name, (n, kms, kops, kby) = dom
-        avg_ms = kms / n
-        if kops:
-            achieved = kops / n / (avg_ms * 1e-3) / 1e12
-            roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS,
-                    "unit": "TOPS", "frac": round(achieved / PEAK_INT8_TOPS, 4),
-                    "traffic": MEASURED_TRAFFIC.get(name),
-                    "kernel": name, "avg_us": round(avg_ms * 1e3, 2),
-                    "ops_per_launch": kops / n}
-        else:
-            achieved = kby / n / (avg_ms * 1e-3) / 1e9
-            roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": MEASURED_TRAFFIC.get(name),
-                    "kernel": name, "avg_us": round(avg_ms * 1e3, 2),
-                    "bytes_per_launch": kby / n}
-
-    kernels = {k: {"launches": v[0], "avg_us": round(v[1] / v[0] * 1e3, 2),
-                   "share": round(v[1] / total_ms, 4)} for k, v in prof.items()}
+    kernels = log_profile(prof)
+    roof = roofline_of(prof)
     stack_bytes = stack.nbytes()
     stack.destroy()
     ctx.close()

@@ -231,3 +231,41 @@ int cpub_dit_block(int conv, const CpubWeight *w, float *x, const float *cond, i
 void cpub_gemm(const uint8_t *a, const int8_t *b, int32_t *c, int M, int N, int K) {
     gemm(a, b, c, M, N, K);
 }
+
+/* The reference's int8 Conv1d (dacvae.c:543-688) on the host: the quantized
+   im2col rows on one thread (the reference's serial loop), the GEMM on MKL
+   threads (ops.c:458-461), the epilogue with bias on one thread
+   (ops.c:468-490), and, with residual, the second plane accumulated.
+   Returns T_out or -1; t[0..2] as cpub_linear. */
+int cpub_conv1d(int conv, const float *x, int T, int C, const int8_t *wq, const float *sw,
+                const int32_t *colsum, int N, int kernel, int stride, int dilation,
+                int padding, const float *bias, int residual, float *y, double *t) {
+    const int T_out = orc_conv1d_output_length(T, kernel, stride, dilation, padding);
+    if (T_out <= 0) return -1;
+    const size_t inner = (size_t)kernel * C;
+    uint8_t *c1 = malloc((size_t)T_out * inner);
+    uint8_t *c2 = residual ? malloc((size_t)T_out * inner) : NULL;
+    float *s1 = malloc(sizeof(float) * T_out), *s2 = malloc(sizeof(float) * T_out);
+    int32_t *z1 = malloc(sizeof(int32_t) * T_out), *z2 = malloc(sizeof(int32_t) * T_out);
+    int32_t *work = malloc(sizeof(int32_t) * (size_t)T_out * N);
+    int ok = c1 && s1 && s2 && z1 && z2 && work && (!residual || c2);
+    if (ok) {
+        double t0 = now_s();
+        ok = orc_conv1d_quantize(conv, x, T, C, kernel, stride, dilation, padding, c1, s1, z1,
+                                 c2, s2, z2) == T_out;
+        double t1 = now_s();
+        t[0] += t1 - t0;
+        for (int plane = 0; ok && plane < (residual ? 2 : 1); plane++) {
+            double a = now_s();
+            gemm(plane ? c2 : c1, wq, work, T_out, N, (int)inner);
+            double b = now_s();
+            orc_epilogue(conv, work, plane ? s2 : s1, plane ? z2 : z1, sw, colsum,
+                         plane ? NULL : bias, y, T_out, N, plane);
+            double c = now_s();
+            t[1] += b - a;
+            t[2] += c - b;
+        }
+    }
+    free(c1); free(c2); free(s1); free(s2); free(z1); free(z2); free(work);
+    return ok ? T_out : -1;
+}

@@ -351,6 +351,93 @@ int orc_conv1d_output_length(int T, int kernel, int stride, int dilation,
     return out <= 0 || out > 0x7fffffffLL ? -1 : (int)out;
 }
 
+/* The quantized im2col rows of the conv (dacvae.c:607-673): per input row
+   the range over channels, per output row the window range over the taps
+   inside [0, T), then the u8 row [tap*C + c] (padding taps = zero point) and,
+   with c2 != NULL, the fixed-scale second plane (dacvae.c:637-663).
+   Returns T_out, or -1 on bad shapes or allocation failure. */
+int orc_conv1d_quantize(int conv, const float *input, int T, int C, int kernel,
+                        int stride, int dilation, int padding, uint8_t *c1,
+                        float *s1, int32_t *z1, uint8_t *c2, float *s2,
+                        int32_t *z2) {
+    const int T_out = orc_conv1d_output_length(T, kernel, stride, dilation, padding);
+    if (T_out <= 0 || C <= 0) return -1;
+    const int inner = kernel * C;
+    const int fast = conv == ORC_GCC_FASTMATH;
+    const int residual = c2 != NULL;
+    /* Per input row (time step) range over channels, with zero included
+       (dacvae.c:607-616). */
+    float *row_lo = malloc(sizeof(float) * (size_t)T);
+    float *row_hi = malloc(sizeof(float) * (size_t)T);
+    if (!row_lo || !row_hi) {
+        free(row_lo); free(row_hi);
+        return -1;
+    }
+    for (int t = 0; t < T; t++) row_range(input + (size_t)t * C, C, &row_lo[t], &row_hi[t]);
+    for (int r = 0; r < T_out; r++) {
+        /* Window range over the taps that land inside [0, T)
+           (dacvae.c:617-627); padding taps do not widen it. */
+        float lo = 0.0f, hi = 0.0f;
+        for (int tap = 0; tap < kernel; tap++) {
+            int it = r * stride - padding + tap * dilation;
+            if (it < 0 || it >= T) continue;
+            lo = row_lo[it] < lo ? row_lo[it] : lo;
+            hi = row_hi[it] > hi ? row_hi[it] : hi;
+        }
+        RowQuant q = row_params(conv, lo, hi);
+        float sc2, inv2;
+        if (fast) {
+            /* dacvae.c:637-638 under fast-math: s/255 -> s*fl(1/255),
+               255/s -> 0x477E00FF/(hi-lo) (s=1 rows are all-zero windows
+               whose plane-2 codes are 128 regardless of inv2). */
+            sc2 = q.s * C_INV255;
+            float d = hi - lo;
+            inv2 = (hi - lo) * C_INV255 > 0.0f ? C_255_OVER_INV255_B / d : 255.0f;
+        } else {
+            sc2 = q.s / 255.0f;
+            inv2 = 255.0f / q.s;
+        }
+        s1[r] = q.s;
+        z1[r] = q.zp;
+        if (residual) {
+            s2[r] = sc2;
+            z2[r] = 128;
+        }
+        uint8_t *dst = c1 + (size_t)r * inner;
+        uint8_t *dst2 = residual ? c2 + (size_t)r * inner : NULL;
+        for (int tap = 0; tap < kernel; tap++) {
+            int it = r * stride - padding + tap * dilation;
+            uint8_t *td = dst + (size_t)tap * C;
+            if (it < 0 || it >= T) {
+                memset(td, q.zp, (size_t)C);
+                if (residual) memset(dst2 + (size_t)tap * C, 128, (size_t)C);
+                continue;
+            }
+            const float *row = input + (size_t)it * C;
+            for (int c = 0; c < C; c++) {
+                uint8_t code = quant_code(conv, row[c], &q);
+                td[c] = code;
+                if (residual) {
+                    float v = (float)code;
+                    float rem, v2;
+                    if (fast) {
+                        rem = fmaf(q.s, q.zpf - v, row[c]);
+                        v2 = rne(fmaf(rem, inv2, 128.0f));
+                    } else {
+                        rem = row[c] - q.s * (v - q.zpf);
+                        v2 = rne(rem * inv2 + 128.0f);
+                    }
+                    v2 = v2 < 0.0f ? 0.0f : v2;
+                    v2 = v2 > 255.0f ? 255.0f : v2;
+                    dst2[(size_t)tap * C + c] = (uint8_t)v2;
+                }
+            }
+        }
+    }
+    free(row_lo); free(row_hi);
+    return T_out;
+}
+
 int orc_conv1d_int8(int conv, const float *input, int T, int C,
                     const int8_t *wq, const float *sw, const int32_t *colsum,
                     int N, int kernel, int stride, int dilation, int padding,
@@ -360,11 +447,6 @@ int orc_conv1d_int8(int conv, const float *input, int T, int C,
     const int T_out = orc_conv1d_output_length(T, kernel, stride, dilation, padding);
     if (T_out <= 0 || C <= 0 || N <= 0) return -1;
     const int inner = kernel * C;
-    const int fast = conv == ORC_GCC_FASTMATH;
-    /* Per input row (time step) range over channels, with zero included
-       (dacvae.c:607-616). */
-    float *row_lo = malloc(sizeof(float) * (size_t)T);
-    float *row_hi = malloc(sizeof(float) * (size_t)T);
     uint8_t *c1 = cols ? cols : malloc((size_t)T_out * inner);
     uint8_t *c2 = residual ? malloc((size_t)T_out * inner) : NULL;
     float *s1 = malloc(sizeof(float) * (size_t)T_out);
@@ -372,70 +454,11 @@ int orc_conv1d_int8(int conv, const float *input, int T, int C,
     float *s2 = residual ? malloc(sizeof(float) * (size_t)T_out) : NULL;
     int32_t *z2 = residual ? malloc(sizeof(int32_t) * (size_t)T_out) : NULL;
     int32_t *work = malloc(sizeof(int32_t) * (size_t)T_out * N);
-    int ok = row_lo && row_hi && c1 && s1 && z1 && work &&
-             (!residual || (c2 && s2 && z2));
+    int ok = c1 && s1 && z1 && work && (!residual || (c2 && s2 && z2));
+    if (ok)
+        ok = orc_conv1d_quantize(conv, input, T, C, kernel, stride, dilation, padding,
+                                 c1, s1, z1, c2, s2, z2) == T_out;
     if (ok) {
-        for (int t = 0; t < T; t++) row_range(input + (size_t)t * C, C, &row_lo[t], &row_hi[t]);
-        for (int r = 0; r < T_out; r++) {
-            /* Window range over the taps that land inside [0, T)
-               (dacvae.c:617-627); padding taps do not widen it. */
-            float lo = 0.0f, hi = 0.0f;
-            for (int tap = 0; tap < kernel; tap++) {
-                int it = r * stride - padding + tap * dilation;
-                if (it < 0 || it >= T) continue;
-                lo = row_lo[it] < lo ? row_lo[it] : lo;
-                hi = row_hi[it] > hi ? row_hi[it] : hi;
-            }
-            RowQuant q = row_params(conv, lo, hi);
-            float sc2, inv2;
-            if (fast) {
-                /* dacvae.c:637-638 under fast-math: s/255 -> s*fl(1/255),
-                   255/s -> 0x477E00FF/(hi-lo) (s=1 rows are all-zero windows
-                   whose plane-2 codes are 128 regardless of inv2). */
-                sc2 = q.s * C_INV255;
-                float d = hi - lo;
-                inv2 = (hi - lo) * C_INV255 > 0.0f ? C_255_OVER_INV255_B / d : 255.0f;
-            } else {
-                sc2 = q.s / 255.0f;
-                inv2 = 255.0f / q.s;
-            }
-            s1[r] = q.s;
-            z1[r] = q.zp;
-            if (residual) {
-                s2[r] = sc2;
-                z2[r] = 128;
-            }
-            uint8_t *dst = c1 + (size_t)r * inner;
-            uint8_t *dst2 = residual ? c2 + (size_t)r * inner : NULL;
-            for (int tap = 0; tap < kernel; tap++) {
-                int it = r * stride - padding + tap * dilation;
-                uint8_t *td = dst + (size_t)tap * C;
-                if (it < 0 || it >= T) {
-                    memset(td, q.zp, (size_t)C);
-                    if (residual) memset(dst2 + (size_t)tap * C, 128, (size_t)C);
-                    continue;
-                }
-                const float *row = input + (size_t)it * C;
-                for (int c = 0; c < C; c++) {
-                    uint8_t code = quant_code(conv, row[c], &q);
-                    td[c] = code;
-                    if (residual) {
-                        float v = (float)code;
-                        float rem, v2;
-                        if (fast) {
-                            rem = fmaf(q.s, q.zpf - v, row[c]);
-                            v2 = rne(fmaf(rem, inv2, 128.0f));
-                        } else {
-                            rem = row[c] - q.s * (v - q.zpf);
-                            v2 = rne(rem * inv2 + 128.0f);
-                        }
-                        v2 = v2 < 0.0f ? 0.0f : v2;
-                        v2 = v2 > 255.0f ? 255.0f : v2;
-                        dst2[(size_t)tap * C + c] = (uint8_t)v2;
-                    }
-                }
-            }
-        }
         orc_int8_linear_ex(conv, c1, s1, z1, wq, sw, colsum, N, inner, bias,
                            output, T_out, work, 0, threads);
         if (residual)
@@ -444,7 +467,6 @@ int orc_conv1d_int8(int conv, const float *input, int T, int C,
         if (row_scale) memcpy(row_scale, s1, sizeof(float) * (size_t)T_out);
         if (row_zero) memcpy(row_zero, z1, sizeof(int32_t) * (size_t)T_out);
     }
-    free(row_lo); free(row_hi);
     if (!cols) free(c1);
     free(c2); free(s1); free(z1); free(s2); free(z2); free(work);
     return ok ? T_out : -1;

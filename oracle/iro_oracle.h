@@ -98,6 +98,13 @@ int orc_conv1d_int8(int conv, const float *input, int T, int C,
                     uint8_t *cols, float *row_scale, int32_t *row_zero,
                     int threads);
 
+/* The quantized im2col rows of the conv alone (dacvae.c:607-673): c1 (and,
+   with c2 != NULL, the second plane) [T_out, kernel*C], per-row s, zp. */
+int orc_conv1d_quantize(int conv, const float *input, int T, int C, int kernel,
+                        int stride, int dilation, int padding, uint8_t *c1,
+                        float *s1, int32_t *z1, uint8_t *c2, float *s2,
+                        int32_t *z2);
+
 /* dacvae.c:340-348 (iro_conv1d_output_length). */
 int orc_conv1d_output_length(int T, int kernel, int stride, int dilation,
                              int padding);

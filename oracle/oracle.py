@@ -316,6 +316,10 @@ class CpuBaseline:
                                      C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
         L.cpub_dit_block.restype = C.c_int
         L.cpub_gemm.argtypes = [_u8p, _i8p, _i32p, C.c_int, C.c_int, C.c_int]
+        L.cpub_conv1d.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p, C.c_int,
+                                  C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int, _f32p,
+                                  C.POINTER(C.c_double)]
+        L.cpub_conv1d.restype = C.c_int
         buf = C.create_string_buffer(256)
         self.mkl = bool(L.cpub_init((mkl_path or "").encode(), threads, buf, 256))
         self.backend = buf.value.decode()
@@ -338,3 +342,22 @@ class CpuBaseline:
                                      residual_mask, t)
         assert rc == 0
         return tuple(t)
+
+    def conv1d(self, conv, x, wq, sw, colsum, kernel, stride, dilation, padding, bias=None,
+               residual=False):
+        """The reference's int8 Conv1d on the host (oneMKL GEMM); returns
+        (y, seconds (quantize, gemm, epilogue))."""
+        x = _f32(x)
+        T, Cin = x.shape
+        N = wq.shape[0]
+        To = (T + 2 * padding - dilation * (kernel - 1) - 1) // stride + 1
+        y = np.zeros((To, N), np.float32)
+        t = (C.c_double * 3)()
+        rc = self.lib.cpub_conv1d(conv, _p(x, _f32p), T, Cin,
+                                  _p(np.ascontiguousarray(wq, np.int8), _i8p), _p(_f32(sw), _f32p),
+                                  _p(np.ascontiguousarray(colsum, np.int32), _i32p), N, kernel,
+                                  stride, dilation, padding,
+                                  _p(None if bias is None else _f32(bias), _f32p),
+                                  int(bool(residual)), _p(y, _f32p), t)
+        assert rc == To
+        return y, tuple(t)
