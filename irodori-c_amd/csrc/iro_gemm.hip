@@ -85,6 +85,7 @@ struct KParams {
     int aflip;             // XOR applied to stored codes: 0x80808080 for u8 codes, 0 if signed
     int spb, groups_n;     // whole-tile kernel: column slabs per block, slab groups per row
     const uint8_t *zero16; // 256 zero bytes
+    int wbytes;            // bytes of the packed weight (< 2^31)
 };
 
 // ops.c:468-490: y = t*c [+ b] or y += t*c [+ b] with the build's rounding.
@@ -417,6 +418,27 @@ __device__ __forceinline__ void dma16(const uint8_t *src, uint8_t *lds) {
                  : "memory", "m0");
 }
 
+// Scheduling fence between the parts of a main-loop k step.  Each step
+// issues the LDS reads of the next step's activation fragments, then (after
+// a fence) its own MFMAs and the weight loads that refill the ring.  Without
+// the fences the scheduler sinks the LDS reads below the MFMAs (and shares
+// their registers with the current step's), which exposes the LDS latency
+// once per k step, and sinks the loads below later MFMAs, which drains the
+// ring.
+__device__ __forceinline__ void fence_sched() { __builtin_amdgcn_sched_barrier(0); }
+
+// Weight fragments are read through a buffer resource: the base and every
+// wave-uniform offset (column block, k block) live in scalar registers and
+// the one per-lane offset (lane * 16) in a vector register, so refilling the
+// weight ring costs no vector ALU work.  The packed weight is below 2 GiB
+// (launch_gemm checks), so 32-bit offsets reach all of it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const KParams &p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(p.bp), 0, p.wbytes, 0x00020000);
+}
+__device__ __forceinline__ v4i load_frag(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
 // Tile -> (column slab, row tile).  Workgroups are dealt to the eight XCDs
 // round-robin (workgroup w runs on XCD w % 8), so workgroup w takes tile
 // (w % 8) * per + w / 8 of a fixed order: each XCD works through one
@@ -461,7 +483,7 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
     if (!tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.tiles_per_xcd, p.row_major, bx, by)) return;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int m0 = by * BM;
     const int nb0 = bx * 4 * TJ + wave * TJ;  // first packed 32-row weight block of this wave
 
@@ -486,8 +508,9 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
         kof[i] = kbl * 32 + (ln >> 5) * 16;
         pa[i] = (pl == 0 ? p.a1 : p.a2) + (size_t)gr * p.lda;
     }
-    const int8_t *pbw = p.bp + (size_t)nb0 * p.kb_count * 1024 + lane * 16;
-    const size_t jstride = (size_t)p.kb_count * 1024;
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(p);
+    const int jstride = p.kb_count * 1024;     // bytes between 32-row weight blocks
+    const int wbase = nb0 * jstride;           // this wave's first block
     const int nkb = (p.K + 31) / 32;  // k blocks holding activation data
     const int nc = (p.K + KC - 1) / KC;
 
@@ -527,8 +550,7 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
         (void)slot_unused;
         kb = kb < nkb ? kb : nkb - 1;  // past the end: a repeat, multiplied by zero codes
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
-            dst[j] = *reinterpret_cast<const v4i *>(pbw + j * jstride + (size_t)kb * 1024);
+        for (int j = 0; j < TJ; ++j) dst[j] = load_frag(wr, lane * 16, wbase + j * jstride + kb * 1024);
     };
     auto read_a = [&](v4i (&a)[PL][TI], const uint8_t *abuf, int kbl) {
 #pragma unroll
@@ -570,18 +592,17 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
         read_a(a0, abuf, 0);
 #pragma unroll
         for (int u = 0; u < KBC; u += 2) {
-            // sched_barrier keeps each step's loads where they are written:
-            // the scheduler would otherwise sink them below later MFMAs and
-            // drain the ring.
             read_a(a1, abuf, u + 1);
+            fence_sched();
             mma(a0, rb[u % R]);
             load_b(u % R, rb[u % R], g0 + u + R);
-            __builtin_amdgcn_sched_barrier(0);
+            fence_sched();
             if (u + 2 < KBC) read_a(a0, abuf, u + 2);
+            fence_sched();
             mma(a1, rb[(u + 1) % R]);
             load_b((u + 1) % R, rb[(u + 1) % R], g0 + u + 1 + R);
             if (u + 2 == R) load_chunk(c + 1 < nc ? c + 1 : c);
-            __builtin_amdgcn_sched_barrier(0);
+            fence_sched();
         }
         store_chunk((c + 1) & 1, c + 1);
         __syncthreads();
@@ -619,7 +640,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel_o2(KParams p) {
 // 128 * rowsum[n] (the signed-operand correction), so they end as the
 // reference's raw u8 x s8 sums.
 template <int CONV, int EPI, int TJ, int R>
-__global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
+__global__ __launch_bounds__(256, (EPI == EPI_QKVG || EPI == EPI_SWIGLU) ? 2 : 1) void gemm_wt_kernel(KParams p) {
     constexpr int TI = 2, BM = 64, KMAX = 1024;
     constexpr int P = R / 2;  // activation pieces per thread per ring turn (a piece spans 2 k blocks)
     // Sweeping several slabs pays for the projections with the largest N
@@ -639,7 +660,7 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
     const int nslab = !MULTI ? 1 : (p.tiles_n - bx0 < p.spb ? p.tiles_n - bx0 : p.spb);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int m0 = by * BM;
 
     stage_rows<EPI, false, BM>(p, rl, m0, tid);
@@ -669,9 +690,10 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
             dma16(src, dst);
         }
     };
-    const size_t jstride = (size_t)p.kb_count * 1024;
-    const size_t slab_stride = (size_t)4 * TJ * jstride;  // bytes between column slabs
-    const int8_t *pb0 = p.bp + (size_t)(bx0 * 4 * TJ + wave * TJ) * jstride + lane * 16;
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(p);
+    const int jstride = p.kb_count * 1024;      // bytes between 32-row weight blocks
+    const int slab_stride = 4 * TJ * jstride;   // bytes between column slabs
+    const int pb0 = (bx0 * 4 * TJ + wave * TJ) * jstride;  // this wave's blocks in slab 0
 
     v16i acc[TI][TJ], acc2[TI][TJ];
     v4i rb[R][TJ];
@@ -679,13 +701,13 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
     // block kk - nkr of the next slab (the last slab repeats itself); k
     // blocks are clamped to nkb - 1 (repeats meet zero codes or are never
     // consumed).
-    auto load_b = [&](v4i (&dst)[TJ], const int8_t *cur, const int8_t *nxt, int kk) {
+    auto load_b = [&](v4i (&dst)[TJ], int cur, int nxt, int kk) {
         const bool next = kk >= nkr;
         int kb = next ? kk - nkr : kk;
         kb = kb < nkb ? kb : nkb - 1;
-        const int8_t *src = (next ? nxt : cur) + (size_t)kb * 1024;
+        const int src = (next ? nxt : cur) + kb * 1024;
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) dst[j] = *reinterpret_cast<const v4i *>(src + j * jstride);
+        for (int j = 0; j < TJ; ++j) dst[j] = load_frag(wr, lane * 16, src + j * jstride);
     };
     auto read_a = [&](v4i (&a)[TI], int kb) {
 #pragma unroll
@@ -712,8 +734,8 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
     static_assert(VM < 64, "vmcnt holds 6 bits");
 
     for (int sl = 0; sl < nslab; ++sl) {
-        const int8_t *pcur = pb0 + sl * slab_stride;
-        const int8_t *pnxt = sl + 1 < nslab ? pcur + slab_stride : pcur;
+        const int pcur = pb0 + sl * slab_stride;
+        const int pnxt = sl + 1 < nslab ? pcur + slab_stride : pcur;
         const int nb0 = (bx0 + sl) * 4 * TJ + wave * TJ;
         const ColParams<TJ> cp = load_cols<EPI, TJ>(p, nb0, lane, m0, BM);
 #pragma unroll
@@ -735,17 +757,24 @@ __global__ __launch_bounds__(256) void gemm_wt_kernel(KParams p) {
                 __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (15 << 8) | ((VM >> 4) << 14));
                 __syncthreads();
             }
-            read_a(a0, g);
+            // After a barrier the turn's first fragments are read here;
+            // otherwise the previous turn read them ahead.
+            if (sl == 0 || t == 0) read_a(a0, g);
 #pragma unroll
             for (int u = 0; u < R; u += 2) {
                 read_a(a1, g + u + 1);
+                fence_sched();
                 mma(a0, rb[u]);
                 load_b(rb[u], pcur, pnxt, g + u + R);
-                __builtin_amdgcn_sched_barrier(0);
-                if (u + 2 < R) read_a(a0, g + u + 2);
+                fence_sched();
+                if (u + 2 < R)
+                    read_a(a0, g + u + 2);
+                else if (sl > 0)
+                    read_a(a0, g + R < nkr ? g + R : nkr - 1);
+                fence_sched();
                 mma(a1, rb[u + 1]);
                 load_b(rb[u + 1], pcur, pnxt, g + u + 1 + R);
-                __builtin_amdgcn_sched_barrier(0);
+                fence_sched();
             }
             if (sl == 0) copy_turn(t + 2);
         }
@@ -985,6 +1014,9 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     const bool skinny = a.M <= 32;
     kp.aflip = a.a_signed ? 0 : (int)0x80808080;
     kp.zero16 = static_cast<const uint8_t *>(ctx->zero16);
+    if ((long long)w->Np * w->Kp >= (1LL << 31))
+        return set_error(ctx, "gemm: packed weight of %d x %d bytes exceeds 2 GiB", w->Np, w->Kp);
+    kp.wbytes = w->Np * w->Kp;
     TileCfg t{0, 0};
     Mode mode = MODE_TILE;
     int ring = ctx->gemm_ring ? ctx->gemm_ring : 4;
