@@ -55,7 +55,11 @@ int iro_hip_sync(IroHipContext *ctx);
 void *iro_hip_stream(IroHipContext *ctx);
 /* GEMM tile shape of the context's M > 32 launches: 32*ti rows by 128*tj
    columns (ti in {1,2,4}, tj in {1,2}; ti = 1 implies tj = 2); ti = tj = 0 restores the per-GEMM
-   choice.  A tuning knob: results are identical for every shape.  No
+   choice.  Negative ti selects another schedule knob with value tj:
+   -1 tile order (-1 per GEMM, 0 column slabs first, 1 row tiles first),
+   -2 weight ring depth of the whole-tile kernel (0 default, 4, 8),
+   -3 column slabs per whole-tile block (0 chosen per GEMM, else 1..64).
+   Tuning knobs only: results are identical for every setting.  No
    counterpart in the reference (oneMKL picks its own blocking). */
 int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj);
 

@@ -25,30 +25,35 @@ __device__ __forceinline__ uint32_t codes4(const float4 &v, const RowQ &r, float
     return (uint32_t)a | ((uint32_t)b << 8) | ((uint32_t)c << 16) | ((uint32_t)d << 24);
 }
 
-// Vector path: K % 4 == 0, 16-byte aligned rows, K <= 256*CH.
-template <int CONV, int CH, bool RES>
-__global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ x, int M, int K,
-                                                      int ldx, uint8_t *__restrict__ q1, int ldq,
-                                                      float *__restrict__ s1,
-                                                      int32_t *__restrict__ z1,
-                                                      float *__restrict__ res,
-                                                      uint8_t *__restrict__ q2,
-                                                      float *__restrict__ s2,
-                                                      int32_t *__restrict__ z2, uint32_t sflip) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= M) return;
-    const float *xr = x + (size_t)row * ldx;
-    float4 v[CH];
-    float lo = 0.0f, hi = 0.0f;
+// Vector path, one row held in registers as CH float4 per lane (lane L
+// holds columns 4*(64c + L) .. +3 of chunk c).  EXACT: K == 256*CH, so no
+// column is out of range.
+template <int CH, bool EXACT>
+__device__ __forceinline__ void load_row(const float *__restrict__ xr, int K, int lane,
+                                         float4 (&v)[CH]) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int col = (c * 64 + lane) * 4;
-        if (col < K) {
+        if (EXACT || col < K)
             v[c] = *reinterpret_cast<const float4 *>(xr + col);
-        } else {
+        else
             v[c] = make_float4(0.f, 0.f, 0.f, 0.f);  // zero is inside every range
-        }
+    }
+}
+
+// ops.c:321-348 (and, with RES, ops.c:427-442) on one row already in
+// registers: range, codes (xor sflip), row scale and zero point; the
+// two-term variant forms the remainder in place and quantizes it again.
+template <int CONV, int CH, bool RES, bool EXACT>
+__device__ __forceinline__ void quant_row(float4 (&v)[CH], int row, int K, int lane,
+                                          uint8_t *__restrict__ q1, int ldq,
+                                          float *__restrict__ s1, int32_t *__restrict__ z1,
+                                          float *__restrict__ res, uint8_t *__restrict__ q2,
+                                          float *__restrict__ s2, int32_t *__restrict__ z2,
+                                          uint32_t sflip) {
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
         lo = sel_min(lo, v[c].x); lo = sel_min(lo, v[c].y);
         lo = sel_min(lo, v[c].z); lo = sel_min(lo, v[c].w);
         hi = sel_max(hi, v[c].x); hi = sel_max(hi, v[c].y);
@@ -64,9 +69,9 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
         const int col = (c * 64 + lane) * 4;
         float4 qv;
         const uint32_t packed = codes4<CONV>(v[c], r, RES ? &qv : nullptr);
-        if (col < K) *reinterpret_cast<uint32_t *>(qr + col) = packed ^ sflip;
+        if (EXACT || col < K) *reinterpret_cast<uint32_t *>(qr + col) = packed ^ sflip;
         if (RES) {
-            if (col < K) {
+            if (EXACT || col < K) {
                 v[c].x = residual_value<CONV>(v[c].x, qv.x, r);
                 v[c].y = residual_value<CONV>(v[c].y, qv.y, r);
                 v[c].z = residual_value<CONV>(v[c].z, qv.z, r);
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
         for (int c = 0; c < CH; ++c) {
             const int col = (c * 64 + lane) * 4;
             const uint32_t packed = codes4<CONV>(v[c], r2, nullptr);
-            if (col < K) {
+            if (EXACT || col < K) {
                 *reinterpret_cast<uint32_t *>(q2r + col) = packed ^ sflip;
                 if (rr) *reinterpret_cast<float4 *>(rr + col) = v[c];
             }
@@ -102,6 +107,25 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
             z2[row] = r2.zp;
         }
     }
+}
+
+// Vector path: K % 4 == 0, 16-byte aligned rows, K <= 256*CH (EXACT:
+// K == 256*CH); one wavefront per row.
+template <int CONV, int CH, bool RES, bool EXACT>
+__global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ x, int M, int K,
+                                                      int ldx, uint8_t *__restrict__ q1, int ldq,
+                                                      float *__restrict__ s1,
+                                                      int32_t *__restrict__ z1,
+                                                      float *__restrict__ res,
+                                                      uint8_t *__restrict__ q2,
+                                                      float *__restrict__ s2,
+                                                      int32_t *__restrict__ z2, uint32_t sflip) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    float4 v[CH];
+    load_row<CH, EXACT>(x + (size_t)row * ldx, K, lane, v);
+    quant_row<CONV, CH, RES, EXACT>(v, row, K, lane, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
 }
 
 // Generic path: any K and alignment; the row is re-read from cache.
@@ -285,15 +309,19 @@ int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ld
                      (!RES || !res || (((uintptr_t)res) & 15) == 0);
     const int ch = (K + 255) / 256;
     hipStream_t st = ctx->stream;
-#define IRO_QR(CH)                                                                               \
-    hipLaunchKernelGGL((quant_rows_vec<CONV, CH, RES>), grid, block, 0, st, x, M, K, ldx, q1, ldq, \
-                       s1, z1, res, q2, s2, z2, sflip)
-    if (vec && ch <= 1) IRO_QR(1);
-    else if (vec && ch <= 2) IRO_QR(2);
-    else if (vec && ch <= 4) IRO_QR(4);
-    else if (vec && ch <= 8) IRO_QR(8);
-    else if (vec && ch <= 12) IRO_QR(12);
-    else if (vec && ch <= 16) IRO_QR(16);
+#define IRO_QR(CH, EX)                                                                        \
+    hipLaunchKernelGGL((quant_rows_vec<CONV, CH, RES, EX>), grid, block, 0, st, x, M, K, ldx, q1, \
+                       ldq, s1, z1, res, q2, s2, z2, sflip)
+    // The DiT row widths (1024, 2816) fill whole 256-column chunks: no
+    // per-chunk bounds.
+    if (vec && K == 1024) IRO_QR(4, true);
+    else if (vec && K == 2816) IRO_QR(11, true);
+    else if (vec && ch <= 1) IRO_QR(1, false);
+    else if (vec && ch <= 2) IRO_QR(2, false);
+    else if (vec && ch <= 4) IRO_QR(4, false);
+    else if (vec && ch <= 8) IRO_QR(8, false);
+    else if (vec && ch <= 12) IRO_QR(12, false);
+    else if (vec && ch <= 16) IRO_QR(16, false);
     else
         hipLaunchKernelGGL((quant_rows_any<CONV, RES>), grid, block, 0, st, x, M, K, ldx, q1, ldq,
                            s1, z1, res, q2, s2, z2, sflip);
