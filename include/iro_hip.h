@@ -217,6 +217,21 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
                         int padding, const float *bias, int residual, float *output,
                         int *t_out);
 
+/* dacvae.c:696-795 (convtranspose1d_forward_impl, int8 weight, no snake):
+   input [T_in, C_in] fp32 time-major; w from iro_hip_weight_create_transposed
+   of the [C_in, kernel, C_out] export layout (N = kernel*C_out, K = C_in,
+   dacvae.c:239-243); output [T_out, C_out] with T_out =
+   (T_in-1)*stride - 2*padding + kernel + output_padding (dacvae.c:350-358).
+   The input rows are quantized per row (two-term when residual, the
+   IRO_CODEC_GROUP_UPSAMPLE policy bit), one int8 GEMM forms the expanded
+   [T_in, kernel*C_out] rows, and each output row is bias plus the taps that
+   land on it, added in ascending input row as the reference's scatter
+   loop does.  *t_out (nullable) receives T_out. */
+int iro_hip_convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_in, int C_in,
+                                 const IroHipWeight *w, int C_out, int kernel, int stride,
+                                 int padding, int output_padding, const float *bias,
+                                 int residual, float *output, int *t_out);
+
 /* ---- per-kernel event profiler ----------------------------------------- */
 
 /* While enabled, every kernel launch on the context is bracketed by HIP

@@ -42,7 +42,7 @@ const char *const kProfNames[PK_COUNT] = {
     "quant_rows",        "quant_rows_residual", "gemm_linear",  "gemm_linear_two_term",
     "gemm_qkvg",         "gemm_qkvg_two_term",  "gemm_swiglu",  "gemm_swiglu_two_term",
     "gemm_gated",        "gemm_gated_two_term", "conv_rows",    "conv_im2col",
-    "other"};
+    "convt_gather",      "other"};
 
 struct ProfState {
     struct Rec {
@@ -714,6 +714,46 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
     a.y = output;
     a.ldy = w->N;
     return launch_gemm(ctx, w, a, EPI_LINEAR);
+}
+
+// dacvae.c:696-795 (convtranspose1d_forward_impl with an int8 weight, no
+// snake): quantize the input rows (two-term when `residual`, the
+// IRO_CODEC_GROUP_UPSAMPLE bit of dacvae.c:27-73), one GEMM to the expanded
+// [T_in, kernel*C_out] rows (plane 2 accumulated in the same pass, as the
+// second iro_int8_linear_ex with accumulate = 1), then the bias and the
+// ordered scatter-add as a gather.
+int iro_hip_convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_in, int C_in,
+                                 const IroHipWeight *w, int C_out, int kernel, int stride,
+                                 int padding, int output_padding, const float *bias,
+                                 int residual, float *output, int *t_out) {
+    if (!ctx || !input || !w || !output || T_in <= 0 || C_in <= 0 || C_out <= 0 || kernel <= 0 ||
+        stride <= 0 || padding < 0 || output_padding < 0)
+        return set_error(ctx, "convtranspose1d_int8: invalid arguments");
+    // dacvae.c:350-358
+    const long long To = (long long)(T_in - 1) * stride - 2LL * padding + kernel + output_padding;
+    if (To <= 0 || To > 0x7fffffffLL) return set_error(ctx, "convtranspose1d_int8: empty output");
+    if (w->N != kernel * C_out || w->K != C_in)
+        return set_error(ctx, "convtranspose1d_int8: weight is %d x %d, want %d x %d", w->N, w->K,
+                         kernel * C_out, C_in);
+    const int T_out = (int)To;
+    if (t_out) *t_out = T_out;
+    const size_t ncols = (size_t)kernel * C_out;
+    Workspace ws{ctx};
+    size_t off[6];
+    act_reserve(ws, T_in, C_in, residual != 0, off);
+    const size_t oexp = ws.reserve(sizeof(float) * ncols * T_in);
+    if (ws.commit()) return -1;
+    const ActBufs b = act_at(ws, C_in, residual != 0, off);
+    float *expanded = ws.at<float>(oexp);
+    if (launch_quant_rows(ctx, input, T_in, C_in, C_in, b.q1, b.ld, b.s1, b.z1, nullptr, b.q2,
+                          b.s2, b.z2, true))
+        return -1;
+    GemmArgs a = gemm_args(b, T_in, C_in);
+    a.y = expanded;
+    a.ldy = (int)ncols;
+    if (launch_gemm(ctx, w, a, EPI_LINEAR)) return -1;
+    return launch_convt_gather(ctx, expanded, T_in, C_out, kernel, stride, padding, T_out, bias,
+                               output);
 }
 
 // ---- backend queries -------------------------------------------------------------------

@@ -1,5 +1,7 @@
 // iro_conv.hip -- the DACVAE int8 Conv1d (dacvae.c:543-688) as an implicit
-// GEMM: quantized im2col rows, then the MFMA GEMM of iro_gemm.hip.
+// GEMM: quantized im2col rows, then the MFMA GEMM of iro_gemm.hip; and the
+// scatter-add tail of the int8 ConvTranspose1d (dacvae.c:696-795), whose
+// GEMM is the plain linear of iro_gemm.hip.
 //
 // Quantization is per OUTPUT time step over its whole kernel*C window
 // (dacvae.c:617-636): each input element is coded under up to `kernel`
@@ -141,7 +143,70 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(
     }
 }
 
+// ConvTranspose1d tail (dacvae.c:708-712, 779-790): y[t, c] = bias[c] plus,
+// for every input row r whose taps reach t (tap = t + padding - r*stride in
+// [0, kernel)), expanded[r, tap*C_out + c], added in ascending r exactly as
+// the reference's scatter loop visits them.  A gather: one thread per four
+// output channels of one time step, no atomics, so the order is fixed.
+template <bool VEC>
+__global__ __launch_bounds__(256) void convt_gather_kernel(const float *__restrict__ expanded,
+                                                           int T_in, int C_out, int kernel,
+                                                           int stride, int padding, int T_out,
+                                                           const float *__restrict__ bias,
+                                                           float *__restrict__ y) {
+    const int groups = VEC ? C_out / 4 : C_out;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long long)T_out * groups) return;
+    const int t = (int)(idx / groups);
+    const int c = (int)(idx - (long long)t * groups) * (VEC ? 4 : 1);
+    const int num = t + padding - kernel + 1;
+    int r = num <= 0 ? 0 : (num + stride - 1) / stride;
+    int r_hi = (t + padding) / stride;
+    r_hi = r_hi < T_in - 1 ? r_hi : T_in - 1;
+    const size_t ncols = (size_t)kernel * C_out;
+    if (VEC) {
+        float4 acc = bias ? *reinterpret_cast<const float4 *>(bias + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (; r <= r_hi; ++r) {
+            const int tap = t + padding - r * stride;
+            const float4 e =
+                *reinterpret_cast<const float4 *>(expanded + (size_t)r * ncols + (size_t)tap * C_out + c);
+            acc.x += e.x;
+            acc.y += e.y;
+            acc.z += e.z;
+            acc.w += e.w;
+        }
+        *reinterpret_cast<float4 *>(y + (size_t)t * C_out + c) = acc;
+    } else {
+        float acc = bias ? bias[c] : 0.0f;
+        for (; r <= r_hi; ++r) {
+            const int tap = t + padding - r * stride;
+            acc += expanded[(size_t)r * ncols + (size_t)tap * C_out + c];
+        }
+        y[(size_t)t * C_out + c] = acc;
+    }
+}
+
 }  // namespace
+
+int launch_convt_gather(IroHipContext *ctx, const float *expanded, int T_in, int C_out,
+                        int kernel, int stride, int padding, int T_out, const float *bias,
+                        float *y) {
+    const bool vec = C_out % 4 == 0 && (((uintptr_t)expanded | (uintptr_t)y) & 15) == 0 &&
+                     (!bias || (((uintptr_t)bias) & 15) == 0);
+    const long long n = (long long)T_out * (vec ? C_out / 4 : C_out);
+    const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    prof_begin(ctx);
+    if (vec)
+        hipLaunchKernelGGL((convt_gather_kernel<true>), grid, block, 0, ctx->stream, expanded, T_in,
+                           C_out, kernel, stride, padding, T_out, bias, y);
+    else
+        hipLaunchKernelGGL((convt_gather_kernel<false>), grid, block, 0, ctx->stream, expanded,
+                           T_in, C_out, kernel, stride, padding, T_out, bias, y);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    // Each expanded value is read once, each output written once.
+    prof_end(ctx, PK_CONVT_GATHER, 0, 4.0 * T_in * kernel * C_out + 4.0 * T_out * C_out);
+    return 0;
+}
 
 int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi) {
     prof_begin(ctx);

@@ -23,6 +23,7 @@ enum ProfKind {
     PK_GEMM_GATED_2T,
     PK_CONV_ROWS,
     PK_CONV_IM2COL,
+    PK_CONVT_GATHER,
     PK_OTHER,
     PK_COUNT
 };
@@ -223,6 +224,9 @@ inline GemmArgs gemm_args(const ActBufs &b, int M, int K) {
 }
 
 int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi);
+int launch_convt_gather(IroHipContext *ctx, const float *expanded, int T_in, int C_out,
+                        int kernel, int stride, int padding, int T_out, const float *bias,
+                        float *y);
 int launch_conv_im2col(IroHipContext *ctx, const float *x, int T, int C, int T_out, int kernel,
                        int stride, int dilation, int padding, const float *row_lo,
                        const float *row_hi, uint8_t *cols1, uint8_t *cols2, int ldc, float *s1,

@@ -83,6 +83,8 @@ def load() -> C.CDLL:
         "iro_hip_dit_swiglu": ([_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i], _i),
         "iro_hip_conv1d_int8": ([_vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _vp, _i, _vp,
                                  C.POINTER(_i)], _i),
+        "iro_hip_convtranspose1d_int8": ([_vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _i, _vp, _i,
+                                          _vp, C.POINTER(_i)], _i),
         "iro_hip_dit_stack_create": ([_vp, _i, _i, _i, _i, C.POINTER(_vp)], _i),
         "iro_hip_dit_stack_set_block": ([_vp, _i] + [_vp] * 9, _i),
         "iro_hip_dit_stack_step": ([_vp, _vp, _vp, _i, _i], _i),
@@ -359,6 +361,16 @@ class Context:
             self.h, x.vp, T, Cin, w.h, kernel, stride, dilation, padding,
             None if bias is None else bias.vp, int(bool(residual)), y.vp, C.byref(t_out)),
             "conv1d_int8")
+        return t_out.value
+
+    def convtranspose1d(self, x, T_in, Cin, w, Cout, kernel, stride, padding, output_padding,
+                        bias, residual, y):
+        """dacvae.c:696-795 int8 ConvTranspose1d (no snake); returns T_out."""
+        t_out = C.c_int()
+        self._check(self.lib.iro_hip_convtranspose1d_int8(
+            self.h, x.vp, T_in, Cin, w.h, Cout, kernel, stride, padding, output_padding,
+            None if bias is None else bias.vp, int(bool(residual)), y.vp, C.byref(t_out)),
+            "convtranspose1d_int8")
         return t_out.value
 
 

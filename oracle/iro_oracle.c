@@ -471,3 +471,70 @@ int orc_conv1d_int8(int conv, const float *input, int T, int C,
     free(c2); free(s1); free(z1); free(s2); free(z2); free(work);
     return ok ? T_out : -1;
 }
+
+/* ---- int8 ConvTranspose1d: dacvae.c:350-358, 696-795 -------------------- */
+
+int orc_convtranspose1d_output_length(int T_in, int kernel, int stride,
+                                      int padding, int output_padding) {
+    if (T_in <= 0 || stride <= 0 || kernel <= 0) return -1;
+    long long out = (long long)(T_in - 1) * stride - 2LL * padding + kernel +
+                    output_padding;
+    return out <= 0 || out > 0x7fffffffLL ? -1 : (int)out;
+}
+
+/* Without snake: every output row starts at the bias; the input rows are
+   quantized (two-term with `residual`), one int8 linear gives the expanded
+   rows [T_in, kernel*C_out] (plane 2 accumulated by a second linear), and
+   the taps are scattered onto the output in ascending input row, tap and
+   channel order, each add rounded on its own. */
+int orc_convtranspose1d_int8(int conv, const float *input, int T_in, int C_in,
+                             const int8_t *wq, const float *sw,
+                             const int32_t *colsum, int C_out, int kernel,
+                             int stride, int padding, int output_padding,
+                             const float *bias, int residual, float *output,
+                             int threads) {
+    const int T_out = orc_convtranspose1d_output_length(T_in, kernel, stride,
+                                                        padding, output_padding);
+    if (T_out <= 0 || C_in <= 0 || C_out <= 0) return -1;
+    const int N = kernel * C_out;
+    for (int t = 0; t < T_out; t++)
+        for (int c = 0; c < C_out; c++)
+            output[(size_t)t * C_out + c] = bias ? bias[c] : 0.0f;
+    uint8_t *q1 = malloc((size_t)T_in * C_in);
+    uint8_t *q2 = residual ? malloc((size_t)T_in * C_in) : NULL;
+    float *s1 = malloc(sizeof(float) * (size_t)T_in);
+    float *s2 = malloc(sizeof(float) * (size_t)T_in);
+    int32_t *z1 = malloc(sizeof(int32_t) * (size_t)T_in);
+    int32_t *z2 = malloc(sizeof(int32_t) * (size_t)T_in);
+    float *rem = residual ? malloc(sizeof(float) * (size_t)T_in * C_in) : NULL;
+    float *expanded = malloc(sizeof(float) * (size_t)T_in * N);
+    int32_t *work = malloc(sizeof(int32_t) * (size_t)T_in * N);
+    int ok = q1 && s1 && s2 && z1 && z2 && expanded && work && (!residual || (q2 && rem));
+    if (ok) {
+        if (residual) {
+            orc_quantize_rows_residual(conv, input, T_in, C_in, q1, s1, z1, rem, q2, s2, z2);
+            orc_int8_linear_ex(conv, q1, s1, z1, wq, sw, colsum, N, C_in, NULL, expanded,
+                               T_in, work, 0, threads);
+            orc_int8_linear_ex(conv, q2, s2, z2, wq, sw, colsum, N, C_in, NULL, expanded,
+                               T_in, work, 1, threads);
+        } else {
+            orc_quantize_rows(conv, input, T_in, C_in, q1, s1, z1);
+            orc_int8_linear_ex(conv, q1, s1, z1, wq, sw, colsum, N, C_in, NULL, expanded,
+                               T_in, work, 0, threads);
+        }
+        for (int row = 0; row < T_in; row++) {
+            const int base = row * stride - padding;
+            const float *src = expanded + (size_t)row * N;
+            for (int tap = 0; tap < kernel; tap++) {
+                const int t = base + tap;
+                if (t < 0 || t >= T_out) continue;
+                float *dst = output + (size_t)t * C_out;
+                const float *k = src + (size_t)tap * C_out;
+                for (int c = 0; c < C_out; c++) dst[c] += k[c];
+            }
+        }
+    }
+    free(q1); free(q2); free(s1); free(s2); free(z1); free(z2);
+    free(rem); free(expanded); free(work);
+    return ok ? T_out : -1;
+}

@@ -105,6 +105,21 @@ int orc_conv1d_quantize(int conv, const float *input, int T, int C, int kernel,
                         float *s1, int32_t *z1, uint8_t *c2, float *s2,
                         int32_t *z2);
 
+/* dacvae.c:350-358 (iro_convtranspose1d_output_length). */
+int orc_convtranspose1d_output_length(int T_in, int kernel, int stride,
+                                      int padding, int output_padding);
+
+/* dacvae.c:696-795 (convtranspose1d_forward_impl) with an int8 weight and
+   no snake: input [T_in, C_in], weight codes [kernel*C_out, C_in] (the
+   transposed quantization of the [C_in, kernel, C_out] export layout),
+   output [T_out, C_out].  Returns T_out, or -1. */
+int orc_convtranspose1d_int8(int conv, const float *input, int T_in, int C_in,
+                             const int8_t *wq, const float *sw,
+                             const int32_t *colsum, int C_out, int kernel,
+                             int stride, int padding, int output_padding,
+                             const float *bias, int residual, float *output,
+                             int threads);
+
 /* dacvae.c:340-348 (iro_conv1d_output_length). */
 int orc_conv1d_output_length(int T, int kernel, int stride, int dilation,
                              int padding);

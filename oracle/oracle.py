@@ -65,6 +65,12 @@ class Oracle:
         L.orc_conv1d_int8.restype = C.c_int
         L.orc_conv1d_output_length.argtypes = [C.c_int] * 5
         L.orc_conv1d_output_length.restype = C.c_int
+        L.orc_convtranspose1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p,
+                                               _i32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                               _f32p, C.c_int, _f32p, C.c_int]
+        L.orc_convtranspose1d_int8.restype = C.c_int
+        L.orc_convtranspose1d_output_length.argtypes = [C.c_int] * 5
+        L.orc_convtranspose1d_output_length.restype = C.c_int
         self.threads = min(8, os.cpu_count() or 1)
 
     def weight_quantize(self, conv, w):
@@ -187,6 +193,26 @@ class Oracle:
         assert rc == To
         return y, cols, s, z
 
+    def convt_out_len(self, T_in, kernel, stride, padding, output_padding):
+        return self.lib.orc_convtranspose1d_output_length(T_in, kernel, stride, padding,
+                                                          output_padding)
+
+    def convtranspose1d(self, conv, x, wq, sw, colsum, C_out, kernel, stride, padding,
+                        output_padding, bias=None, residual=False):
+        """dacvae.c:696-795 without snake; wq [kernel*C_out, C_in]."""
+        x = _f32(x)
+        T_in, Cin = x.shape
+        To = self.convt_out_len(T_in, kernel, stride, padding, output_padding)
+        assert To > 0
+        y = np.empty((To, C_out), np.float32)
+        rc = self.lib.orc_convtranspose1d_int8(
+            conv, _p(x, _f32p), T_in, Cin, _p(np.ascontiguousarray(wq, np.int8), _i8p),
+            _p(_f32(sw), _f32p), _p(np.ascontiguousarray(colsum, np.int32), _i32p), C_out, kernel,
+            stride, padding, output_padding, _p(None if bias is None else _f32(bias), _f32p),
+            int(bool(residual)), _p(y, _f32p), self.threads)
+        assert rc == To
+        return y
+
 
 class _Weight(C.Structure):
     # ops.h:23-28 IroInt8Weight
@@ -217,6 +243,9 @@ class Reference:
         L.ref_conv1d_int8.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                       C.c_int, _i8p, _f32p, _i32p, _f32p, C.c_int, _f32p]
         L.ref_conv1d_int8.restype = C.c_int
+        L.ref_convtranspose1d_int8.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                               C.c_int, C.c_int, _i8p, _f32p, _i32p, _f32p, _f32p]
+        L.ref_convtranspose1d_int8.restype = C.c_int
 
     def weight_quantize(self, w, transposed_shape=None):
         w = _f32(w)
@@ -293,6 +322,20 @@ class Reference:
                                       _p(np.ascontiguousarray(colsum, np.int32), _i32p),
                                       _p(None if bias is None else _f32(bias), _f32p),
                                       int(bool(residual)), _p(y, _f32p))
+        assert rc == 0
+        return y
+
+    def convtranspose1d(self, x, wq, sw, colsum, C_out, kernel, stride, padding, output_padding,
+                        bias, out_len):
+        """The reference's convtranspose1d_forward_impl (int8, no snake); its
+        two-term choice follows IRO_CODEC_INT8_RESIDUAL, read once per process."""
+        x = _f32(x)
+        T_in, Cin = x.shape
+        y = np.empty((out_len, C_out), np.float32)
+        rc = self.lib.ref_convtranspose1d_int8(
+            _p(x, _f32p), T_in, Cin, C_out, kernel, stride, padding, output_padding,
+            _p(np.ascontiguousarray(wq, np.int8), _i8p), _p(_f32(sw), _f32p),
+            _p(np.ascontiguousarray(colsum, np.int32), _i32p), _p(_f32(bias), _f32p), _p(y, _f32p))
         assert rc == 0
         return y
 

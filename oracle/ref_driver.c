@@ -28,3 +28,29 @@ int ref_conv1d_int8(const float *input, int T, int C, int N, int kernel,
     return conv1d_int8_forward(&conv, &w, input, T, output, bias, NULL,
                                residual, NULL, NULL, NULL);
 }
+
+/* The int8 ConvTranspose1d without snake (dacvae.c:696-795); its two-term
+   choice follows the reference's own policy (dacvae.c:27-73: off for the
+   upsample group unless IRO_CODEC_INT8_RESIDUAL says otherwise). */
+int ref_convtranspose1d_int8(const float *input, int T_in, int C_in, int C_out,
+                             int kernel, int stride, int padding,
+                             int output_padding, int8_t *wq, float *sw,
+                             int32_t *colsum, const float *bias,
+                             float *output) {
+    IroConvTranspose1d conv = {0};
+    conv.bias = bias;
+    conv.in_channels = C_in;
+    conv.out_channels = C_out;
+    conv.kernel = kernel;
+    conv.stride = stride;
+    conv.padding = padding;
+    conv.output_padding = output_padding;
+    IroInt8Weight w = {0};
+    w.data = wq;
+    w.scale = sw;
+    w.colsum = colsum;
+    w.N = kernel * C_out;
+    w.K = C_in;
+    return convtranspose1d_forward_impl(&conv, &w, input, T_in, output, NULL,
+                                        NULL, 0);
+}

@@ -55,3 +55,32 @@ def test_conv_small(ctx, oracle, T, C, N, k, st, dil, pad, residual):
 def test_conv_baseline_shapes(ctx, oracle, T, C, N, dil, pad):
     got, want = _conv(ctx, oracle, T, C, N, 7, 1, dil, pad, 0, 90, zero_band=False)
     assert_bits_equal(got, want, "conv output")
+
+
+# (T_in, C_in, C_out, kernel, stride, padding, output_padding); the first
+# four are the decoder's upsampling geometry at its rates 12/10/8/2
+# (dacvae.c:150-160, 177-179) on short inputs, the last is stage 0 at full
+# width on 200 latent frames.
+CONVT_CASES = [(37, 48, 16, 24, 12, 6, 0), (20, 40, 24, 20, 10, 5, 0), (31, 32, 8, 16, 8, 4, 0),
+               (50, 24, 12, 4, 2, 1, 0), (9, 16, 8, 6, 3, 2, 1), (1, 8, 4, 4, 2, 1, 0),
+               (13, 12, 20, 3, 1, 0, 0), (11, 8, 8, 2, 3, 0, 2), (200, 1536, 768, 24, 12, 6, 0)]
+
+
+@pytest.mark.parametrize("T,Ci,Co,k,st,pad,opad", CONVT_CASES)
+@pytest.mark.parametrize("residual", [0, 1], ids=["one-plane", "two-plane"])
+def test_convtranspose(ctx, oracle, T, Ci, Co, k, st, pad, opad, residual):
+    conv = ctx.convention
+    x = gauss(80 + T, (T, Ci))
+    if T > 8:
+        x[3:6] = 0.0
+    w_export = gauss(81 + T, (Ci, k * Co), 0.02)  # [C_in, kernel, C_out]
+    b = gauss(82 + T, (Co,), 0.01)
+    W = ctx.weight(ctx.to_device(w_export), k * Co, Ci, transposed=True)
+    To = oracle.convt_out_len(T, k, st, pad, opad)
+    yd = ctx.empty((To, Co), np.float32)
+    got_len = ctx.convtranspose1d(ctx.to_device(x), T, Ci, W, Co, k, st, pad, opad,
+                                  ctx.to_device(b), residual, yd)
+    assert got_len == To
+    wq = oracle.weight_quantize_transposed(conv, w_export, k * Co, Ci)
+    want = oracle.convtranspose1d(conv, x, *wq, Co, k, st, pad, opad, bias=b, residual=residual)
+    assert_bits_equal(yd.numpy(), want, "convtranspose output")

@@ -106,6 +106,69 @@ def test_oracle_conv_matches_reference_build(oracle, conv, flavour, T, C, N, k, 
     assert _eq(yo, yr)
 
 
+# (T_in, C_in, C_out, kernel, stride, padding, output_padding): the decoder's
+# upsampling layers use kernel 2*rate, stride rate, padding (rate+1)/2,
+# output_padding rate&1 (dacvae.c:150-160, rates 12/10/8/2, dacvae.c:177-179);
+# the rest cover T_in = 1, odd rates, padding 0 and kernel < stride.
+CONVT_CASES = [(37, 48, 16, 24, 12, 6, 0), (20, 40, 24, 20, 10, 5, 0), (31, 32, 8, 16, 8, 4, 0),
+               (50, 24, 12, 4, 2, 1, 0), (9, 16, 8, 6, 3, 2, 1), (1, 8, 4, 4, 2, 1, 0),
+               (13, 12, 20, 3, 1, 0, 0), (11, 8, 8, 2, 3, 0, 2)]
+
+
+def _convt_inputs(oracle, conv, T, Ci, Co, k, seed):
+    x = gauss(seed, (T, Ci))
+    if T > 8:
+        x[3:6] = 0.0  # all-zero rows: scale 1, zero point 0
+    w_export = gauss(seed + 1, (Ci, k * Co), 0.02)  # [C_in, kernel, C_out] export layout
+    b = gauss(seed + 2, (Co,), 0.01)
+    wq = oracle.weight_quantize_transposed(conv, w_export, k * Co, Ci)
+    return x, w_export, b, wq
+
+
+@pytest.mark.parametrize("conv,flavour", CONVS, ids=["strict", "fastmath"])
+@pytest.mark.parametrize("T,Ci,Co,k,st,pad,opad", CONVT_CASES)
+def test_oracle_convtranspose_matches_reference_build(oracle, conv, flavour, T, Ci, Co, k, st,
+                                                      pad, opad):
+    ref = _ref(flavour)
+    x, _, b, wq = _convt_inputs(oracle, conv, T, Ci, Co, k, 80 + T)
+    To = oracle.convt_out_len(T, k, st, pad, opad)
+    yr = ref.convtranspose1d(x, *wq, Co, k, st, pad, opad, b, To)
+    yo = oracle.convtranspose1d(conv, x, *wq, Co, k, st, pad, opad, bias=b)
+    assert _eq(yo, yr)
+
+
+def test_oracle_convtranspose_two_term_matches_reference_build():
+    # The reference takes the two-term path only under its upsample policy
+    # bit (dacvae.c:54-62, IRO_CODEC_INT8_RESIDUAL read once per process),
+    # so this pin runs in a child process with that bit set.
+    _ref("strict")
+    import subprocess
+    import sys
+    code = (
+        "import sys, numpy as np\n"
+        f"sys.path[:0] = {[HERE, os.path.join(os.path.dirname(HERE), 'irodori-c_amd')]!r}\n"
+        "from oracle import Oracle, Reference, STRICT, GCC_FASTMATH\n"
+        "from iro_synth import gauss\n"
+        "o = Oracle()\n"
+        "for conv, fl in ((STRICT, 'strict'), (GCC_FASTMATH, 'fast')):\n"
+        "    ref = Reference(fl)\n"
+        "    for T, Ci, Co, k, st, pad, opad in ((37, 48, 16, 24, 12, 6, 0), (9, 16, 8, 6, 3, 2, 1)):\n"
+        "        x = gauss(90 + T, (T, Ci)); x[3:6] = 0.0\n"
+        "        w = gauss(91 + T, (Ci, k * Co), 0.02); b = gauss(92 + T, (Co,), 0.01)\n"
+        "        wq = o.weight_quantize_transposed(conv, w, k * Co, Ci)\n"
+        "        To = o.convt_out_len(T, k, st, pad, opad)\n"
+        "        yr = ref.convtranspose1d(x, *wq, Co, k, st, pad, opad, b, To)\n"
+        "        yo = o.convtranspose1d(conv, x, *wq, Co, k, st, pad, opad, bias=b, residual=True)\n"
+        "        y1 = o.convtranspose1d(conv, x, *wq, Co, k, st, pad, opad, bias=b, residual=False)\n"
+        "        assert np.array_equal(yo.view(np.int32), yr.view(np.int32)), (fl, T)\n"
+        "        assert not np.array_equal(y1.view(np.int32), yr.view(np.int32)), (fl, T)\n"
+        "print('ok')\n")
+    env = dict(os.environ, IRO_CODEC_INT8_RESIDUAL="2")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", out.stderr[-2000:]
+
+
 def test_oracle_silu_matches_strict_reference_build(oracle):
     ref = _ref("strict")
     a = gauss(3, (200000,), 4.0)
