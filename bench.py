@@ -13,7 +13,10 @@ The fp32 attention core and RMSNorm-modulate are not part of the stack.
 
 `--workload conv7` (T=24000, 512->512, kernel 7, padding 3) and
 `--workload conv7-dil3` (T=6000, 1024->256, dilation 3, padding 9) measure
-the codec's int8 Conv1d instead: one conv per step, same JSON line.
+the codec's int8 Conv1d instead: one conv per step, same JSON line;
+`--workload convt-stage0` / `convt-stage2` the decoder's int8 upsampling
+ConvTranspose1d (stage 0: 750 frames, 1536->768, kernel 24, stride 12;
+stage 2: 90000 frames, 384->192, kernel 16, stride 8).
 
 Prints one JSON line on stdout; diagnostics go to stderr.
 """
@@ -112,6 +115,12 @@ def cpu_baseline(args, base, x0, cond, D, H, ops_per_step):
 CONV_WORKLOADS = {  # T, C_in, C_out, kernel, stride, dilation, padding
     "conv7": (24000, 512, 512, 7, 1, 1, 3),
     "conv7-dil3": (6000, 1024, 256, 7, 1, 3, 9),
+}
+# Decoder upsampling ConvTranspose1d (dacvae.c:150-160, 177-179) on 750
+# latent frames: T_in, C_in, C_out, kernel, stride, padding, output_padding.
+CONVT_WORKLOADS = {
+    "convt-stage0": (750, 1536, 768, 24, 12, 6, 0),
+    "convt-stage2": (90000, 384, 192, 16, 8, 4, 0),
 }
 
 
@@ -240,6 +249,107 @@ def conv_main(args):
     print(json.dumps(out), flush=True)
 
 
+def convt_main(args):
+    """The codec's int8 ConvTranspose1d (dacvae.c:696-795, no snake): one step
+    = row quantization, the GEMM to the expanded taps and the ordered
+    gather-add with bias, input and weights resident in HBM."""
+    T, Cin, Co, k, st, pad, opad = CONVT_WORKLOADS[args.workload]
+    To = (T - 1) * st - 2 * pad + k + opad
+    planes = 2 if args.conv_residual else 1
+    ops = 2 * T * k * Co * Cin * planes
+    conv = iro_hip.STRICT if args.convention == "strict" else iro_hip.GCC_FASTMATH
+    x = gauss(42, (T, Cin))
+    w = gauss(43, (Cin, k * Co), 0.02)  # [C_in, kernel, C_out] export layout
+    b = gauss(44, (Co,), 0.01)
+    ctx = iro_hip.Context(0, conv)
+    log("backend:", ctx.backend())
+    wd = ctx.to_device(w)
+    W = ctx.weight(wd, k * Co, Cin, transposed=True)
+    wd.free()
+    xd, bd = ctx.to_device(x), ctx.to_device(b)
+    y = ctx.empty((To, Co), np.float32)
+
+    def step():
+        ctx.convtranspose1d(xd, T, Cin, W, Co, k, st, pad, opad, bd, args.conv_residual, y)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    log(f"{args.workload}: {ms_step:.3f} ms/step wall")
+    ctx.profile(True)
+    for _ in range(args.profile_steps):
+        step()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    kernels = log_profile(prof)
+    roof = roofline_of(prof)
+    ygpu = y.numpy()
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import Oracle
+        threads = min(16, len(os.sched_getaffinity(0)))
+        o = Oracle()
+        o.threads = threads
+        cv = 0 if conv == iro_hip.STRICT else 1
+        wq = o.weight_quantize_transposed(cv, w, k * Co, Cin)
+        # Bounded sample: the first rows of the input (the work is linear in
+        # T_in), timed as the oracle's restatement with its OpenMP GEMM.
+        Ts = T
+        while 2.0 * Ts * k * Co * Cin * planes > 40e9 and Ts > 16:
+            Ts //= 2
+        xs = np.ascontiguousarray(x[:Ts])
+        t1 = time.perf_counter()
+        ycpu = o.convtranspose1d(cv, xs, *wq, Co, k, st, pad, opad, bias=b,
+                                 residual=args.conv_residual)
+        sec = time.perf_counter() - t1
+        Tso = (Ts - 1) * st - 2 * pad + k + opad
+        # Rows the sample's last input row does not finish differ only in
+        # the missing contributions; compare the rows it completes.
+        full = max(0, (Ts - 1) * st - pad)
+        same = bool(np.array_equal(ycpu[:full].view(np.uint32), ygpu[:full].view(np.uint32)))
+        sops = 2.0 * Ts * k * Co * Cin * planes
+        log(f"cpu baseline: T_in sample {Ts} ({sops / 1e9:.1f} GOP) in {sec:.2f}s on {threads} "
+            f"threads (oracle restatement); completed rows bit-identical to the GPU: {same}")
+        cpu = {"value": round(sops / sec / 1e12, 4), "unit": "TOPS", "cores": threads,
+               "kind": "port", "ms_per_step": round(sec * ops / sops * 1e3, 2),
+               "sample": (f"the first {Ts} of {T} input rows ({Tso} output rows), oracle "
+                          f"restatement with its OpenMP GEMM on {threads} threads, scaled by work"),
+               "gpu_output_bit_identical": same}
+
+    out = {
+        "metric": f"int8 ConvTranspose1d TOPS ({args.workload}), 1 GPU",
+        "value": round(ops * args.steps / wall / 1e12, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded Irwin-Hall Gaussian input, random-init weights)",
+        "config": {"workload": (f"int8 ConvTranspose1d T_in={T}, {Cin}->{Co}, kernel {k}, stride "
+                                f"{st}, padding {pad}, output_padding {opad}, {planes} plane(s), "
+                                f"bias; one layer per step"),
+                   "T_in": T, "T_out": To, "c_in": Cin, "c_out": Co, "kernel": k, "stride": st,
+                   "planes": planes, "ops_per_step": ops, "convention": args.convention,
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,8 +365,10 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["stack"] + sorted(CONV_WORKLOADS), default="stack",
-                    help="stack (default): the DiT linear stack; conv7*: the codec int8 Conv1d")
+    ap.add_argument("--workload", choices=["stack"] + sorted(CONV_WORKLOADS) + sorted(CONVT_WORKLOADS),
+                    default="stack",
+                    help="stack (default): the DiT linear stack; conv7*: the codec int8 Conv1d; "
+                         "convt-*: the codec int8 ConvTranspose1d")
     ap.add_argument("--conv-residual", action="store_true",
                     help="conv workloads: add the fixed-scale second plane")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -281,8 +393,11 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(--gpus must be 1)", file=sys.stderr)
         sys.exit(2)
-    if args.workload != "stack":
+    if args.workload in CONV_WORKLOADS:
         conv_main(args)
+        return
+    if args.workload in CONVT_WORKLOADS:
+        convt_main(args)
         return
 
     B, S, D, H = args.batch, args.frames, args.hidden, args.mlp

@@ -85,6 +85,7 @@ def load() -> C.CDLL:
                                  C.POINTER(_i)], _i),
         "iro_hip_convtranspose1d_int8": ([_vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _i, _vp, _i,
                                           _vp, C.POINTER(_i)], _i),
+        "iro_hip_conv1x1_skip_int8": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp], _i),
         "iro_hip_dit_stack_create": ([_vp, _i, _i, _i, _i, C.POINTER(_vp)], _i),
         "iro_hip_dit_stack_set_block": ([_vp, _i] + [_vp] * 9, _i),
         "iro_hip_dit_stack_step": ([_vp, _vp, _vp, _i, _i], _i),
@@ -372,6 +373,12 @@ class Context:
             None if bias is None else bias.vp, int(bool(residual)), y.vp, C.byref(t_out)),
             "convtranspose1d_int8")
         return t_out.value
+
+    def conv1x1_skip(self, hidden, skip, T, w, bias, residual, out):
+        """dacvae.c:974-1012: out = skip + conv1(hidden) + bias (int8)."""
+        self._check(self.lib.iro_hip_conv1x1_skip_int8(
+            self.h, hidden.vp, skip.vp, T, w.h, None if bias is None else bias.vp,
+            int(bool(residual)), out.vp), "conv1x1_skip_int8")
 
 
     # -- profiler ----------------------------------------------------------------------

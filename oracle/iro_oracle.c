@@ -538,3 +538,38 @@ int orc_convtranspose1d_int8(int conv, const float *input, int T_in, int C_in,
     free(rem); free(expanded); free(work);
     return ok ? T_out : -1;
 }
+
+/* ---- int8 1x1 projection onto the skip: dacvae.c:974-1012 --------------- */
+
+/* output = skip, then the reference's two accumulating linears:
+   output += lin(q1) + bias; with residual, output += lin(q2). */
+int orc_conv1x1_skip_int8(int conv, const float *hidden, const float *skip,
+                          int T, const int8_t *wq, const float *sw,
+                          const int32_t *colsum, int C_out, int C_in,
+                          const float *bias, int residual, float *output,
+                          int threads) {
+    if (T <= 0 || C_in <= 0 || C_out <= 0) return -1;
+    memmove(output, skip, sizeof(float) * (size_t)T * C_out);
+    uint8_t *q1 = malloc((size_t)T * C_in);
+    uint8_t *q2 = residual ? malloc((size_t)T * C_in) : NULL;
+    float *s1 = malloc(sizeof(float) * (size_t)T), *s2 = malloc(sizeof(float) * (size_t)T);
+    int32_t *z1 = malloc(sizeof(int32_t) * (size_t)T), *z2 = malloc(sizeof(int32_t) * (size_t)T);
+    float *rem = residual ? malloc(sizeof(float) * (size_t)T * C_in) : NULL;
+    int32_t *work = malloc(sizeof(int32_t) * (size_t)T * C_out);
+    int ok = q1 && s1 && s2 && z1 && z2 && work && (!residual || (q2 && rem));
+    if (ok) {
+        if (residual) {
+            orc_quantize_rows_residual(conv, hidden, T, C_in, q1, s1, z1, rem, q2, s2, z2);
+            orc_int8_linear_ex(conv, q1, s1, z1, wq, sw, colsum, C_out, C_in, bias, output,
+                               T, work, 1, threads);
+            orc_int8_linear_ex(conv, q2, s2, z2, wq, sw, colsum, C_out, C_in, NULL, output,
+                               T, work, 1, threads);
+        } else {
+            orc_quantize_rows(conv, hidden, T, C_in, q1, s1, z1);
+            orc_int8_linear_ex(conv, q1, s1, z1, wq, sw, colsum, C_out, C_in, bias, output,
+                               T, work, 1, threads);
+        }
+    }
+    free(q1); free(q2); free(s1); free(s2); free(z1); free(z2); free(rem); free(work);
+    return ok ? 0 : -1;
+}

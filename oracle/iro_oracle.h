@@ -120,6 +120,15 @@ int orc_convtranspose1d_int8(int conv, const float *input, int T_in, int C_in,
                              const float *bias, int residual, float *output,
                              int threads);
 
+/* dacvae.c:974-1012 (the int8 1x1 projection of run_residual_int8):
+   output = skip + lin(q1) + bias (+ lin(q2) with residual), hidden [T, C_in]
+   quantized per row, weight codes [C_out, C_in]; output may equal skip. */
+int orc_conv1x1_skip_int8(int conv, const float *hidden, const float *skip,
+                          int T, const int8_t *wq, const float *sw,
+                          const int32_t *colsum, int C_out, int C_in,
+                          const float *bias, int residual, float *output,
+                          int threads);
+
 /* dacvae.c:340-348 (iro_conv1d_output_length). */
 int orc_conv1d_output_length(int T, int kernel, int stride, int dilation,
                              int padding);

@@ -71,6 +71,9 @@ class Oracle:
         L.orc_convtranspose1d_int8.restype = C.c_int
         L.orc_convtranspose1d_output_length.argtypes = [C.c_int] * 5
         L.orc_convtranspose1d_output_length.restype = C.c_int
+        L.orc_conv1x1_skip_int8.argtypes = [C.c_int, _f32p, _f32p, C.c_int, _i8p, _f32p, _i32p,
+                                            C.c_int, C.c_int, _f32p, C.c_int, _f32p, C.c_int]
+        L.orc_conv1x1_skip_int8.restype = C.c_int
         self.threads = min(8, os.cpu_count() or 1)
 
     def weight_quantize(self, conv, w):
@@ -192,6 +195,21 @@ class Oracle:
                                       _p(s, _f32p), _p(z, _i32p), self.threads)
         assert rc == To
         return y, cols, s, z
+
+    def conv1x1_skip(self, conv, hidden, skip, wq, sw, colsum, bias=None, residual=False):
+        """dacvae.c:974-1012: skip + lin(q1) + bias (+ lin(q2)); wq [C_out, C_in]."""
+        hidden = _f32(hidden)
+        T, Cin = hidden.shape
+        Cout = wq.shape[0]
+        out = np.empty((T, Cout), np.float32)
+        rc = self.lib.orc_conv1x1_skip_int8(
+            conv, _p(hidden, _f32p), _p(_f32(skip), _f32p), T,
+            _p(np.ascontiguousarray(wq, np.int8), _i8p), _p(_f32(sw), _f32p),
+            _p(np.ascontiguousarray(colsum, np.int32), _i32p), Cout, Cin,
+            _p(None if bias is None else _f32(bias), _f32p), int(bool(residual)), _p(out, _f32p),
+            self.threads)
+        assert rc == 0
+        return out
 
     def convt_out_len(self, T_in, kernel, stride, padding, output_padding):
         return self.lib.orc_convtranspose1d_output_length(T_in, kernel, stride, padding,

@@ -84,3 +84,22 @@ def test_convtranspose(ctx, oracle, T, Ci, Co, k, st, pad, opad, residual):
     wq = oracle.weight_quantize_transposed(conv, w_export, k * Co, Ci)
     want = oracle.convtranspose1d(conv, x, *wq, Co, k, st, pad, opad, bias=b, residual=residual)
     assert_bits_equal(yd.numpy(), want, "convtranspose output")
+
+
+@pytest.mark.parametrize("T,C", [(40, 96), (7, 24), (3000, 192), (1200, 768)])
+@pytest.mark.parametrize("residual", [0, 1], ids=["one-plane", "two-plane"])
+@pytest.mark.parametrize("in_place", [False, True], ids=["out", "in-place"])
+def test_conv1x1_skip(ctx, oracle, T, C, residual, in_place):
+    conv = ctx.convention
+    hidden = gauss(60 + T, (T, C))
+    hidden[2:4] = 0.0
+    skip = gauss(61 + T, (T, C))
+    w = gauss(62, (C, C), 0.02)
+    b = gauss(63, (C,), 0.01)
+    W = ctx.weight(ctx.to_device(w), C, C)
+    sd = ctx.to_device(skip)
+    out = sd if in_place else ctx.empty((T, C), np.float32)
+    ctx.conv1x1_skip(ctx.to_device(hidden), sd, T, W, ctx.to_device(b), residual, out)
+    want = oracle.conv1x1_skip(conv, hidden, skip, *oracle.weight_quantize(conv, w), bias=b,
+                               residual=residual)
+    assert_bits_equal(out.numpy(), want, "conv1x1 onto skip")

@@ -169,6 +169,33 @@ def test_oracle_convtranspose_two_term_matches_reference_build():
     assert out.returncode == 0 and out.stdout.strip() == "ok", out.stderr[-2000:]
 
 
+@pytest.mark.parametrize("conv,flavour", CONVS, ids=["strict", "fastmath"])
+@pytest.mark.parametrize("T,C", [(40, 96), (7, 24), (300, 192)])
+@pytest.mark.parametrize("residual", [0, 1])
+def test_oracle_conv1x1_skip_matches_reference_calls(oracle, conv, flavour, T, C, residual):
+    # dacvae.c:986-1005 runs the 1x1 projection of a residual unit as the
+    # reference's own calls: memcpy(skip), quantize (two-term or not), then
+    # iro_int8_linear_ex with accumulate = 1 and the bias, and the second
+    # plane accumulated without bias.  The same calls on the reference build
+    # pin the oracle's composition.
+    ref = _ref(flavour)
+    hidden = gauss(60 + T, (T, C))
+    hidden[2:4] = 0.0
+    skip = gauss(61 + T, (T, C))
+    w = gauss(62, (C, C), 0.02)
+    b = gauss(63, (C,), 0.01)
+    wq = ref.weight_quantize(w)
+    if residual:
+        q1, _, q2 = ref.quantize_rows_residual(hidden)
+        y, _ = ref.linear(*q1, *wq, bias=b, y=skip, accumulate=True)
+        want, _ = ref.linear(*q2, *wq, bias=None, y=y, accumulate=True)
+    else:
+        q1 = ref.quantize_rows(hidden)
+        want, _ = ref.linear(*q1, *wq, bias=b, y=skip, accumulate=True)
+    got = oracle.conv1x1_skip(conv, hidden, skip, *wq, bias=b, residual=residual)
+    assert _eq(got, want)
+
+
 def test_oracle_silu_matches_strict_reference_build(oracle):
     ref = _ref("strict")
     a = gauss(3, (200000,), 4.0)
