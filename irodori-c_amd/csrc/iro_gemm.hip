@@ -475,6 +475,10 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
     constexpr int PLANE = BM * KC;                      // LDS bytes per plane per chunk
     constexpr int R = 8 / TJ <= KBC ? 8 / TJ : KBC;     // weight ring depth in k blocks
     static_assert(KC % 32 == 0 && KBC % R == 0 && R % 2 == 0 && KBC >= 2, "chunk must hold whole rings");
+    // Two-plane 64 x 256 tiles run one block per CU (their accumulators take
+    // 128 registers), so nothing hides the activation loads but their own
+    // lead: those stage two chunks ahead.
+    constexpr bool DEEP = TWO && TI * TJ == 4;
     __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][PL * PLANE];
     __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
     __shared__ uint64_t exptab[32];
@@ -525,26 +529,31 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
                 acc2[i][j][r] = 0;
             }
 
-    v4i ra[CP];
+    // Staging registers of the activation chunks: DEEP keeps two chunks in
+    // flight (chunk c+2 is loaded while chunk c runs), one otherwise.
+    constexpr int NRA = DEEP ? 2 : 1;
+    v4i ra[NRA][CP];
     v4i rb[R][TJ];
     const v4i flip = {p.aflip, p.aflip, p.aflip, p.aflip};
     const v4i zero4 = {0, 0, 0, 0};
 
-    auto load_chunk = [&](int c) {
+    // Staging slot of chunk c is c % NRA; callers pass it as a constant
+    // (the chunk loop is unrolled by two) so the registers stay registers.
+    auto load_chunk = [&](v4i (&dst)[CP], int c) {
 #pragma unroll
         for (int i = 0; i < CP; ++i) {
             int k = c * KC + kof[i];
             k = k < p.K - 16 ? k : p.K - 16;  // past the extent: any in-bounds bytes
-            ra[i] = *reinterpret_cast<const v4i *>(pa[i] + k);
+            dst[i] = *reinterpret_cast<const v4i *>(pa[i] + k);
         }
     };
     // Codes enter LDS as a - 128; bytes at k >= K enter as 0, so every MFMA
     // of a chunk can run unconditionally (zero times any weight is zero).
-    auto store_chunk = [&](int buf, int c) {
+    auto store_chunk = [&](const v4i (&src)[CP], int buf, int c) {
 #pragma unroll
         for (int i = 0; i < CP; ++i)
             *reinterpret_cast<v4i *>(&lds_a[buf][(tid + 256 * i) * 16]) =
-                c * KC + kof[i] < p.K ? (ra[i] ^ flip) : zero4;
+                c * KC + kof[i] < p.K ? (src[i] ^ flip) : zero4;
     };
     auto load_b = [&](int slot_unused, v4i (&dst)[TJ], int kb) {
         (void)slot_unused;
@@ -572,11 +581,13 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
             }
     };
 
-    // Prologue: chunk 0 and the first R weight k blocks in flight together.
-    load_chunk(0);
+    // Prologue: chunk 0 (and with DEEP chunk 1) and the first R weight k
+    // blocks in flight together.
+    load_chunk(ra[0], 0);
 #pragma unroll
     for (int u = 0; u < R; ++u) load_b(u, rb[u], u);
-    store_chunk(0, 0);
+    if (DEEP) load_chunk(ra[NRA - 1], 1 < nc ? 1 : 0);
+    store_chunk(ra[0], 0, 0);
     __syncthreads();
     // Each chunk is one straight run of KBC k steps (fully unrolled, no
     // branches): step u reads the activation fragments of step u+1 from
@@ -585,8 +596,9 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
     // the first ring turn: loads complete in issue order, so weight
     // fragments issued after them are consumed a full turn later.  In the
     // last chunk they reload in-bounds bytes into the idle buffer.
-    for (int c = 0; c < nc; ++c) {
-        const uint8_t *abuf = lds_a[c & 1];
+    auto run_chunk = [&](int c, auto par) {
+        constexpr int PAR = decltype(par)::value;  // c % 2
+        const uint8_t *abuf = lds_a[PAR];
         const int g0 = c * KBC;
         v4i a0[PL][TI], a1[PL][TI];
         read_a(a0, abuf, 0);
@@ -601,11 +613,21 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
             fence_sched();
             mma(a1, rb[(u + 1) % R]);
             load_b((u + 1) % R, rb[(u + 1) % R], g0 + u + 1 + R);
-            if (u + 2 == R) load_chunk(c + 1 < nc ? c + 1 : c);
+            if (u + 2 == R) {
+                // DEEP: chunk c+2 into the registers chunk c left (stored
+                // before this chunk began); past the end a reload of an
+                // in-bounds chunk into the same registers.
+                const int cl = c + (DEEP ? 2 : 1);
+                load_chunk(ra[DEEP ? PAR : 0], cl < nc ? cl : c);
+            }
             fence_sched();
         }
-        store_chunk((c + 1) & 1, c + 1);
+        store_chunk(ra[DEEP ? 1 - PAR : 0], 1 - PAR, c + 1);
         __syncthreads();
+    };
+    for (int c = 0; c < nc; c += 2) {
+        run_chunk(c, std::integral_constant<int, 0>{});
+        if (c + 1 < nc) run_chunk(c + 1, std::integral_constant<int, 1>{});
     }
 
     epilogue<CONV, EPI, TWO, TI, TJ, BM>(p, acc, acc2, cp, rl, exptab, m0, nb0, lane);
@@ -1044,10 +1066,15 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
         kp.row_major = ctx->tile_order >= 0 ? ctx->tile_order : (abytes > wbytes ? 1 : 0);
         grid = (unsigned)(8 * kp.tiles_per_xcd);
         if (mode == MODE_WHOLE) {
-            // Slabs per block: the fewest that still leave about one block
-            // per CU per resident slot pair, so the stationary tile serves
-            // as many slabs as the grid allows.
+            // Slabs per block: W1/W3 takes the fewest that still leave
+            // about one block per CU per resident slot pair, so the
+            // stationary tile serves as many slabs as the grid allows (its
+            // SiLU epilogue then overlaps the weight stream of the next
+            // slab).  QKVG runs one slab per block: its store-bound epilogue
+            // gains more from the extra blocks (measured 26.9 us against
+            // 29.5 us with two slabs at M = 2250, N = 4096, K = 1024).
             int spb = (epi == EPI_QKVG || epi == EPI_SWIGLU) ? ctx->gemm_spb : 1;
+            if (spb <= 0 && epi == EPI_QKVG) spb = 1;
             if (spb <= 0) {
                 const int cus = ctx->cus > 0 ? ctx->cus : 256;
                 spb = 1;
