@@ -476,9 +476,9 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
     constexpr int R = 8 / TJ <= KBC ? 8 / TJ : KBC;     // weight ring depth in k blocks
     static_assert(KC % 32 == 0 && KBC % R == 0 && R % 2 == 0 && KBC >= 2, "chunk must hold whole rings");
     // Two-plane 64 x 256 tiles run one block per CU (their accumulators take
-    // 128 registers), so nothing hides the activation loads but their own
-    // lead: those stage two chunks ahead.
-    constexpr bool DEEP = TWO && TI * TJ == 4;
+    // 128 registers), so nothing hides the activation staging but the MFMAs
+    // of the same wave: those stage two chunks ahead, one piece per k step.
+    constexpr bool DEEP = TWO && TI == 2 && TJ == 2;
     __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][PL * PLANE];
     __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
     __shared__ uint64_t exptab[32];
@@ -537,6 +537,16 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
     const v4i flip = {p.aflip, p.aflip, p.aflip, p.aflip};
     const v4i zero4 = {0, 0, 0, 0};
 
+    // One piece of chunk c: its global load and its LDS store.
+    auto load_piece = [&](v4i (&dst)[CP], int c, int i) {
+        int k = c * KC + kof[i];
+        k = k < p.K - 16 ? k : p.K - 16;  // past the extent: any in-bounds bytes
+        dst[i] = *reinterpret_cast<const v4i *>(pa[i] + k);
+    };
+    auto store_piece = [&](const v4i (&src)[CP], int buf, int c, int i) {
+        *reinterpret_cast<v4i *>(&lds_a[buf][(tid + 256 * i) * 16]) =
+            c * KC + kof[i] < p.K ? (src[i] ^ flip) : zero4;
+    };
     // Staging slot of chunk c is c % NRA; callers pass it as a constant
     // (the chunk loop is unrolled by two) so the registers stay registers.
     auto load_chunk = [&](v4i (&dst)[CP], int c) {
@@ -596,7 +606,43 @@ __device__ __forceinline__ void gemm_tile_body(const KParams &p) {
     // the first ring turn: loads complete in issue order, so weight
     // fragments issued after them are consumed a full turn later.  In the
     // last chunk they reload in-bounds bytes into the idle buffer.
+    // DEEP: chunk c+1 (in registers since chunk c-1) goes to LDS and chunk
+    // c+2 is loaded piece by piece, one piece per k step of chunk c, so the
+    // staging issues among the MFMAs; the chunk ends with the barrier alone.
+    // The buffer chunk c+1 is written to was last read in chunk c-1, before
+    // the barrier that ended it.
+    static_assert(!DEEP || CP == KBC, "one staged piece per k step");
+    auto run_chunk_deep = [&](int c, auto par) {
+        constexpr int PAR = decltype(par)::value;  // c % 2
+        const uint8_t *abuf = lds_a[PAR];
+        const int g0 = c * KBC;
+        const int cn = c + 2 < nc ? c + 2 : c;  // past the end: an in-bounds reload
+        v4i a0[PL][TI], a1[PL][TI];
+        read_a(a0, abuf, 0);
+#pragma unroll
+        for (int u = 0; u < KBC; u += 2) {
+            read_a(a1, abuf, u + 1);
+            fence_sched();
+            mma(a0, rb[u % R]);
+            load_b(u % R, rb[u % R], g0 + u + R);
+            store_piece(ra[1 - PAR], 1 - PAR, c + 1, u);
+            load_piece(ra[PAR], cn, u);
+            fence_sched();
+            if (u + 2 < KBC) read_a(a0, abuf, u + 2);
+            fence_sched();
+            mma(a1, rb[(u + 1) % R]);
+            load_b((u + 1) % R, rb[(u + 1) % R], g0 + u + 1 + R);
+            store_piece(ra[1 - PAR], 1 - PAR, c + 1, u + 1);
+            load_piece(ra[PAR], cn, u + 1);
+            fence_sched();
+        }
+        __syncthreads();
+    };
     auto run_chunk = [&](int c, auto par) {
+        if constexpr (DEEP) {
+            run_chunk_deep(c, par);
+            return;
+        }
         constexpr int PAR = decltype(par)::value;  // c % 2
         const uint8_t *abuf = lds_a[PAR];
         const int g0 = c * KBC;
