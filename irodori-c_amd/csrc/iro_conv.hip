@@ -111,8 +111,7 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(
                 const float4 v = *reinterpret_cast<const float4 *>(xr + c);
                 const float a = quant_value<CONV>(v.x, q), b = quant_value<CONV>(v.y, q);
                 const float e = quant_value<CONV>(v.z, q), f = quant_value<CONV>(v.w, q);
-                *reinterpret_cast<uint32_t *>(t1 + c) =
-                    (uint32_t)a | ((uint32_t)b << 8) | ((uint32_t)e << 16) | ((uint32_t)f << 24);
+                *reinterpret_cast<uint32_t *>(t1 + c) = pack_codes4(a, b, e, f);
                 if (RES) {
                     *reinterpret_cast<uint32_t *>(t2 + c) =
                         plane2_code<CONV>(v.x, a, q, inv2) | (plane2_code<CONV>(v.y, b, q, inv2) << 8) |

@@ -227,7 +227,10 @@ __device__ __forceinline__ ColParams<TJ> load_cols(const KParams &p, int nb0, in
     return c;
 }
 
-// Epilogue of one wave's TI x TJ accumulator tiles.  32x32 accumulator
+// Epilogue of one wave's TI x TJ accumulator tiles.  The QKVG planes and
+// the SwiGLU hidden state, the two largest output streams, are stored
+// nontemporally (measured 1-2 % faster over the stack: the store bursts of
+// all blocks drain sooner when they do not displace cached lines).  32x32 accumulator
 // layout: lane L, register r holds row 8*(r/4) + 4*(L/32) + r%4 and column
 // L%32 of the tile.  Row (m0 + i*32 + 8*g + e) is wave-uniform, so every
 // store address is a scalar row base plus one per-lane offset fixed per
@@ -364,7 +367,7 @@ __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc
                         if (p.work) p.work[(ru + half * 4) * p.ldw + pc[j]] = raw;
                     }
                 } else if (EPI == EPI_QKVG) {
-                    if (ok) segp[j][ru * p.seg_n] = y;
+                    if (ok) __builtin_nontemporal_store(y, &segp[j][ru * p.seg_n]);
                 } else if (EPI == EPI_GATED) {
                     if (ok)
                         p.xres[ru * p.ldx + off[j]] =
@@ -381,7 +384,8 @@ __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float h = silu_mul(yv[j][r], yv[j + 1][r], exptab);
-                    if (row_ok(r) && hok) p.hidden[(size_t)rowu(r) * p.ldh + offh[j / 2]] = h;
+                    if (row_ok(r) && hok)
+                        __builtin_nontemporal_store(h, &p.hidden[(size_t)rowu(r) * p.ldh + offh[j / 2]]);
                 }
             }
         }

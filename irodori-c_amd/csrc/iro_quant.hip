@@ -22,7 +22,7 @@ __device__ __forceinline__ uint32_t codes4(const float4 &v, const RowQ &r, float
     float a = quant_value<CONV>(v.x, r), b = quant_value<CONV>(v.y, r);
     float c = quant_value<CONV>(v.z, r), d = quant_value<CONV>(v.w, r);
     if (vals) *vals = make_float4(a, b, c, d);
-    return (uint32_t)a | ((uint32_t)b << 8) | ((uint32_t)c << 16) | ((uint32_t)d << 24);
+    return pack_codes4(a, b, c, d);
 }
 
 // Vector path, one row held in registers as CH float4 per lane (lane L

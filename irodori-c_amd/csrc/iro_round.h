@@ -58,14 +58,24 @@ __device__ __forceinline__ RowQ row_params(float lo, float hi) {
     return r;
 }
 
-// Code as a float in [0, 255] (the reference keeps it as a float `v`).
+// Code as a float in [0, 255] (the reference keeps it as a float `v` and
+// clamps it with `v < 0 ? 0 : v`, `v > 255 ? 255 : v`).  fmax / fmin give
+// the same value for every non-NaN v; a NaN v (NaN input) becomes 0 here,
+// where the reference's clamp keeps NaN and its conversion to u8 then
+// yields code 0 as well, so the stored code is the same.
 template <int CONV>
 __device__ __forceinline__ float quant_value(float x, const RowQ &r) {
-    float v = CONV == 1 ? __builtin_rintf(__builtin_fmaf(x, r.inv, r.zpf))
-                        : __builtin_rintf(x * r.inv + r.zpf);
-    v = v < 0.0f ? 0.0f : v;
-    v = v > 255.0f ? 255.0f : v;
-    return v;
+    const float v = CONV == 1 ? __builtin_rintf(__builtin_fmaf(x, r.inv, r.zpf))
+                              : __builtin_rintf(x * r.inv + r.zpf);
+    return __builtin_fminf(__builtin_fmaxf(v, 0.0f), 255.0f);
+}
+
+// Four codes (values in [0, 255], integral) packed little-endian into a u32.
+__device__ __forceinline__ uint32_t pack_codes4(float a, float b, float c, float d) {
+    uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(a, 0, 0u);
+    w = __builtin_amdgcn_cvt_pk_u8_f32(b, 1, w);
+    w = __builtin_amdgcn_cvt_pk_u8_f32(c, 2, w);
+    return __builtin_amdgcn_cvt_pk_u8_f32(d, 3, w);
 }
 
 // ops.c:437-439 residual: r = x - s1*(q1 - zp1).
@@ -74,20 +84,45 @@ __device__ __forceinline__ float residual_value(float x, float v, const RowQ &r)
     return CONV == 1 ? __builtin_fmaf(r.s, r.zpf - v, x) : x - r.s * (v - r.zpf);
 }
 
-// Reference select semantics: lo = x < lo ? x : lo, hi = x > hi ? x : hi.
-__device__ __forceinline__ float sel_min(float a, float b) { return b < a ? b : a; }
-__device__ __forceinline__ float sel_max(float a, float b) { return b > a ? b : a; }
+// Row ranges.  The reference accumulates lo = x < lo ? x : lo and
+// hi = x > hi ? x : hi from lo = hi = 0 (ops.c:327-331), which skips NaN
+// and never leaves [-inf, 0] resp. [0, inf].  fmin / fmax (one instruction,
+// any order) skip NaN too and give the same values, except that a zero
+// result may come out as -0 where the reference keeps +0; a zero lo or hi
+// of either sign yields the same range, scale, inverse and zero point
+// (hi - lo, -lo * inv and rint of them are +-0 alike), so codes and row
+// parameters do not change.  Every caller accumulates such a range (or a
+// range of |w| from +0).
+__device__ __forceinline__ float sel_min(float a, float b) { return __builtin_fminf(a, b); }
+__device__ __forceinline__ float sel_max(float a, float b) { return __builtin_fmaxf(a, b); }
 
-__device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = sel_min(v, __shfl_xor(v, off, 64));
-    return v;
+// Cross-lane moves for wavefront reductions: DPP within rows of 16 lanes,
+// a swizzle across the two rows of each 32-lane half, and the two halves
+// combined through scalar reads.  The result is in every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = sel_max(v, __shfl_xor(v, off, 64));
-    return v;
+__device__ __forceinline__ float swz_xor16(float v) {
+    // bitmask mode: and 0x1f, or 0, xor 0x10 (lane ^ 16 within 32 lanes)
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
+template <bool MAX>
+__device__ __forceinline__ float wave_range(float v) {
+    auto op = [](float a, float b) { return MAX ? __builtin_fmaxf(a, b) : __builtin_fminf(a, b); };
+    v = op(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_mov<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_mov<0x140>(v));  // row_mirror
+    v = op(v, swz_xor16(v));
+    const int bits = __builtin_bit_cast(int, v);
+    return op(__builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0)),
+              __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32)));
+}
+__device__ __forceinline__ float wave_min(float v) { return wave_range<false>(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave_range<true>(v); }
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -55,6 +55,10 @@ def _rows(M, K, seed, heavy):
     if M > 4:
         x[3] = -np.abs(x[3])  # all non-positive row
         x[4, 17 % K] = 20.0   # outlier (tests/test_int8_ops.c:49-53)
+    if M > 6:
+        x[5] = -0.0           # signed zeros only: range [0, 0] whatever its signs
+        x[6] = -np.abs(x[6])  # non-positive with negative zeros: hi = +0
+        x[6, ::3] = -0.0
     return x
 
 
