@@ -260,6 +260,15 @@ int iro_hip_profile_read(IroHipContext *ctx, int kind, const char **name, long l
 
 /* Runs the ops.c:375-398 known answer through the MFMA GEMM: 0 exact. */
 int iro_hip_selfcheck(IroHipContext *ctx);
+/* Exhaustive check of the SiLU gate's device pieces over all 2^32 float
+   inputs (no counterpart in the reference; a test hook): exp_digest = sum
+   mod 2^64 of (bits(x) * 0x9E3779B97F4A7C15) ^ (bits(expf(x)) *
+   0xC2B2AE3D27D4EB4F) for the device's glibc-exact expf (NaN results as
+   0x7FC00000), to be compared with the same sum over glibc's expf;
+   div_mismatches = inputs a whose fast quotient a / (1 + expf(-a)) differs
+   from the IEEE division (0 expected).  Takes well under a second. */
+int iro_hip_selfcheck_silu(IroHipContext *ctx, unsigned long long *exp_digest,
+                           unsigned long long *div_mismatches);
 /* "gfx950 MFMA i8" plus device name; never NULL. */
 const char *iro_hip_backend_name(IroHipContext *ctx);
 

@@ -826,4 +826,20 @@ int iro_hip_selfcheck(IroHipContext *ctx) {
     return 0;
 }
 
+int iro_hip_selfcheck_silu(IroHipContext *ctx, unsigned long long *exp_digest,
+                           unsigned long long *div_mismatches) {
+    if (!ctx || !exp_digest || !div_mismatches) return -1;
+    void *buf = nullptr;
+    if (iro_hip_alloc(ctx, 16, &buf)) return -1;
+    unsigned long long h[2] = {0, 0};
+    int rc = iro_hip_upload(ctx, buf, h, sizeof(h));
+    if (!rc) rc = launch_silu_selfcheck(ctx, static_cast<unsigned long long *>(buf));
+    if (!rc) rc = iro_hip_download(ctx, h, buf, sizeof(h));
+    iro_hip_free(ctx, buf);
+    if (rc) return -1;
+    *exp_digest = h[0];
+    *div_mismatches = h[1];
+    return 0;
+}
+
 }  // extern "C"

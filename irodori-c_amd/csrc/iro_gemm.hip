@@ -128,21 +128,25 @@ __constant__ uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
 // Branch-free: the table path runs on x clamped into its domain (the clamp
-// is the identity there; NaN becomes the lower bound) and the special cases
-// are selected afterwards, so a wavefront never splits on them.
+// is the identity there; a NaN x takes whatever value the median gives, the
+// table index stays in range, and the result is replaced) and the special
+// cases are selected afterwards, so a wavefront never splits on them.  The
+// scale 2^(k/32) is built in 32-bit halves: (k << 47) only touches the high
+// word of the table entry.
 __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     constexpr float hi = 0x1.62e42ep6f, lo = -0x1.9fe368p6f;  // overflow / underflow bounds
-    const float xc = __builtin_fminf(__builtin_fmaxf(x, lo), hi);
+    const float xc = __builtin_amdgcn_fmed3f(x, lo, hi);
     const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
     const double xd = (double)xc;
     double kd = __builtin_fma(invln2n, xd, shift);
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    const uint32_t klo = (uint32_t)__double_as_longlong(kd);
     kd -= shift;
     const double r = __builtin_fma(invln2n, xd, -kd);
-    const uint64_t t = tab[ki % 32] + (ki << 47);
-    const double s = __longlong_as_double((long long)t);
+    const uint64_t tv = tab[klo & 31];
+    const uint32_t thi = (uint32_t)(tv >> 32) + (klo << 15);
+    const double s = __hiloint2double((int)thi, (int)(uint32_t)tv);
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
@@ -153,10 +157,64 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     return x != x ? x + x : e;
 }
 
+// a / b, correctly rounded, for b = 1 + expf(-a) (so b >= 1): reciprocal,
+// one Newton step, the quotient and one remainder correction (Markstein)
+// give the IEEE quotient when b < 2^64 and 2^-100 <= |a| < 2^126, checked
+// against the IEEE division for every float a on the GPU; zeros return a
+// (= a / b); the remaining lanes (a < -44, denormal or non-finite a) take
+// the IEEE division.
+__device__ __forceinline__ float silu_div(float a, float b) {
+    const float aa = __builtin_fabsf(a);
+    const bool fast = b < 0x1p64f && aa < 0x1p126f && (aa >= 0x1p-100f || a == 0.0f);
+    const float y = __builtin_amdgcn_rcpf(b);
+    const float y1 = __builtin_fmaf(__builtin_fmaf(-b, y, 1.0f), y, y);
+    const float q0 = a * y1;
+    float q = __builtin_fmaf(__builtin_fmaf(-b, q0, a), y1, q0);
+    q = a == 0.0f ? a : q;
+    if (__builtin_expect(!fast, 0)) q = a / b;
+    return q;
+}
+
 // ops.c:781-784 as the strict build computes it: x / (1 + expf(-x)) * g.
 __device__ __forceinline__ float silu_mul(float a, float g, const uint64_t *tab) {
     const float e = expf_glibc(-a, tab);
-    return (a / (1.0f + e)) * g;
+    return silu_div(a, 1.0f + e) * g;
+}
+
+// Exhaustive self-check of the SiLU gate's pieces over the 2^28 float
+// inputs with bit patterns base .. base + 2^28 - 1 (one per thread): the
+// expf digest term (bits(x) * 0x9E3779B97F4A7C15) ^ (bits(e) *
+// 0xC2B2AE3D27D4EB4F), NaN results as 0x7FC00000, summed into out[0]; and
+// into out[1] the inputs a whose silu_div(a, 1 + expf(-a)) differs from the
+// IEEE quotient (NaN == NaN).
+__global__ __launch_bounds__(256) void silu_selfcheck_kernel(unsigned long long *out, unsigned base) {
+    __shared__ uint64_t tab[32];
+    __shared__ unsigned long long part[2][4];
+    if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+    __syncthreads();
+    const unsigned u = base + blockIdx.x * 256u + threadIdx.x;
+    const float x = __uint_as_float(u);
+    const float e = expf_glibc(x, tab);
+    const unsigned ue = e != e ? 0x7FC00000u : __float_as_uint(e);
+    unsigned long long h = ((unsigned long long)u * 0x9E3779B97F4A7C15ull) ^
+                           ((unsigned long long)ue * 0xC2B2AE3D27D4EB4Full);
+    const float b = 1.0f + expf_glibc(-x, tab);
+    const float q0 = x / b, q1 = silu_div(x, b);
+    unsigned long long bad = __float_as_uint(q0) != __float_as_uint(q1) && !(q0 != q0 && q1 != q1);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        h += __shfl_xor(h, off, 64);
+        bad += __shfl_xor(bad, off, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[0][threadIdx.x >> 6] = h;
+        part[1][threadIdx.x >> 6] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        atomicAdd(&out[0], part[0][0] + part[0][1] + part[0][2] + part[0][3]);
+        atomicAdd(&out[1], part[1][0] + part[1][1] + part[1][2] + part[1][3]);
+    }
 }
 
 // Per-row parameters of a block's rows, staged in LDS: scale and zero
@@ -1033,6 +1091,16 @@ TileCfg choose_tile(int M, int Np, int cus, bool two, Epi epi, int forced) {
 }
 
 }  // namespace
+
+// All 2^32 inputs in 16 launches of 2^20 blocks; out[2] must start zeroed.
+int launch_silu_selfcheck(IroHipContext *ctx, unsigned long long *out) {
+    for (unsigned long long base = 0; base < (1ull << 32); base += (1ull << 28)) {
+        hipLaunchKernelGGL(silu_selfcheck_kernel, dim3(1u << 20), dim3(256), 0, ctx->stream, out,
+                           (unsigned)base);
+        IRO_HIP_CHECK_LAUNCH(ctx);
+    }
+    return 0;
+}
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi) {
     if (a.M <= 0) return 0;

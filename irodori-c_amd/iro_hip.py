@@ -92,6 +92,7 @@ def load() -> C.CDLL:
         "iro_hip_dit_stack_bytes": ([_vp], C.c_size_t),
         "iro_hip_dit_stack_buffers": ([_vp] + [C.POINTER(_vp)] * 6, _i),
         "iro_hip_dit_stack_destroy": ([_vp], None),
+        "iro_hip_selfcheck_silu": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_stack_use_graph": ([_vp, _i], _i),
         "iro_hip_profile_enable": ([_vp, _i], _i),
         "iro_hip_profile_reset": ([_vp], _i),
@@ -266,6 +267,13 @@ class Context:
 
     def selfcheck(self) -> int:
         return self.lib.iro_hip_selfcheck(self.h)
+
+    def selfcheck_silu(self):
+        """(expf digest over every float input, fast-division mismatches)."""
+        d, m = C.c_ulonglong(0), C.c_ulonglong(0)
+        self._check(self.lib.iro_hip_selfcheck_silu(self.h, C.byref(d), C.byref(m)),
+                    "selfcheck_silu")
+        return int(d.value), int(m.value)
 
     # -- events --------------------------------------------------------------------
     def event(self):

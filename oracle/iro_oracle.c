@@ -322,6 +322,34 @@ long long orc_expf_mismatches(int threads) {
     return bad;
 }
 
+/* Order-independent digest of orc_expf_restated over every float input:
+   the sum (mod 2^64) of (bits(x) * 0x9E3779B97F4A7C15) ^ (bits(e) *
+   0xC2B2AE3D27D4EB4F), with every NaN result counted as 0x7FC00000.  The
+   device restatement's self-check computes the same sum. */
+unsigned long long orc_expf_digest(int threads) {
+    unsigned long long sum = 0;
+#ifdef _OPENMP
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) reduction(+ : sum) num_threads(threads)
+#else
+    (void)threads;
+#endif
+    for (long long hi = 0; hi < 65536; hi++) {
+        for (uint32_t lo = 0; lo < 65536; lo++) {
+            const uint32_t u = ((uint32_t)hi << 16) | lo;
+            float x;
+            memcpy(&x, &u, sizeof x);
+            const float e = orc_expf_restated(x);
+            uint32_t ue;
+            memcpy(&ue, &e, 4);
+            if (e != e) ue = 0x7FC00000u;
+            sum += ((unsigned long long)u * 0x9E3779B97F4A7C15ull) ^
+                   ((unsigned long long)ue * 0xC2B2AE3D27D4EB4Full);
+        }
+    }
+    return sum;
+}
+
 /* ---- gated residual: dit.c:1013-1020, 1032-1039 ------------------------ */
 
 void orc_gated_residual(int conv, float *x, const float *gate,

@@ -80,6 +80,10 @@ float orc_expf_restated(float x);
 /* Count the float inputs (all 2^32 bit patterns) where orc_expf_restated
    and this process's libm expf differ (NaN == NaN). */
 long long orc_expf_mismatches(int threads);
+/* Sum over every float x (mod 2^64) of (bits(x) * 0x9E3779B97F4A7C15) ^
+   (bits(orc_expf_restated(x)) * 0xC2B2AE3D27D4EB4F), NaN results counted as
+   0x7FC00000: the digest a device restatement must reproduce. */
+unsigned long long orc_expf_digest(int threads);
 
 /* dit.c:1013-1020 / 1032-1039: x[b,s,:] += gate[b,:] * branch[b,s,:].
    Strict: two roundings.  Fast-math: one FMA (vfmadd132ps). */

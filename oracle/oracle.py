@@ -58,6 +58,8 @@ class Oracle:
         L.orc_expf_restated.restype = C.c_float
         L.orc_expf_mismatches.argtypes = [C.c_int]
         L.orc_expf_mismatches.restype = C.c_longlong
+        L.orc_expf_digest.argtypes = [C.c_int]
+        L.orc_expf_digest.restype = C.c_ulonglong
         L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
         L.orc_conv1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p,
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int,
@@ -163,6 +165,9 @@ class Oracle:
 
     def expf_mismatches(self):
         return self.lib.orc_expf_mismatches(self.threads)
+
+    def expf_digest(self):
+        return int(self.lib.orc_expf_digest(self.threads))
 
     def gated_residual(self, conv, x, gate, branch, B, S):
         x = np.array(x, np.float32, copy=True)

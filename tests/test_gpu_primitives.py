@@ -176,3 +176,14 @@ def test_inconsistent_colsum_keeps_raw_sums(ctx, oracle):
     yo, wo = oracle.linear(conv, q, s, z, wq, sw, fake)
     assert_bits_equal(work.numpy(), wo, "raw sums")
     assert_bits_equal(yd.numpy(), yo, "y with the given colsum")
+
+
+def test_silu_gate_pieces_on_every_float(ctx, oracle):
+    """The SiLU gate (ops.c:781-784) on the device: its glibc-exact expf gives,
+    over all 2^32 inputs, the digest of the oracle's restatement (itself equal
+    to libm's expf on every input, tests/test_oracle_pins.py), and its fast
+    correctly rounded quotient a / (1 + expf(-a)) equals the IEEE division for
+    every a."""
+    digest, mismatches = ctx.selfcheck_silu()
+    assert mismatches == 0
+    assert digest == oracle.expf_digest()
