@@ -249,6 +249,101 @@ def conv_main(args):
     print(json.dumps(out), flush=True)
 
 
+def weights_main(args):
+    """The weight source (safetensors.c:302-530, generate.c:526-544): one step
+    = the int8 weights of one DiT block (modulation, Wq/Wk/Wv/Wgate, Wo, W1,
+    W3, W2) built from an fp32 safetensors checkpoint (mmap, upload,
+    quantization and packing), and the same weights read back from their
+    packed files.  Host-to-device copies are inside the timing: this path
+    starts from a file."""
+    import tempfile
+    from safetensors.numpy import save_file
+    D, H = args.hidden, args.mlp
+    shapes = {"ada": (6 * D, D), "wq": (D, D), "wk": (D, D), "wv": (D, D), "wgate": (D, D),
+              "wo": (D, D), "w1": (H, D), "w3": (H, D), "w2": (D, H)}
+    tensors = {f"blocks.0.{k}.weight": gauss(60 + i, s, 0.02)
+               for i, (k, s) in enumerate(shapes.items())}
+    src_bytes = sum(a.nbytes for a in tensors.values())
+    conv = iro_hip.STRICT if args.convention == "strict" else iro_hip.GCC_FASTMATH
+    ctx = iro_hip.Context(0, conv)
+    log("backend:", ctx.backend())
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "block.safetensors")
+        save_file(tensors, path)
+        st = iro_hip.Safetensors(path)
+
+        def build():
+            ws = [ctx.weight_from_st(st, n) for n in tensors]
+            ctx.sync()
+            return ws
+
+        for _ in range(args.warmup):
+            for w in build():
+                w.destroy()
+        times, ws = [], []
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            ws = build()
+            times.append(time.perf_counter() - t0)
+            if len(times) < args.steps:
+                for w in ws:
+                    w.destroy()
+        files = [os.path.join(tmp, f"w{i}.iro8") for i in range(len(ws))]
+        for w, f in zip(ws, files):
+            ctx.weight_save(w, f)
+        packed_bytes = sum(os.path.getsize(f) for f in files)
+        ltimes = []
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            ls = [ctx.weight_load(f) for f in files]
+            ctx.sync()
+            ltimes.append(time.perf_counter() - t0)
+            same = all(np.array_equal(a.export()[0], b.export()[0]) for a, b in zip(ls, ws))
+            for w in ls:
+                w.destroy()
+        st.close()
+    med, lmed = sorted(times)[len(times) // 2], sorted(ltimes)[len(ltimes) // 2]
+    log(f"weights: build {med * 1e3:.1f} ms/block ({src_bytes / med / 1e9:.2f} GB/s of fp32), "
+        f"packed-file load {lmed * 1e3:.1f} ms/block; reloaded codes identical: {same}")
+    ctx.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import Oracle
+        o = Oracle()
+        c = 0 if conv == iro_hip.STRICT else 1
+        t0 = time.perf_counter()
+        for a in tensors.values():
+            o.weight_quantize(c, a)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(src_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port", "ms_per_step": round(dt * 1e3, 1),
+               "sample": "the oracle's iro_int8_weight_quantize restatement (ops.c:259-293) on "
+                         "the block's nine fp32 tensors, one thread, packing not included"}
+    out = {
+        "metric": "int8 weight build from a safetensors checkpoint (GB/s of fp32 source), 1 GPU",
+        "value": round(src_bytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(med * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32->int8",
+        "data": "synthetic (seeded Irwin-Hall Gaussian weights written with safetensors.numpy)",
+        "config": {"workload": f"one DiT block's int8 weights (hidden {D}, MLP {H}) from fp32 "
+                               f"safetensors: mmap, upload, quantize, pack",
+                   "fp32_bytes": src_bytes, "packed_file_bytes": packed_bytes,
+                   "packed_file_load_ms": round(lmed * 1e3, 3),
+                   "convention": args.convention, "parallelism": "single GPU"},
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def convt_main(args):
     """The codec's int8 ConvTranspose1d (dacvae.c:696-795, no snake): one step
     = row quantization, the GEMM to the expanded taps and the ordered
@@ -365,7 +460,7 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["stack"] + sorted(CONV_WORKLOADS) + sorted(CONVT_WORKLOADS),
+    ap.add_argument("--workload", choices=["stack", "weights"] + sorted(CONV_WORKLOADS) + sorted(CONVT_WORKLOADS),
                     default="stack",
                     help="stack (default): the DiT linear stack; conv7*: the codec int8 Conv1d; "
                          "convt-*: the codec int8 ConvTranspose1d")
@@ -398,6 +493,9 @@ def main():
         return
     if args.workload in CONVT_WORKLOADS:
         convt_main(args)
+        return
+    if args.workload == "weights":
+        weights_main(args)
         return
 
     B, S, D, H = args.batch, args.frames, args.hidden, args.mlp

@@ -169,6 +169,44 @@ int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWe
                        const IroHipWeight *w2, int residual_w13, int residual_w2,
                        float *hidden, float *out, float *x_res, const float *gate, int S);
 
+/* ---- weight source: safetensors checkpoints, packed weight files ------- */
+
+/* A safetensors checkpoint opened read-only through mmap, its header parsed
+   and checked as iro_st_load checks it (safetensors.c:302-497): header
+   length inside the file, every tensor with a known dtype (IroDType order:
+   0 F32, 1 F16, 2 BF16, 3 I64, 4 I32, 5 I16, 6 I8, 7 U8, 8 BOOL), at most 8
+   dimensions, data_offsets inside the data section and numel x item size
+   equal to its byte length; "__metadata__" an object of strings.  Needs no
+   device.  Returns 0, or -1 with iro_hip_st_last_error() set. */
+typedef struct IroHipSafetensors IroHipSafetensors;
+int iro_hip_st_open(const char *path, IroHipSafetensors **out);
+void iro_hip_st_close(IroHipSafetensors *st);
+const char *iro_hip_st_last_error(void);
+/* Number of tensors and the i-th name (header order). */
+int iro_hip_st_count(const IroHipSafetensors *st);
+const char *iro_hip_st_name(const IroHipSafetensors *st, int i);
+/* safetensors.c:520-524 iro_st_get: dtype, ndims, shape[8], a pointer into
+   the mapping and the byte length of the named tensor; -1 if absent. */
+int iro_hip_st_tensor(const IroHipSafetensors *st, const char *name, int *dtype, int *ndims,
+                      uint64_t *shape, const void **data, uint64_t *nbytes);
+/* safetensors.c:526-530 iro_st_meta: the metadata value, NULL if absent. */
+const char *iro_hip_st_meta(const IroHipSafetensors *st, const char *key);
+/* The int8 weight of a 2-D F32 / F16 / BF16 tensor ([N, K] rows = output
+   rows, or [K, N] with transposed = 1), 16-bit formats widened exactly:
+   uploaded, quantized and packed as iro_hip_weight_create does, the step
+   the reference takes at engine init from its mmapped tensors
+   (generate.c:526-544, iro_dit_int8_quantize).  The fp32 copy is not kept. */
+int iro_hip_weight_from_st(IroHipContext *ctx, const IroHipSafetensors *st, const char *name,
+                           int transposed, IroHipWeight **out);
+/* The packed int8 weight (fragments, scales, sums, shape, layout, parts and
+   the rounding convention its codes were made under) as a file, and back
+   without re-quantizing: no counterpart in the reference, which quantizes
+   at every engine init; for callers that start often.  Loading checks the
+   header, the size, a 64-bit checksum of the payload and that the
+   convention matches the context's. */
+int iro_hip_weight_save(IroHipContext *ctx, const IroHipWeight *w, const char *path);
+int iro_hip_weight_load(IroHipContext *ctx, const char *path, IroHipWeight **out);
+
 /* ---- the int8 linear stack of one Euler step --------------------------- */
 
 /* The int8 projections of `blocks` DiT blocks (dit.h:51-58 IroDiTInt8,

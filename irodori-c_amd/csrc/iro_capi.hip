@@ -121,6 +121,8 @@ int device_guard(IroHipContext *ctx) {
     return 0;
 }
 
+}  // namespace
+
 // Allocate the packed buffers of a weight whose logical shape is known.
 int weight_alloc(IroHipContext *ctx, int N, int K, int layout, int nparts, const int *parts_N,
                  bool separate_rowsum, IroHipWeight **out) {
@@ -147,6 +149,8 @@ int weight_alloc(IroHipContext *ctx, int N, int K, int layout, int nparts, const
     return 0;
 }
 
+namespace {
+
 // Quantize parts on the device into a row-major staging copy, then pack.
 int weight_build(IroHipContext *ctx, const float *const *parts, const int *parts_N, int nparts,
                  int K, int layout, bool transposed, IroHipWeight **out) {
@@ -162,6 +166,7 @@ int weight_build(IroHipContext *ctx, const float *const *parts, const int *parts
     if (device_guard(ctx)) return -1;
     IroHipWeight *w = nullptr;
     if (weight_alloc(ctx, N, K, layout, nparts, parts_N, false, &w)) return -1;
+    w->convention = ctx->convention;
     int8_t *q = nullptr;
     float *scale = nullptr;
     int32_t *colsum = nullptr;
@@ -248,6 +253,7 @@ int weight_rows_copy(IroHipContext *ctx, IroHipWeight *dst, int row0, const IroH
         row0 % 32 || row0 < 0 || row0 + src->Np > dst->Np || src->rowsum != src->colsum ||
         dst->rowsum != dst->colsum)
         return set_error(ctx, "weight: rows do not fit the destination weight");
+    dst->convention = src->convention;
     // Packed rows are 32-row blocks of Kp/32 fragments: rows row0.. start at
     // byte row0 * Kp, and the source's Np rows are one contiguous run.
     IRO_HIP_TRY(ctx, hipMemcpyAsync(dst->packed + (size_t)row0 * dst->Kp, src->packed,

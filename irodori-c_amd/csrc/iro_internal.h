@@ -80,6 +80,8 @@ struct IroHipWeight {
     int32_t *rowsum = nullptr;  // true sum of the packed codes of each row;
                                 // equals colsum unless a caller supplied an
                                 // inconsistent one (ops.c:391 selfcheck does)
+    int convention = -1;        // rounding convention the codes were made
+                                // under; -1 when the caller supplied them
 };
 
 namespace iro {
@@ -135,6 +137,9 @@ int launch_fill(IroHipContext *ctx, void *dst, int value, size_t bytes);
 // A zeroed layout-0 weight of N x K, and a copy of a whole layout-0 weight
 // into its rows row0 .. row0 + src->Np (row0 a multiple of 32): several
 // weights that share one activation become one GEMM.
+// The packed buffers of a weight of logical N x K (contents undefined).
+int weight_alloc(IroHipContext *ctx, int N, int K, int layout, int nparts, const int *parts_N,
+                 bool separate_rowsum, IroHipWeight **out);
 int weight_rows_alloc(IroHipContext *ctx, int N, int K, IroHipWeight **out);
 int weight_rows_copy(IroHipContext *ctx, IroHipWeight *dst, int row0, const IroHipWeight *src);
 

@@ -46,6 +46,17 @@ def load() -> C.CDLL:
     L = C.CDLL(LIB_PATH)
     sig = {
         "iro_hip_create": ([_i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_st_open": ([C.c_char_p, C.POINTER(_vp)], _i),
+        "iro_hip_st_close": ([_vp], None),
+        "iro_hip_st_last_error": ([], C.c_char_p),
+        "iro_hip_st_count": ([_vp], _i),
+        "iro_hip_st_name": ([_vp, _i], C.c_char_p),
+        "iro_hip_st_tensor": ([_vp, C.c_char_p, C.POINTER(_i), C.POINTER(_i),
+                               C.POINTER(C.c_uint64), C.POINTER(_vp), C.POINTER(C.c_uint64)], _i),
+        "iro_hip_st_meta": ([_vp, C.c_char_p], C.c_char_p),
+        "iro_hip_weight_from_st": ([_vp, _vp, C.c_char_p, _i, C.POINTER(_vp)], _i),
+        "iro_hip_weight_save": ([_vp, _vp, C.c_char_p], _i),
+        "iro_hip_weight_load": ([_vp, C.c_char_p, C.POINTER(_vp)], _i),
         "iro_hip_destroy": ([_vp], None),
         "iro_hip_get_convention": ([_vp], _i),
         "iro_hip_error": ([_vp], C.c_char_p),
@@ -167,6 +178,61 @@ class DeviceArray:
         if self.ptr:
             self.ctx.lib.iro_hip_free(self.ctx.h, self.vp)
             self.ptr = None
+
+
+ST_DTYPES = ["F32", "F16", "BF16", "I64", "I32", "I16", "I8", "U8", "BOOL"]
+_ST_NP = {"F32": np.float32, "F16": np.float16, "I64": np.int64, "I32": np.int32,
+          "I16": np.int16, "I8": np.int8, "U8": np.uint8, "BOOL": np.bool_}
+
+
+class StError(RuntimeError):
+    pass
+
+
+class Safetensors:
+    """A safetensors checkpoint through iro_hip_st_* (mmapped; no device)."""
+
+    def __init__(self, path: str):
+        self.lib = load()
+        h = C.c_void_p()
+        if self.lib.iro_hip_st_open(os.fsencode(path), C.byref(h)) != 0:
+            raise StError(self.lib.iro_hip_st_last_error().decode(errors="replace"))
+        self.h = h
+
+    def names(self) -> list[str]:
+        return [self.lib.iro_hip_st_name(self.h, i).decode()
+                for i in range(self.lib.iro_hip_st_count(self.h))]
+
+    def info(self, name: str):
+        """(dtype name, shape, address, nbytes) of a tensor."""
+        dt, nd = C.c_int(), C.c_int()
+        shape = (C.c_uint64 * 8)()
+        data, nb = C.c_void_p(), C.c_uint64()
+        if self.lib.iro_hip_st_tensor(self.h, name.encode(), C.byref(dt), C.byref(nd), shape,
+                                      C.byref(data), C.byref(nb)) != 0:
+            raise KeyError(name)
+        return ST_DTYPES[dt.value], tuple(shape[i] for i in range(nd.value)), data.value, nb.value
+
+    def bytes(self, name: str) -> bytes:
+        _, _, addr, nb = self.info(name)
+        return C.string_at(addr, nb) if nb else b""
+
+    def array(self, name: str) -> np.ndarray:
+        dt, shape, _, _ = self.info(name)
+        raw = self.bytes(name)
+        if dt == "BF16":
+            u = np.frombuffer(raw, np.uint16).astype(np.uint32) << 16
+            return u.view(np.float32).reshape(shape)
+        return np.frombuffer(raw, _ST_NP[dt]).reshape(shape)
+
+    def meta(self, key: str):
+        v = self.lib.iro_hip_st_meta(self.h, key.encode())
+        return v.decode() if v is not None else None
+
+    def close(self):
+        if self.h:
+            self.lib.iro_hip_st_close(self.h)
+            self.h = None
 
 
 class Weight:
@@ -297,6 +363,25 @@ class Context:
         fn = (self.lib.iro_hip_weight_create_transposed if transposed
               else self.lib.iro_hip_weight_create)
         self._check(fn(self.h, w_dev.vp, N, K, C.byref(h)), "weight_create")
+        w = Weight(self, h.value)
+        self._weights.append(w)
+        return w
+
+    def weight_from_st(self, st: Safetensors, name: str, transposed: bool = False) -> Weight:
+        h = C.c_void_p()
+        self._check(self.lib.iro_hip_weight_from_st(self.h, st.h, name.encode(), int(transposed),
+                                                    C.byref(h)), "weight_from_st")
+        w = Weight(self, h.value)
+        self._weights.append(w)
+        return w
+
+    def weight_save(self, w: Weight, path: str):
+        self._check(self.lib.iro_hip_weight_save(self.h, w.h, os.fsencode(path)), "weight_save")
+
+    def weight_load(self, path: str) -> Weight:
+        h = C.c_void_p()
+        self._check(self.lib.iro_hip_weight_load(self.h, os.fsencode(path), C.byref(h)),
+                    "weight_load")
         w = Weight(self, h.value)
         self._weights.append(w)
         return w
