@@ -63,7 +63,8 @@ def _rows(M, K, seed, heavy):
 
 
 QROWS = [(1, 64, 0), (7, 64, 0), (23, 128, 1), (256, 1024, 0), (2250, 1024, 1),
-         (300, 2816, 1), (5, 100, 0), (33, 4100, 0), (9, 5000, 1), (4, 16, 0)]
+         (300, 2816, 1), (2249, 2816, 1), (37, 3000, 1), (5, 100, 0), (33, 4100, 0),
+         (9, 5000, 1), (4, 16, 0)]
 
 
 @pytest.mark.parametrize("M,K,heavy", QROWS)
