@@ -17,6 +17,9 @@ the codec's int8 Conv1d instead: one conv per step, same JSON line;
 `--workload convt-stage0` / `convt-stage2` the decoder's int8 upsampling
 ConvTranspose1d (stage 0: 750 frames, 1536->768, kernel 24, stride 12;
 stage 2: 90000 frames, 384->192, kernel 16, stride 8).
+`--workload adaln` the fp32 adaLN apply step of a DiT block on the same
+M = 2250 rows (one call per step); `--workload weights` the int8 weight
+build from a safetensors checkpoint.
 
 Prints one JSON line on stdout; diagnostics go to stderr.
 """
@@ -249,6 +252,91 @@ def conv_main(args):
     print(json.dumps(out), flush=True)
 
 
+def adaln_main(args):
+    """The adaLN apply step (dit.c:593-606) on the stack's rows: one step =
+    one call of iro_hip_dit_adaln_apply on x [B*S, D] resident in HBM.  The
+    per-row sum of squares is a serial chain of D dependent fp32 additions
+    (bit-exact to the strict build), which bounds the kernel before HBM does;
+    the roofline line still prices the algorithmic bytes (x read once, h
+    written once) against HBM."""
+    B, S, D = args.batch, args.frames, args.hidden
+    M = B * S
+    conv = iro_hip.STRICT if args.convention == "strict" else iro_hip.GCC_FASTMATH
+    x = gauss(71, (M, D))
+    shift, scale = gauss(72, (B, D), 0.3), gauss(73, (B, D), 0.3)
+    eps = 1e-6
+    ctx = iro_hip.Context(0, conv)
+    log("backend:", ctx.backend())
+    xd, shd, scd = ctx.to_device(x), ctx.to_device(shift), ctx.to_device(scale)
+    h = ctx.empty((M, D), np.float32)
+
+    def step():
+        ctx.dit_adaln_apply(xd, B, S, D, shd, scd, eps, h)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    t0 = time.perf_counter()
+    ctx.record(e0)
+    for _ in range(args.steps):
+        step()
+    ctx.record(e1)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.elapsed_ms(e0, e1) / args.steps
+    hgpu = h.numpy()
+    ctx.close()
+    alg_bytes = 8 * M * D + 8 * B * D
+    achieved = alg_bytes / (ev_ms * 1e-3) / 1e9
+    log(f"adaln: {wall * 1e3 / args.steps:.4f} ms/call wall, {ev_ms * 1e3:.2f} us/call events, "
+        f"{achieved:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import Oracle
+        o = Oracle()
+        times = []
+        start = time.perf_counter()
+        while len(times) < 20 and time.perf_counter() - start < args.cpu_seconds:
+            t1 = time.perf_counter()
+            hcpu = o.adaln_apply(x, shift, scale, B, S, eps)
+            times.append(time.perf_counter() - t1)
+        med = sorted(times)[len(times) // 2]
+        same = bool(np.array_equal(hcpu.view(np.uint32), hgpu.view(np.uint32)))
+        log(f"cpu baseline: {len(times)} calls, median {med * 1e3:.2f} ms; GPU output "
+            f"bit-identical: {same}")
+        cpu = {"value": round(M / med / 1e6, 4), "unit": "Mrows/s", "cores": 1, "kind": "port",
+               "ms_per_step": round(med * 1e3, 3),
+               "sample": f"the oracle's dit.c:593-606 restatement on all {M} rows "
+                         f"({len(times)} calls, median), one thread",
+               "gpu_output_bit_identical": same}
+    out = {
+        "metric": "adaLN apply rows/s (Mrows/s), 1 GPU",
+        "value": round(M / (ev_ms * 1e-3) / 1e6, 2),
+        "unit": "Mrows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ev_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Irwin-Hall Gaussian x, shift, scale)",
+        "config": {"workload": f"fp32 adaLN apply on {B} x {S} rows of {D}, one call per step",
+                   "rows": M, "dim": D, "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+                   "convention": args.convention, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "note": (f"algorithmic bytes {alg_bytes} per launch (x read and h written "
+                              f"once, shift/scale rows); the serial sum of {D} dependent fp32 "
+                              f"additions per row bounds the kernel first")},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def weights_main(args):
     """The weight source (safetensors.c:302-530, generate.c:526-544): one step
     = the int8 weights of one DiT block (modulation, Wq/Wk/Wv/Wgate, Wo, W1,
@@ -460,7 +548,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["stack", "weights"] + sorted(CONV_WORKLOADS) + sorted(CONVT_WORKLOADS),
+    ap.add_argument("--workload", choices=["stack", "weights", "adaln"] + sorted(CONV_WORKLOADS)
+                    + sorted(CONVT_WORKLOADS),
                     default="stack",
                     help="stack (default): the DiT linear stack; conv7*: the codec int8 Conv1d; "
                          "convt-*: the codec int8 ConvTranspose1d")
@@ -496,6 +585,9 @@ def main():
         return
     if args.workload == "weights":
         weights_main(args)
+        return
+    if args.workload == "adaln":
+        adaln_main(args)
         return
 
     B, S, D, H = args.batch, args.frames, args.hidden, args.mlp

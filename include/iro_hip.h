@@ -207,6 +207,18 @@ int iro_hip_weight_from_st(IroHipContext *ctx, const IroHipSafetensors *st, cons
 int iro_hip_weight_save(IroHipContext *ctx, const IroHipWeight *w, const char *path);
 int iro_hip_weight_load(IroHipContext *ctx, const char *path, IroHipWeight **out);
 
+/* ---- fp32 neighbours ------------------------------------------------------ */
+
+/* dit.c:593-606, the apply step of dit_adaln: h = x * inv * (1 + scale[b])
+   + shift[b] for row r of x [B*S, D] (b = r / S, shift/scale [B, D]) with
+   inv = 1 / sqrtf(mean(x^2) + eps), the sum of squares taken in index order
+   as the strict build does, so h is bit-identical to it.  (The fast-math
+   build vectorizes that sum in a host-dependent order.)  shift and scale
+   come from the caller (dit.c:580-588 computes them with fp32 low-rank
+   linears on the host). */
+int iro_hip_dit_adaln_apply(IroHipContext *ctx, const float *x, int B, int S, int D,
+                            const float *shift, const float *scale, float eps, float *h);
+
 /* ---- the int8 linear stack of one Euler step --------------------------- */
 
 /* The int8 projections of `blocks` DiT blocks (dit.h:51-58 IroDiTInt8,
@@ -307,6 +319,12 @@ int iro_hip_selfcheck(IroHipContext *ctx);
    from the IEEE division (0 expected).  Takes well under a second. */
 int iro_hip_selfcheck_silu(IroHipContext *ctx, unsigned long long *exp_digest,
                            unsigned long long *div_mismatches);
+/* Exhaustive digests (same form) of the device's sqrtf(x) and 1 / x over all
+   2^32 float inputs, to be compared with the host's IEEE results: the
+   correctly rounded operations the adaLN apply relies on (no counterpart in
+   the reference; a test hook). */
+int iro_hip_selfcheck_fp32(IroHipContext *ctx, unsigned long long *sqrt_digest,
+                           unsigned long long *recip_digest);
 /* "gfx950 MFMA i8" plus device name; never NULL. */
 const char *iro_hip_backend_name(IroHipContext *ctx);
 

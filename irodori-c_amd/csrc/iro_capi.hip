@@ -832,6 +832,22 @@ int iro_hip_selfcheck(IroHipContext *ctx) {
     return 0;
 }
 
+int iro_hip_selfcheck_fp32(IroHipContext *ctx, unsigned long long *sqrt_digest,
+                           unsigned long long *recip_digest) {
+    if (!ctx || !sqrt_digest || !recip_digest) return -1;
+    void *buf = nullptr;
+    if (iro_hip_alloc(ctx, 16, &buf)) return -1;
+    unsigned long long h[2] = {0, 0};
+    int rc = iro_hip_upload(ctx, buf, h, sizeof(h));
+    if (!rc) rc = launch_fp32_selfcheck(ctx, static_cast<unsigned long long *>(buf));
+    if (!rc) rc = iro_hip_download(ctx, h, buf, sizeof(h));
+    iro_hip_free(ctx, buf);
+    if (rc) return -1;
+    *sqrt_digest = h[0];
+    *recip_digest = h[1];
+    return 0;
+}
+
 int iro_hip_selfcheck_silu(IroHipContext *ctx, unsigned long long *exp_digest,
                            unsigned long long *div_mismatches) {
     if (!ctx || !exp_digest || !div_mismatches) return -1;

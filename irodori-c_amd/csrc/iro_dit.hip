@@ -16,6 +16,382 @@ namespace iro {
 
 namespace {
 
+// dit.c:593-606, the adaLN RMSNorm modulate of a DiT block, as the strict
+// build evaluates it: per row, ms accumulates x[d] * x[d] in index order
+// (each square rounded, then added -- a serial chain, so one lane owns a
+// row), inv = 1 / sqrtf(ms / D + eps), and h = ((x * inv) * (1 + scale)) +
+// shift with the row's branch b = row / S.  A block takes ROWS rows.  Their
+// columns pass through LDS 256 at a time (coalesced loads by the whole
+// block, the next chunk in flight while the current one is summed; rows
+// padded to 260 floats so the row owners' 16-byte reads are conflict-free);
+// ROWS lanes of wave 0 own one row each and run the chains.  Then every
+// wave writes ROWS / 4 rows with coalesced accesses.  V4: D % 4 == 0 and 16-byte
+// aligned rows.
+constexpr int kAdaCols = 256, kAdaPitch = 260;
+
+template <bool V4, int ROWS>
+__global__ __launch_bounds__(256) void adaln_apply_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ shift,
+                                                          const float *__restrict__ scale, int M,
+                                                          int S, int D, float eps,
+                                                          float *__restrict__ h) {
+    constexpr int PP = ROWS / 4;  // pieces per thread per chunk; rows per wave
+    __shared__ __attribute__((aligned(16))) float tile[2][ROWS * kAdaPitch];
+    __shared__ float inv_s[ROWS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * ROWS;
+    const int nch = (D + kAdaCols - 1) / kAdaCols;
+    // Chunk c, piece i (0..PP-1) of this thread: row i * 4 + tid / 64, float4
+    // column tid % 64; rows past M repeat row M-1, columns past D read 0.
+    float4 st[PP];
+    auto load = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < PP; ++i) {
+            int row = r0 + i * 4 + wave;
+            row = row < M ? row : M - 1;
+            const int col = c * kAdaCols + lane * 4;
+            const float *src = x + (size_t)row * D + col;
+            if (V4) {
+                st[i] = col < D ? *reinterpret_cast<const float4 *>(src) : make_float4(0, 0, 0, 0);
+            } else {
+                st[i].x = col + 0 < D ? src[0] : 0.0f;
+                st[i].y = col + 1 < D ? src[1] : 0.0f;
+                st[i].z = col + 2 < D ? src[2] : 0.0f;
+                st[i].w = col + 3 < D ? src[3] : 0.0f;
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PP; ++i)
+            *reinterpret_cast<float4 *>(&tile[buf][(i * 4 + wave) * kAdaPitch + lane * 4]) = st[i];
+    };
+    load(0);
+    store(0);
+    __syncthreads();
+    float ms = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+        if (c + 1 < nch) load(c + 1);
+        if (wave == 0 && lane < ROWS) {
+            const float *tr = &tile[c & 1][lane * kAdaPitch];
+            const int n = D - c * kAdaCols < kAdaCols ? D - c * kAdaCols : kAdaCols;
+            // 64 values per batch read ahead of their additions, so the
+            // chain waits on LDS once per batch.
+            int d = 0;
+            for (; d + 64 <= n; d += 64) {
+                float4 v[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = *reinterpret_cast<const float4 *>(tr + d + 4 * j);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    ms = ms + v[j].x * v[j].x;
+                    ms = ms + v[j].y * v[j].y;
+                    ms = ms + v[j].z * v[j].z;
+                    ms = ms + v[j].w * v[j].w;
+                }
+            }
+            for (; d < n; ++d) ms = ms + tr[d] * tr[d];
+        }
+        if (c + 1 < nch) store((c + 1) & 1);
+        __syncthreads();
+    }
+    if (wave == 0 && lane < ROWS) inv_s[lane] = 1.0f / __builtin_sqrtf(ms / (float)D + eps);
+    __syncthreads();
+    // Wave w writes rows PP w .. PP w + PP-1, eight rows per batch: the
+    // batch's loads of x, scale and shift all go out before any is used.
+    constexpr int RB = PP < 8 ? PP : 8;
+    static_assert(PP % RB == 0, "whole batches per wave");
+    for (int i0 = 0; i0 < PP; i0 += RB) {
+        int rows[RB];
+        const float *xr[RB], *sc[RB], *sh[RB];
+        float *hr[RB];
+        float inv[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const int rl = wave * PP + i0 + i;
+            rows[i] = r0 + rl;
+            const int row = rows[i] < M ? rows[i] : M - 1;
+            const int b = row / S;
+            xr[i] = x + (size_t)row * D;
+            sc[i] = scale + (size_t)b * D;
+            sh[i] = shift + (size_t)b * D;
+            hr[i] = h + (size_t)row * D;
+            inv[i] = inv_s[rl];
+        }
+        if (V4) {
+            for (int d = lane * 4; d < D; d += 256) {
+                float4 v[RB], cs[RB], t[RB];
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    v[i] = *reinterpret_cast<const float4 *>(xr[i] + d);
+                    cs[i] = *reinterpret_cast<const float4 *>(sc[i] + d);
+                    t[i] = *reinterpret_cast<const float4 *>(sh[i] + d);
+                }
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    if (rows[i] >= M) continue;
+                    float4 o;
+                    o.x = ((v[i].x * inv[i]) * (1.0f + cs[i].x)) + t[i].x;
+                    o.y = ((v[i].y * inv[i]) * (1.0f + cs[i].y)) + t[i].y;
+                    o.z = ((v[i].z * inv[i]) * (1.0f + cs[i].z)) + t[i].z;
+                    o.w = ((v[i].w * inv[i]) * (1.0f + cs[i].w)) + t[i].w;
+                    *reinterpret_cast<float4 *>(hr[i] + d) = o;
+                }
+            }
+        } else {
+            for (int d = lane; d < D; d += 64) {
+                float v[RB], cs[RB], t[RB];
+#pragma unroll
+                for (int i = 0; i < RB; ++i) {
+                    v[i] = xr[i][d];
+                    cs[i] = sc[i][d];
+                    t[i] = sh[i][d];
+                }
+#pragma unroll
+                for (int i = 0; i < RB; ++i)
+                    if (rows[i] < M) hr[i][d] = ((v[i] * inv[i]) * (1.0f + cs[i])) + t[i];
+            }
+        }
+    }
+}
+
+// The same computation with one wave per block and RW rows per wave, for
+// rows that fit in LDS whole: the wave loads its rows once (every load in
+// flight together), lanes 0..RW-1 run the rows' chains from LDS, and h is
+// written from the LDS copy, so x is read from HBM once and no block barrier
+// stands between the waves.  The chain is the floor: D dependent additions
+// per row, which a wave pays once whatever RW is, so RW sets how many waves
+// share the rows.
+template <bool V4, int RW>
+__global__ __launch_bounds__(64) void adaln_rows_kernel(const float *__restrict__ x,
+                                                        const float *__restrict__ shift,
+                                                        const float *__restrict__ scale, int M,
+                                                        int S, int D, float eps,
+                                                        float *__restrict__ h) {
+    extern __shared__ __attribute__((aligned(16))) float rows_lds[];
+    const int lane = threadIdx.x;
+    const int pitch = ((D + 3) & ~3) + 4;
+    const int r0 = blockIdx.x * RW;
+    int row[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) row[r] = r0 + r < M ? r0 + r : M - 1;
+    // 1) The rows into LDS, 1024 columns of every row per batch.
+    for (int c0 = 0; c0 < D; c0 += 1024) {
+        if (V4) {
+            float4 v[RW][4];
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = c0 + j * 256 + lane * 4;
+                    v[r][j] = col < D ? *reinterpret_cast<const float4 *>(x + (size_t)row[r] * D + col)
+                                      : make_float4(0, 0, 0, 0);
+                }
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = c0 + j * 256 + lane * 4;
+                    if (col < D) *reinterpret_cast<float4 *>(&rows_lds[r * pitch + col]) = v[r][j];
+                }
+        } else {
+            float v[RW][16];
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int col = c0 + j * 64 + lane;
+                    v[r][j] = col < D ? x[(size_t)row[r] * D + col] : 0.0f;
+                }
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int col = c0 + j * 64 + lane;
+                    if (col < D) rows_lds[r * pitch + col] = v[r][j];
+                }
+        }
+    }
+    __syncthreads();
+    // 2) Lane r < RW runs row r's chain in index order.
+    float inv = 0.0f;
+    if (lane < RW) {
+        const float *tr = &rows_lds[lane * pitch];
+        float ms = 0.0f;
+        int d = 0;
+        for (; d + 64 <= D; d += 64) {
+            float4 v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = *reinterpret_cast<const float4 *>(tr + d + 4 * j);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                ms = ms + v[j].x * v[j].x;
+                ms = ms + v[j].y * v[j].y;
+                ms = ms + v[j].z * v[j].z;
+                ms = ms + v[j].w * v[j].w;
+            }
+        }
+        for (; d < D; ++d) ms = ms + tr[d] * tr[d];
+        inv = 1.0f / __builtin_sqrtf(ms / (float)D + eps);
+    }
+    // 3) h from the LDS rows; scale and shift rows of the row's branch.
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        if (r0 + r >= M) break;
+        const float ir = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+        const int b = row[r] / S;
+        const float *sc = scale + (size_t)b * D, *sh = shift + (size_t)b * D;
+        float *hr = h + (size_t)row[r] * D;
+        const float *tr = &rows_lds[r * pitch];
+        if (V4) {
+            for (int c0 = 0; c0 < D; c0 += 1024) {
+                float4 v[4], cs[4], t[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = c0 + j * 256 + lane * 4;
+                    if (col < D) {
+                        v[j] = *reinterpret_cast<const float4 *>(tr + col);
+                        cs[j] = *reinterpret_cast<const float4 *>(sc + col);
+                        t[j] = *reinterpret_cast<const float4 *>(sh + col);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = c0 + j * 256 + lane * 4;
+                    if (col >= D) continue;
+                    float4 o;
+                    o.x = ((v[j].x * ir) * (1.0f + cs[j].x)) + t[j].x;
+                    o.y = ((v[j].y * ir) * (1.0f + cs[j].y)) + t[j].y;
+                    o.z = ((v[j].z * ir) * (1.0f + cs[j].z)) + t[j].z;
+                    o.w = ((v[j].w * ir) * (1.0f + cs[j].w)) + t[j].w;
+                    *reinterpret_cast<float4 *>(hr + col) = o;
+                }
+            }
+        } else {
+            for (int c0 = 0; c0 < D; c0 += 1024) {
+                float v[16], cs[16], t[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int col = c0 + j * 64 + lane;
+                    if (col < D) {
+                        v[j] = tr[col];
+                        cs[j] = sc[col];
+                        t[j] = sh[col];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int col = c0 + j * 64 + lane;
+                    if (col < D) hr[col] = ((v[j] * ir) * (1.0f + cs[j])) + t[j];
+                }
+            }
+        }
+    }
+}
+
+// Register-resident form for D % 4 == 0, D <= 256 NJ: each lane loads its
+// NJ float4 columns of x, scale and shift for the wave's RW rows at once
+// (every load in flight together, none behind a branch, x first in column
+// order).  The rounded squares x[d] * x[d] of each 256-column chunk go to LDS
+// as soon as that chunk has arrived, and lanes 0..RW-1 add them in index
+// order -- the same values and order as the serial loop, with the multiplies
+// off the chain -- while the later chunks are still in flight.  The chain is
+// the floor (one dependent add per column, about 4 ns each on gfx950); h is
+// computed from the registers, so x crosses HBM once.
+template <int RW, int NJ>
+__global__ __launch_bounds__(64) void adaln_reg_kernel(const float *__restrict__ x,
+                                                       const float *__restrict__ shift,
+                                                       const float *__restrict__ scale, int M,
+                                                       int S, int D, float eps,
+                                                       float *__restrict__ h) {
+    extern __shared__ __attribute__((aligned(16))) float sq_lds[];
+    const int lane = threadIdx.x;
+    const int pitch = D + 4;
+    const int r0 = blockIdx.x * RW;
+    float4 v[RW][NJ], cs[RW][NJ], t[RW][NJ];
+    int row[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) row[r] = r0 + r < M ? r0 + r : M - 1;
+    // Columns past D load column D-4 (in bounds, never used).
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            int col = j * 256 + lane * 4;
+            col = col < D ? col : D - 4;
+            v[r][j] = *reinterpret_cast<const float4 *>(x + (size_t)row[r] * D + col);
+        }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int b = row[r] / S;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            int col = j * 256 + lane * 4;
+            col = col < D ? col : D - 4;
+            cs[r][j] = *reinterpret_cast<const float4 *>(scale + (size_t)b * D + col);
+            t[r][j] = *reinterpret_cast<const float4 *>(shift + (size_t)b * D + col);
+        }
+    }
+    float ms = 0.0f;
+    const float *tr = &sq_lds[(lane < RW ? lane : 0) * pitch];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int col = j * 256 + lane * 4;
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+            if (col < D) {
+                float4 q;
+                q.x = v[r][j].x * v[r][j].x;
+                q.y = v[r][j].y * v[r][j].y;
+                q.z = v[r][j].z * v[r][j].z;
+                q.w = v[r][j].w * v[r][j].w;
+                *reinterpret_cast<float4 *>(&sq_lds[r * pitch + col]) = q;
+            }
+        __syncthreads();
+        if (lane < RW) {
+            const int c0 = j * 256;
+            if (c0 + 256 <= D) {
+                // 16 reads ahead of their additions: one LDS wait per 64.
+#pragma unroll
+                for (int k0 = 0; k0 < 64; k0 += 16) {
+                    float4 q[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k)
+                        q[k] = *reinterpret_cast<const float4 *>(tr + c0 + 4 * (k0 + k));
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) {
+                        ms = ms + q[k].x;
+                        ms = ms + q[k].y;
+                        ms = ms + q[k].z;
+                        ms = ms + q[k].w;
+                    }
+                }
+            } else {
+                for (int d = c0; d < D; ++d) ms = ms + tr[d];
+            }
+        }
+    }
+    float inv = 0.0f;
+    if (lane < RW) inv = 1.0f / __builtin_sqrtf(ms / (float)D + eps);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const float ir = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+        const bool live = r0 + r < M;
+        float *hr = h + (size_t)row[r] * D;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int col = j * 256 + lane * 4;
+            if (!live || col >= D) continue;
+            float4 o;
+            o.x = ((v[r][j].x * ir) * (1.0f + cs[r][j].x)) + t[r][j].x;
+            o.y = ((v[r][j].y * ir) * (1.0f + cs[r][j].y)) + t[r][j].y;
+            o.z = ((v[r][j].z * ir) * (1.0f + cs[r][j].z)) + t[r][j].z;
+            o.w = ((v[r][j].w * ir) * (1.0f + cs[r][j].w)) + t[r][j].w;
+            *reinterpret_cast<float4 *>(hr + col) = o;
+        }
+    }
+}
+
 int qkvg_impl(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w, float *q,
               float *k, float *v, float *gate, int residual) {
     const int D = w->K;
@@ -230,6 +606,68 @@ int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWe
     if (M == 0) return 0;
     return swiglu_impl(ctx, h, M, w13, w2, residual_w13, residual_w2, hidden, out, x_res, gate,
                        w13->K, S);
+}
+
+int iro_hip_dit_adaln_apply(IroHipContext *ctx, const float *x, int B, int S, int D,
+                            const float *shift, const float *scale, float eps, float *h) {
+    if (!ctx || B < 0 || S < 0 || D <= 0 || ((long long)B * S && (!x || !shift || !scale || !h)))
+        return set_error(ctx, "dit_adaln_apply: invalid arguments");
+    const int M = B * S;
+    if (M == 0) return 0;
+    const bool v4 = D % 4 == 0 && ((((uintptr_t)x) | ((uintptr_t)shift) | ((uintptr_t)scale) |
+                                     ((uintptr_t)h)) & 15) == 0;
+    // Register-resident rows up to D = 2048 (V4).
+    if (v4 && D <= 2048) {
+        const int nj = (D + 255) / 256;
+        const size_t pitch_bytes = ((size_t)D + 4) * sizeof(float);
+#define IRO_ADA_REG_LAUNCH(RWV, NJV)                                                              \
+    hipLaunchKernelGGL((adaln_reg_kernel<RWV, NJV>), dim3((M + RWV - 1) / RWV), dim3(64),         \
+                       RWV * pitch_bytes, ctx->stream, x, shift, scale, M, S, D, eps, h)
+        if (nj <= 2)
+            IRO_ADA_REG_LAUNCH(2, 2);
+        else if (nj <= 4)
+            IRO_ADA_REG_LAUNCH(2, 4);
+        else if (nj <= 5)
+            IRO_ADA_REG_LAUNCH(2, 5);
+        else
+            IRO_ADA_REG_LAUNCH(1, 8);
+#undef IRO_ADA_REG_LAUNCH
+        IRO_HIP_CHECK_LAUNCH(ctx);
+        return 0;
+    }
+    // Rows resident in LDS when they fit in 64 KiB: two rows per wave up
+    // to D = 8184, one up to D = 16380.
+    const size_t row_bytes = ((size_t)((D + 3) & ~3) + 4) * sizeof(float);
+    const int rw = 2 * row_bytes <= 65536 ? 2 : 1;
+    if (rw * row_bytes <= 65536) {
+        const dim3 g((M + rw - 1) / rw), blk(64);
+        const size_t lds = rw * row_bytes;
+#define IRO_ADA_ROWS_LAUNCH(RWV)                                                                 \
+    if (v4)                                                                                     \
+        hipLaunchKernelGGL((adaln_rows_kernel<true, RWV>), g, blk, lds, ctx->stream, x, shift,  \
+                           scale, M, S, D, eps, h);                                             \
+    else                                                                                        \
+        hipLaunchKernelGGL((adaln_rows_kernel<false, RWV>), g, blk, lds, ctx->stream, x, shift, \
+                           scale, M, S, D, eps, h);
+        if (rw == 2) {
+            IRO_ADA_ROWS_LAUNCH(2)
+        } else {
+            IRO_ADA_ROWS_LAUNCH(1)
+        }
+#undef IRO_ADA_ROWS_LAUNCH
+        IRO_HIP_CHECK_LAUNCH(ctx);
+        return 0;
+    }
+    constexpr int R = 16;
+    const dim3 grid((M + R - 1) / R), block(256);
+    if (v4)
+        hipLaunchKernelGGL((adaln_apply_kernel<true, R>), grid, block, 0, ctx->stream, x, shift,
+                           scale, M, S, D, eps, h);
+    else
+        hipLaunchKernelGGL((adaln_apply_kernel<false, R>), grid, block, 0, ctx->stream, x, shift,
+                           scale, M, S, D, eps, h);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
 }
 
 int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int residual_mask,

@@ -1095,6 +1095,46 @@ TileCfg choose_tile(int M, int Np, int cus, bool two, Epi epi, int forced) {
 
 }  // namespace
 
+// Exhaustive digests of the device's sqrtf and 1 / x (the correctly
+// rounded operations the adaLN apply relies on) over the 2^28 inputs from
+// base: out[0] += (bits(x) * 0x9E3779B97F4A7C15) ^ (bits(sqrtf(x)) *
+// 0xC2B2AE3D27D4EB4F), out[1] the same for 1 / x; NaN results as 0x7FC00000.
+__global__ __launch_bounds__(256) void fp32_selfcheck_kernel(unsigned long long *out, unsigned base) {
+    __shared__ unsigned long long part[2][4];
+    const unsigned u = base + blockIdx.x * 256u + threadIdx.x;
+    const float x = __uint_as_float(u);
+    const float r = __builtin_sqrtf(x), q = 1.0f / x;
+    const unsigned ur = r != r ? 0x7FC00000u : __float_as_uint(r);
+    const unsigned uq = q != q ? 0x7FC00000u : __float_as_uint(q);
+    unsigned long long hs = ((unsigned long long)u * 0x9E3779B97F4A7C15ull) ^
+                            ((unsigned long long)ur * 0xC2B2AE3D27D4EB4Full);
+    unsigned long long hq = ((unsigned long long)u * 0x9E3779B97F4A7C15ull) ^
+                            ((unsigned long long)uq * 0xC2B2AE3D27D4EB4Full);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        hs += __shfl_xor(hs, off, 64);
+        hq += __shfl_xor(hq, off, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        part[0][threadIdx.x >> 6] = hs;
+        part[1][threadIdx.x >> 6] = hq;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        atomicAdd(&out[0], part[0][0] + part[0][1] + part[0][2] + part[0][3]);
+        atomicAdd(&out[1], part[1][0] + part[1][1] + part[1][2] + part[1][3]);
+    }
+}
+
+int launch_fp32_selfcheck(IroHipContext *ctx, unsigned long long *out) {
+    for (unsigned long long base = 0; base < (1ull << 32); base += (1ull << 28)) {
+        hipLaunchKernelGGL(fp32_selfcheck_kernel, dim3(1u << 20), dim3(256), 0, ctx->stream, out,
+                           (unsigned)base);
+        IRO_HIP_CHECK_LAUNCH(ctx);
+    }
+    return 0;
+}
+
 // All 2^32 inputs in 16 launches of 2^20 blocks; out[2] must start zeroed.
 int launch_silu_selfcheck(IroHipContext *ctx, unsigned long long *out) {
     for (unsigned long long base = 0; base < (1ull << 32); base += (1ull << 28)) {

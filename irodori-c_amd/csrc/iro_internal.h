@@ -173,6 +173,7 @@ struct GemmArgs {
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi);
 int launch_silu_selfcheck(IroHipContext *ctx, unsigned long long *out);
+int launch_fp32_selfcheck(IroHipContext *ctx, unsigned long long *out);
 
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 

@@ -105,6 +105,8 @@ def load() -> C.CDLL:
         "iro_hip_dit_stack_destroy": ([_vp], None),
         "iro_hip_selfcheck_silu": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_stack_use_graph": ([_vp, _i], _i),
+        "iro_hip_dit_adaln_apply": ([_vp, _vp, _i, _i, _i, _vp, _vp, C.c_float, _vp], _i),
+        "iro_hip_selfcheck_fp32": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_profile_enable": ([_vp, _i], _i),
         "iro_hip_profile_reset": ([_vp], _i),
         "iro_hip_profile_kinds": ([], _i),
@@ -334,6 +336,13 @@ class Context:
     def selfcheck(self) -> int:
         return self.lib.iro_hip_selfcheck(self.h)
 
+    def selfcheck_fp32(self):
+        """(sqrtf digest, 1/x digest) over every float input."""
+        d, r = C.c_ulonglong(0), C.c_ulonglong(0)
+        self._check(self.lib.iro_hip_selfcheck_fp32(self.h, C.byref(d), C.byref(r)),
+                    "selfcheck_fp32")
+        return int(d.value), int(r.value)
+
     def selfcheck_silu(self):
         """(expf digest over every float input, fast-division mismatches)."""
         d, m = C.c_ulonglong(0), C.c_ulonglong(0)
@@ -366,6 +375,11 @@ class Context:
         w = Weight(self, h.value)
         self._weights.append(w)
         return w
+
+    def dit_adaln_apply(self, x: DeviceArray, B: int, S: int, D: int, shift: DeviceArray,
+                        scale: DeviceArray, eps: float, h: DeviceArray):
+        self._check(self.lib.iro_hip_dit_adaln_apply(self.h, x.vp, B, S, D, shift.vp, scale.vp,
+                                                     eps, h.vp), "dit_adaln_apply")
 
     def weight_from_st(self, st: Safetensors, name: str, transposed: bool = False) -> Weight:
         h = C.c_void_p()

@@ -350,6 +350,66 @@ unsigned long long orc_expf_digest(int threads) {
     return sum;
 }
 
+/* The same digest form for the host's sqrtf(x) and 1.0f / x (IEEE, as the
+   strict reference computes them) over every float input. */
+void orc_fp32_digests(int threads, unsigned long long *sqrt_digest,
+                      unsigned long long *recip_digest) {
+    unsigned long long hs = 0, hq = 0;
+#ifdef _OPENMP
+    if (threads < 1) threads = 1;
+#pragma omp parallel for schedule(static) reduction(+ : hs, hq) num_threads(threads)
+#else
+    (void)threads;
+#endif
+    for (long long hi = 0; hi < 65536; hi++) {
+        for (uint32_t lo = 0; lo < 65536; lo++) {
+            const uint32_t u = ((uint32_t)hi << 16) | lo;
+            float x;
+            memcpy(&x, &u, sizeof x);
+            const float r = sqrtf(x), q = 1.0f / x;
+            uint32_t ur, uq;
+            memcpy(&ur, &r, 4);
+            memcpy(&uq, &q, 4);
+            if (r != r) ur = 0x7FC00000u;
+            if (q != q) uq = 0x7FC00000u;
+            hs += ((unsigned long long)u * 0x9E3779B97F4A7C15ull) ^
+                  ((unsigned long long)ur * 0xC2B2AE3D27D4EB4Full);
+            hq += ((unsigned long long)u * 0x9E3779B97F4A7C15ull) ^
+                  ((unsigned long long)uq * 0xC2B2AE3D27D4EB4Full);
+        }
+    }
+    *sqrt_digest = hs;
+    *recip_digest = hq;
+}
+
+/* ---- adaLN RMSNorm modulate: dit.c:593-606 ------------------------------ */
+
+/* h = x * inv * (1 + scale[b]) + shift[b] for the rows of branch b = row / S,
+   inv = 1 / sqrtf(ms / D + eps), ms the row's sum of squares accumulated in
+   order d = 0 .. D-1 (each square rounded, then added), as the strict build
+   evaluates dit.c:597-603. */
+void orc_adaln_apply(const float *x, const float *shift, const float *scale, int B, int S, int D,
+                     float eps, float *h) {
+    for (int b = 0; b < B; b++) {
+        for (int s = 0; s < S; s++) {
+            const float *row = x + ((size_t)b * S + s) * D;
+            float *out = h + ((size_t)b * S + s) * D;
+            float ms = 0.0f;
+            for (int d = 0; d < D; d++) {
+                const float sq = row[d] * row[d];
+                ms = ms + sq;
+            }
+            const float inv = 1.0f / sqrtf(ms / (float)D + eps);
+            const float *sh = shift + (size_t)b * D, *sc = scale + (size_t)b * D;
+            for (int d = 0; d < D; d++) {
+                const float t = row[d] * inv;
+                const float m = t * (1.0f + sc[d]);
+                out[d] = m + sh[d];
+            }
+        }
+    }
+}
+
 /* ---- gated residual: dit.c:1013-1020, 1032-1039 ------------------------ */
 
 void orc_gated_residual(int conv, float *x, const float *gate,

@@ -84,6 +84,15 @@ long long orc_expf_mismatches(int threads);
    (bits(orc_expf_restated(x)) * 0xC2B2AE3D27D4EB4F), NaN results counted as
    0x7FC00000: the digest a device restatement must reproduce. */
 unsigned long long orc_expf_digest(int threads);
+/* dit.c:593-606 (strict build): the adaLN RMSNorm modulate of x [B*S, D]
+   with branch rows shift/scale [B, D]; the sum of squares runs in index
+   order, as the strict build accumulates it. */
+/* Digests of the host's sqrtf and 1.0f / x over every float input, in the
+   form of orc_expf_digest. */
+void orc_fp32_digests(int threads, unsigned long long *sqrt_digest,
+                      unsigned long long *recip_digest);
+void orc_adaln_apply(const float *x, const float *shift, const float *scale, int B, int S, int D,
+                     float eps, float *h);
 
 /* dit.c:1013-1020 / 1032-1039: x[b,s,:] += gate[b,:] * branch[b,s,:].
    Strict: two roundings.  Fast-math: one FMA (vfmadd132ps). */

@@ -60,6 +60,10 @@ class Oracle:
         L.orc_expf_mismatches.restype = C.c_longlong
         L.orc_expf_digest.argtypes = [C.c_int]
         L.orc_expf_digest.restype = C.c_ulonglong
+        L.orc_fp32_digests.argtypes = [C.c_int, C.POINTER(C.c_ulonglong),
+                                       C.POINTER(C.c_ulonglong)]
+        L.orc_adaln_apply.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_float,
+                                      _f32p]
         L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
         L.orc_conv1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p,
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int,
@@ -169,6 +173,19 @@ class Oracle:
     def expf_digest(self):
         return int(self.lib.orc_expf_digest(self.threads))
 
+    def fp32_digests(self):
+        d, r = C.c_ulonglong(0), C.c_ulonglong(0)
+        self.lib.orc_fp32_digests(self.threads, C.byref(d), C.byref(r))
+        return int(d.value), int(r.value)
+
+    def adaln_apply(self, x, shift, scale, B, S, eps):
+        x, shift, scale = _f32(x), _f32(shift), _f32(scale)
+        D = x.shape[-1]
+        h = np.empty_like(x)
+        self.lib.orc_adaln_apply(_p(x, _f32p), _p(shift, _f32p), _p(scale, _f32p), B, S, D,
+                                 eps, _p(h, _f32p))
+        return h
+
     def gated_residual(self, conv, x, gate, branch, B, S):
         x = np.array(x, np.float32, copy=True)
         D = x.shape[-1]
@@ -269,6 +286,25 @@ class Reference:
         L.ref_convtranspose1d_int8.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                                C.c_int, C.c_int, _i8p, _f32p, _i32p, _f32p, _f32p]
         L.ref_convtranspose1d_int8.restype = C.c_int
+        L.ref_dit_adaln_zero_rank.argtypes = [C.c_float, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                               C.c_int, C.c_int, _f32p, _f32p,
+                                               C.POINTER(C.c_int)]
+        L.ref_dit_adaln_zero_rank.restype = C.c_int
+
+    def dit_adaln_zero_rank(self, eps, x, cond, shift_bias, scale_bias, gate_bias, B, S):
+        """iro_dit_adaln (dit.c:614) with zero low-rank linears: (h, gate, D)."""
+        x, cond = _f32(x), _f32(cond)
+        D = x.shape[-1]
+        h = np.empty_like(x)
+        gate = np.empty((B, D), np.float32)
+        dim = C.c_int(0)
+        rc = self.lib.ref_dit_adaln_zero_rank(eps, _p(x, _f32p), _p(cond, _f32p),
+                                              _p(_f32(shift_bias), _f32p),
+                                              _p(_f32(scale_bias), _f32p),
+                                              _p(_f32(gate_bias), _f32p), B, S, _p(h, _f32p),
+                                              _p(gate, _f32p), C.byref(dim))
+        assert rc == 0 and dim.value == D, (rc, dim.value, D)
+        return h, gate
 
     def weight_quantize(self, w, transposed_shape=None):
         w = _f32(w)

@@ -54,3 +54,24 @@ int ref_convtranspose1d_int8(const float *input, int T_in, int C_in, int C_out,
     return convtranspose1d_forward_impl(&conv, &w, input, T_in, output, NULL,
                                         NULL, 0);
 }
+
+/* The adaLN of a DiT block (dit.c:561-617, iro_dit_adaln) with its low-rank
+   linears zeroed: each branch then outputs its bias plus its slice of cond
+   (dit.c:543-558), so shift = fl(shift_bias + cond[:, 0:D]) and scale =
+   fl(scale_bias + cond[:, D:2D]) exactly, and h is the reference's RMSNorm
+   modulate (dit.c:593-606) on those rows.  x and h are [B*S, D], cond is
+   [B, 3D], D = the reference's model dimension. */
+#include "dit.h"
+int ref_dit_adaln_zero_rank(float eps, const float *x, const float *cond,
+                            const float *shift_bias, const float *scale_bias,
+                            const float *gate_bias, int B, int S, float *h, float *gate,
+                            int *dim) {
+    const size_t n = (size_t)IRO_DIT_MODEL_DIM * 192;
+    float *z = calloc(n, sizeof(float));
+    if (!z) return -1;
+    IroAdaLN a = {z, z, shift_bias, z, z, scale_bias, z, z, gate_bias};
+    const int rc = iro_dit_adaln(&a, eps, x, cond, B, S, h, gate);
+    free(z);
+    *dim = IRO_DIT_MODEL_DIM;
+    return rc;
+}

@@ -131,3 +131,27 @@ def test_swiglu_mlp_single_term_w2(ctx, oracle):
     err, mism, n, got, want = _swiglu_case(ctx, oracle, 2, 40, 256, 320, 0, residual_w2=False)
     assert mism == 0, f"hidden state: {mism}/{n} differ"
     assert_bits_equal(got, want, "x += gate * W2(one-term)")
+
+
+@pytest.mark.parametrize("B,S,D", [
+    (3, 750, 1024), (3, 40, 1280), (1, 1, 1024),    # registers, 2 rows per wave
+    (2, 5, 600), (1, 3, 1500),                      # partial chunks; 1 row per wave
+    (2, 33, 98), (2, 17, 2052),                     # rows kept in LDS
+    (1, 9, 20000), (1, 7, 16390),                   # rows too long for LDS: chunked
+])
+def test_adaln_apply(ctx, oracle, B, S, D):
+    """dit.c:593-606 on the device: bit-identical to the strict build's
+    evaluation (the oracle's restatement, pinned against the reference build
+    in tests/test_oracle_pins.py); the device evaluates the strict order in
+    both conventions.  The shapes reach each of the three kernels."""
+    x = gauss(620, (B * S, D))
+    x[0] = 0.0
+    if B * S > 2:
+        x[1] = 1e-20
+        x[2, ::5] *= 1e4
+    shift = gauss(621, (B, D), 0.3)
+    scale = gauss(622, (B, D), 0.3)
+    h = ctx.empty((B * S, D), np.float32)
+    ctx.dit_adaln_apply(ctx.to_device(x), B, S, D, ctx.to_device(shift), ctx.to_device(scale),
+                        1e-6, h)
+    assert_bits_equal(h.numpy(), oracle.adaln_apply(x, shift, scale, B, S, 1e-6), "adaLN h")

@@ -188,3 +188,9 @@ def test_silu_gate_pieces_on_every_float(ctx, oracle):
     digest, mismatches = ctx.selfcheck_silu()
     assert mismatches == 0
     assert digest == oracle.expf_digest()
+
+
+def test_sqrt_and_reciprocal_on_every_float(ctx, oracle):
+    """The device's sqrtf and 1 / x, which the adaLN apply uses, equal the
+    host's IEEE results on all 2^32 inputs (digests of every result)."""
+    assert ctx.selfcheck_fp32() == oracle.fp32_digests()

@@ -287,3 +287,35 @@ def test_degenerate_rows_closed_form(oracle, conv):
 def test_expf_restatement_equals_libm_on_every_float(oracle):
     # glibc's expf (the libm call of ops.c:783) restated: all 2^32 inputs
     assert oracle.expf_mismatches() == 0
+
+
+# --- adaLN RMSNorm modulate (dit.c:593-606) ------------------------------------------
+
+
+def _adaln_inputs(B, S, D, seed):
+    x = gauss(seed, (B * S, D))
+    x[1] = 0.0                       # ms = 0: inv = 1 / sqrtf(eps)
+    x[2] = 1e-20                     # squares underflow to denormals / zero
+    x[3, ::7] *= 1e4                 # a row dominated by a few large values
+    cond = gauss(seed + 1, (B, 3 * D), 0.5)
+    sb, cb, gb = (gauss(seed + k, (D,), 0.1) for k in (2, 3, 4))
+    return x, cond, sb, cb, gb
+
+
+def test_adaln_apply_equals_reference_strict_build(oracle):
+    """iro_dit_adaln of the strict reference build, with its low-rank linears
+    zeroed so that shift = fl(bias + cond) exactly, equals the oracle's
+    restatement of the apply step bit for bit; the fast-math build sums the
+    squares in a host-dependent vector order (parity unpinned there), so only
+    its closeness is checked."""
+    D, B, S, eps = 1280, 3, 40, 1e-6  # the reference's model dimension
+    x, cond, sb, cb, gb = _adaln_inputs(B, S, D, 610)
+    shift = (sb[None, :] + cond[:, :D]).astype(np.float32)
+    scale = (cb[None, :] + cond[:, D:2 * D]).astype(np.float32)
+    want = oracle.adaln_apply(x, shift, scale, B, S, eps)
+    h, _ = _ref("strict").dit_adaln_zero_rank(eps, x, cond, sb, cb, gb, B, S)
+    assert _eq(h, want)
+    hf, _ = _ref("fast").dit_adaln_zero_rank(eps, x, cond, sb, cb, gb, B, S)
+    rows = want.reshape(B * S, D)
+    err = np.abs(hf - want).max(axis=1) / (np.abs(rows).max(axis=1) + 1e-30)
+    assert err.max() < 1e-5
