@@ -18,8 +18,9 @@ the codec's int8 Conv1d instead: one conv per step, same JSON line;
 ConvTranspose1d (stage 0: 750 frames, 1536->768, kernel 24, stride 12;
 stage 2: 90000 frames, 384->192, kernel 16, stride 8).
 `--workload adaln` the fp32 adaLN apply step of a DiT block on the same
-M = 2250 rows (one call per step); `--workload weights` the int8 weight
-build from a safetensors checkpoint.
+M = 2250 rows (one call per step), `--workload qknorm` the per-head RMSNorm
+and half-RoPE of q and k; `--workload weights` the int8 weight build from a
+safetensors checkpoint.
 
 Prints one JSON line on stdout; diagnostics go to stderr.
 """
@@ -337,6 +338,83 @@ def adaln_main(args):
     print(json.dumps(out), flush=True)
 
 
+def qknorm_main(args):
+    """QK-norm + half-RoPE (dit.c:638-706) on the stack's q and k: one step =
+    one call of iro_hip_dit_qk_norm_rope, in place on q, k [B*S, D] resident
+    in HBM (x D/64 heads of 64).  Algorithmic bytes: q and k read and written
+    once."""
+    B, S, D = args.batch, args.frames, args.hidden
+    M = B * S
+    q, k = gauss(81, (M, D)), gauss(82, (M, D))
+    qw, kw = gauss(83, (D,), 0.2) + 1.0, gauss(84, (D,), 0.2) + 1.0
+    eps = 1e-6
+    ctx = iro_hip.Context(0, iro_hip.STRICT)
+    log("backend:", ctx.backend())
+    qd, kd, qwd, kwd = ctx.to_device(q), ctx.to_device(k), ctx.to_device(qw), ctx.to_device(kw)
+    ctx.dit_qk_norm_rope(qd, qwd, kd, kwd, B, S, D, eps)
+    first_q, first_k = qd.numpy(), kd.numpy()
+    for _ in range(args.warmup):
+        ctx.dit_qk_norm_rope(qd, qwd, kd, kwd, B, S, D, eps)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    t0 = time.perf_counter()
+    ctx.record(e0)
+    for _ in range(args.steps):
+        ctx.dit_qk_norm_rope(qd, qwd, kd, kwd, B, S, D, eps)
+    ctx.record(e1)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.elapsed_ms(e0, e1) / args.steps
+    ctx.close()
+    alg_bytes = 16 * M * D + 8 * D + 256 * S
+    achieved = alg_bytes / (ev_ms * 1e-3) / 1e9
+    log(f"qknorm: {ev_ms * 1e3:.2f} us/call events, {achieved:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import Oracle
+        o = Oracle()
+        times = []
+        start = time.perf_counter()
+        while len(times) < 20 and time.perf_counter() - start < args.cpu_seconds:
+            t1 = time.perf_counter()
+            oq, ok = o.head_norm_rope(q, qw, k, kw, B, S, eps)
+            times.append(time.perf_counter() - t1)
+        med = sorted(times)[len(times) // 2]
+        same = bool(np.array_equal(oq.view(np.uint32), first_q.view(np.uint32))
+                    and np.array_equal(ok.view(np.uint32), first_k.view(np.uint32)))
+        log(f"cpu baseline: {len(times)} calls, median {med * 1e3:.2f} ms; first GPU call "
+            f"bit-identical: {same}")
+        cpu = {"value": round(2 * M * D // 64 / med / 1e6, 4), "unit": "Mheads/s", "cores": 1,
+               "kind": "port", "ms_per_step": round(med * 1e3, 3),
+               "sample": f"the oracle's dit.c:638-706 restatement on all {M} rows of q and k "
+                         f"({len(times)} calls, median, rotation table included), one thread",
+               "gpu_output_bit_identical": same}
+    out = {
+        "metric": "QK-norm + half-RoPE head rows/s (Mheads/s), 1 GPU",
+        "value": round(2 * M * D // 64 / (ev_ms * 1e-3) / 1e6, 2),
+        "unit": "Mheads/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ev_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Irwin-Hall Gaussian q, k and norm weights)",
+        "config": {"workload": f"fp32 per-head RMSNorm + half-RoPE of q and k, {B} x {S} rows "
+                               f"of {D} ({D // 64} heads of 64), in place, one call per step",
+                   "rows": M, "dim": D, "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "note": f"algorithmic bytes {alg_bytes} per launch (q and k read and "
+                             f"written once, norm weights, rotation table rows)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def weights_main(args):
     """The weight source (safetensors.c:302-530, generate.c:526-544): one step
     = the int8 weights of one DiT block (modulation, Wq/Wk/Wv/Wgate, Wo, W1,
@@ -548,7 +626,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["stack", "weights", "adaln"] + sorted(CONV_WORKLOADS)
+    ap.add_argument("--workload", choices=["stack", "weights", "adaln", "qknorm"]
+                    + sorted(CONV_WORKLOADS)
                     + sorted(CONVT_WORKLOADS),
                     default="stack",
                     help="stack (default): the DiT linear stack; conv7*: the codec int8 Conv1d; "
@@ -588,6 +667,9 @@ def main():
         return
     if args.workload == "adaln":
         adaln_main(args)
+        return
+    if args.workload == "qknorm":
+        qknorm_main(args)
         return
 
     B, S, D, H = args.batch, args.frames, args.hidden, args.mlp

@@ -219,6 +219,23 @@ int iro_hip_weight_load(IroHipContext *ctx, const char *path, IroHipWeight **out
 int iro_hip_dit_adaln_apply(IroHipContext *ctx, const float *x, int B, int S, int D,
                             const float *shift, const float *scale, float eps, float *h);
 
+/* dit.c:638-706 head_rmsnorm_rope_pair, in place on q and k [B*S, D]
+   (D = heads * 64, 16-byte aligned): per 64-wide head row, inv = 1 /
+   sqrtf(mean(x^2) + eps) with the squares summed in index order, x = x *
+   (inv * weight[h*64 + d]); heads h < heads/2 then rotate pair p by position
+   s = row % S of the reference's table (double recurrence of the step 1 /
+   10000^(2p/64), dit.c:641-657, 697-703).  Bit-identical to the strict build.
+   The context keeps the table; a call with more positions than any before it
+   allocates and uploads a longer one (so the first call per length is not
+   capturable). */
+int iro_hip_dit_qk_norm_rope(IroHipContext *ctx, float *q, const float *q_weight, float *k,
+                             const float *k_weight, int B, int S, int D, float eps);
+
+/* dit.c:619-636 head_rmsnorm (the text and speaker keys, no rotation), in
+   place on x [B*S, D]; same arithmetic as above. */
+int iro_hip_dit_head_rmsnorm(IroHipContext *ctx, float *x, const float *weight, int B, int S,
+                             int D, float eps);
+
 /* ---- the int8 linear stack of one Euler step --------------------------- */
 
 /* The int8 projections of `blocks` DiT blocks (dit.h:51-58 IroDiTInt8,

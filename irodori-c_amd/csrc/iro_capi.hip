@@ -313,6 +313,7 @@ void iro_hip_destroy(IroHipContext *ctx) {
     ctx->prof = nullptr;
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->zero16) (void)hipFree(ctx->zero16);
+    if (ctx->rope) (void)hipFree(ctx->rope);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }

@@ -6,6 +6,8 @@
 // group: the split Q/K/V/gate store, silu(w1)*w3, or the gated residual
 // x += gate * y (dit.c:1013-1020, 1032-1039), so the projection outputs of
 // Wo and W2 never round-trip HBM.
+#include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -392,6 +394,103 @@ __global__ __launch_bounds__(64) void adaln_reg_kernel(const float *__restrict__
     }
 }
 
+// dit.c:619-706, the per-head RMSNorm of q and k and the half-RoPE: each
+// 64-wide head row's mean square is summed in index order (the strict
+// build's serial chain), inv = 1 / sqrtf(ms / 64 + eps), x' = x * (inv * w);
+// with ROPE, heads h < heads / 2 rotate the pairs (x'0, x'1) by the table
+// entry of the row's position s = token % S: (x'0 c - x'1 s, x'0 s + x'1 c),
+// each product rounded.  Rows are the head rows of q then of k ([M, heads,
+// 64] each, updated in place); a wave takes 32 of them: 16 lanes per row load
+// float4s (four rows per load), the rounded squares go to LDS, lanes 0..31
+// run the rows' chains, and the same lanes that loaded a row write it.
+constexpr int kHeadRows = 32, kHeadPitch = 68;
+
+template <bool ROPE>
+__global__ __launch_bounds__(64) void head_norm_kernel(float *__restrict__ q,
+                                                       const float *__restrict__ qw,
+                                                       float *__restrict__ k,
+                                                       const float *__restrict__ kw,
+                                                       const float *__restrict__ rope, int M,
+                                                       int S, int heads, int G, float eps) {
+    __shared__ __attribute__((aligned(16))) float sq[kHeadRows * kHeadPitch];
+    __shared__ float inv_s[kHeadRows];
+    const int lane = threadIdx.x, sub = lane >> 4, c4 = (lane & 15) * 4;
+    const int g0 = blockIdx.x * kHeadRows;
+    const int MH = M * heads;
+    float4 v[8];
+    float *rowp[8];
+    int head[8], pos[8];
+    bool live[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        int g = g0 + 4 * j + sub;
+        live[j] = g < G;
+        g = live[j] ? g : G - 1;
+        const int t = g >= MH;
+        const int local = g - (t ? MH : 0);
+        const int token = local / heads;
+        head[j] = local - token * heads;
+        pos[j] = token % S;
+        rowp[j] = (t ? k : q) + (size_t)local * 64;
+        v[j] = *reinterpret_cast<const float4 *>(rowp[j] + c4);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        float4 e;
+        e.x = v[j].x * v[j].x;
+        e.y = v[j].y * v[j].y;
+        e.z = v[j].z * v[j].z;
+        e.w = v[j].w * v[j].w;
+        *reinterpret_cast<float4 *>(&sq[(4 * j + sub) * kHeadPitch + c4]) = e;
+    }
+    __syncthreads();
+    if (lane < kHeadRows) {
+        const float *tr = &sq[lane * kHeadPitch];
+        float ms = 0.0f;
+#pragma unroll
+        for (int b0 = 0; b0 < 16; b0 += 8) {
+            float4 e[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e[i] = *reinterpret_cast<const float4 *>(tr + 4 * (b0 + i));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ms = ms + e[i].x;
+                ms = ms + e[i].y;
+                ms = ms + e[i].z;
+                ms = ms + e[i].w;
+            }
+        }
+        inv_s[lane] = 1.0f / __builtin_sqrtf(ms / 64.0f + eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if (!live[j]) continue;
+        const float inv = inv_s[4 * j + sub];
+        const int g = g0 + 4 * j + sub;
+        const float *w = (g >= MH ? kw : qw) + head[j] * 64 + c4;
+        const float4 wv = *reinterpret_cast<const float4 *>(w);
+        float4 o;
+        o.x = v[j].x * (inv * wv.x);
+        o.y = v[j].y * (inv * wv.y);
+        o.z = v[j].z * (inv * wv.z);
+        o.w = v[j].w * (inv * wv.w);
+        if (ROPE && head[j] < heads / 2) {
+            // Pairs c4/2 and c4/2 + 1 of this position.
+            const float *tab = rope + (size_t)pos[j] * 64 + (c4 >> 1);
+            const float2 cs = *reinterpret_cast<const float2 *>(tab);
+            const float2 sn = *reinterpret_cast<const float2 *>(tab + 32);
+            float4 r;
+            r.x = (o.x * cs.x) - (o.y * sn.x);
+            r.y = (o.x * sn.x) + (o.y * cs.x);
+            r.z = (o.z * cs.y) - (o.w * sn.y);
+            r.w = (o.z * sn.y) + (o.w * cs.y);
+            o = r;
+        }
+        *reinterpret_cast<float4 *>(rowp[j] + c4) = o;
+    }
+}
+
 int qkvg_impl(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w, float *q,
               float *k, float *v, float *gate, int residual) {
     const int D = w->K;
@@ -668,6 +767,86 @@ int iro_hip_dit_adaln_apply(IroHipContext *ctx, const float *x, int B, int S, in
                            scale, M, S, D, eps, h);
     IRO_HIP_CHECK_LAUNCH(ctx);
     return 0;
+}
+
+// The rotation table of dit.c:641-657 and 697-703 for positions 0..S-1, in
+// the context: per pair p the double step (cos, sin) of 1 / 10000^(2p/64)
+// from the C library, then position s+1 = position s times the step (each
+// double product rounded, no fused multiply-add; this file is compiled with
+// contraction off), stored as float.  Position s's entry does not depend on S,
+// so a longer table serves every shorter sequence; it is rebuilt only when a
+// call needs more positions (the first call per length allocates).
+static int rope_table(IroHipContext *ctx, int S) {
+    if (S <= ctx->rope_S) return 0;
+    const int n = S < 1024 ? 1024 : S;
+    std::vector<float> tab((size_t)n * 64);
+    double cs[32], sn[32], c[32], s[32];
+    for (int p = 0; p < 32; ++p) {
+        const double theta = 1.0 / std::pow(10000.0, (double)(2 * p) / 64.0);
+        cs[p] = std::cos(theta);
+        sn[p] = std::sin(theta);
+        c[p] = 1.0;
+        s[p] = 0.0;
+    }
+    for (int t = 0; t < n; ++t) {
+        for (int p = 0; p < 32; ++p) {
+            tab[(size_t)t * 64 + p] = (float)c[p];
+            tab[(size_t)t * 64 + 32 + p] = (float)s[p];
+        }
+        for (int p = 0; p < 32; ++p) {
+            const double a = c[p] * cs[p], b = s[p] * sn[p];
+            const double e = s[p] * cs[p], f = c[p] * sn[p];
+            c[p] = a - b;
+            s[p] = e + f;
+        }
+    }
+    float *dev = nullptr;
+    if (hipMalloc(&dev, tab.size() * sizeof(float)) != hipSuccess)
+        return set_error(ctx, "dit_qk_norm_rope: out of device memory for the rotation table");
+    if (hipMemcpyAsync(dev, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice,
+                       ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        (void)hipFree(dev);
+        return set_error(ctx, "dit_qk_norm_rope: rotation table upload failed");
+    }
+    if (ctx->rope) (void)hipFree(ctx->rope);
+    ctx->rope = dev;
+    ctx->rope_S = n;
+    return 0;
+}
+
+static int head_norm(IroHipContext *ctx, float *q, const float *qw, float *k, const float *kw,
+                     int B, int S, int D, float eps, bool rope, const char *name) {
+    if (!ctx || B < 0 || S < 0 || D <= 0 || D % 64 || !q || !qw || (k && !kw) ||
+        (rope && !k))
+        return set_error(ctx, "%s: invalid arguments (D must be a multiple of 64)", name);
+    const long long M = (long long)B * S;
+    if (M == 0) return 0;
+    const int heads = D / 64;
+    const long long G = M * heads * (k ? 2 : 1);
+    if (G > INT32_MAX - kHeadRows) return set_error(ctx, "%s: too many rows", name);
+    if (((((uintptr_t)q) | ((uintptr_t)qw) | ((uintptr_t)k) | ((uintptr_t)kw)) & 15) != 0)
+        return set_error(ctx, "%s: q, k and the weights must be 16-byte aligned", name);
+    if (rope && rope_table(ctx, S)) return -1;
+    const dim3 grid((unsigned)((G + kHeadRows - 1) / kHeadRows)), block(64);
+    if (rope)
+        hipLaunchKernelGGL((head_norm_kernel<true>), grid, block, 0, ctx->stream, q, qw, k, kw,
+                           ctx->rope, (int)M, S, heads, (int)G, eps);
+    else
+        hipLaunchKernelGGL((head_norm_kernel<false>), grid, block, 0, ctx->stream, q, qw, k, kw,
+                           nullptr, (int)M, S, heads, (int)G, eps);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+int iro_hip_dit_qk_norm_rope(IroHipContext *ctx, float *q, const float *q_weight, float *k,
+                             const float *k_weight, int B, int S, int D, float eps) {
+    return head_norm(ctx, q, q_weight, k, k_weight, B, S, D, eps, true, "dit_qk_norm_rope");
+}
+
+int iro_hip_dit_head_rmsnorm(IroHipContext *ctx, float *x, const float *weight, int B, int S,
+                             int D, float eps) {
+    return head_norm(ctx, x, weight, nullptr, nullptr, B, S, D, eps, false, "dit_head_rmsnorm");
 }
 
 int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int residual_mask,

@@ -51,6 +51,8 @@ struct IroHipContext {
     int gemm_ring = 0;    // weight ring depth of the whole-tile kernel (0: default)
     int gemm_spb = 0;     // column slabs per whole-tile block (0: chosen per GEMM)
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
+    float *rope = nullptr;  // rotation table: per position cos[32] then sin[32]
+    int rope_S = 0;         // positions held by rope
 };
 
 // A quantized weight, pre-packed for the MFMA B operand.

@@ -106,6 +106,8 @@ def load() -> C.CDLL:
         "iro_hip_selfcheck_silu": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_stack_use_graph": ([_vp, _i], _i),
         "iro_hip_dit_adaln_apply": ([_vp, _vp, _i, _i, _i, _vp, _vp, C.c_float, _vp], _i),
+        "iro_hip_dit_qk_norm_rope": ([_vp, _vp, _vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
+        "iro_hip_dit_head_rmsnorm": ([_vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
         "iro_hip_selfcheck_fp32": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_profile_enable": ([_vp, _i], _i),
         "iro_hip_profile_reset": ([_vp], _i),
@@ -380,6 +382,19 @@ class Context:
                         scale: DeviceArray, eps: float, h: DeviceArray):
         self._check(self.lib.iro_hip_dit_adaln_apply(self.h, x.vp, B, S, D, shift.vp, scale.vp,
                                                      eps, h.vp), "dit_adaln_apply")
+
+    def dit_qk_norm_rope(self, q: DeviceArray, q_weight: DeviceArray, k: DeviceArray,
+                         k_weight: DeviceArray, B: int, S: int, D: int, eps: float):
+        """dit.c:638-706 in place on q, k [B*S, D]."""
+        self._check(self.lib.iro_hip_dit_qk_norm_rope(self.h, q.vp, q_weight.vp, k.vp,
+                                                      k_weight.vp, B, S, D, eps),
+                    "dit_qk_norm_rope")
+
+    def dit_head_rmsnorm(self, x: DeviceArray, weight: DeviceArray, B: int, S: int, D: int,
+                         eps: float):
+        """dit.c:619-636 in place on x [B*S, D]."""
+        self._check(self.lib.iro_hip_dit_head_rmsnorm(self.h, x.vp, weight.vp, B, S, D, eps),
+                    "dit_head_rmsnorm")
 
     def weight_from_st(self, st: Safetensors, name: str, transposed: bool = False) -> Weight:
         h = C.c_void_p()

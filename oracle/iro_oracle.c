@@ -410,6 +410,94 @@ void orc_adaln_apply(const float *x, const float *shift, const float *scale, int
     }
 }
 
+/* ---- per-head RMSNorm and half-RoPE: dit.c:619-706 ---------------------- */
+
+/* The rotation table of head_rmsnorm_rope_pair (dit.c:641-657, 697-703): per
+   pair p of a 64-wide head, the angle step 1 / 10000^(2p/64) as a double
+   cosine/sine pair from libm, and position s's rotation advanced from
+   position s-1 by one complex multiplication in double (each product rounded,
+   no fused multiply-add), rounded to float for use.  cos_t/sin_t are
+   [S][32]. */
+void orc_rope_table(int S, float *cos_t, float *sin_t) {
+    double cs[32], sn[32], c[32], s[32];
+    for (int p = 0; p < 32; p++) {
+        const double theta = 1.0 / pow(10000.0, (double)(2 * p) / 64.0);
+        cs[p] = cos(theta);
+        sn[p] = sin(theta);
+        c[p] = 1.0;
+        s[p] = 0.0;
+    }
+    for (int t = 0; t < S; t++) {
+        for (int p = 0; p < 32; p++) {
+            cos_t[(size_t)t * 32 + p] = (float)c[p];
+            sin_t[(size_t)t * 32 + p] = (float)s[p];
+        }
+        for (int p = 0; p < 32; p++) {
+            const double a = c[p] * cs[p], b = s[p] * sn[p];
+            const double e = s[p] * cs[p], f = c[p] * sn[p];
+            c[p] = a - b;
+            s[p] = e + f;
+        }
+    }
+}
+
+/* One 64-wide head row: mean square in index order, inv = 1/sqrtf(ms/64 +
+   eps), then either y = x * (inv * w) or, for a rotated head, the pairs
+   (y0, y1) = (x0' c - x1' s, x0' s + x1' c) with x' = x * (inv * w)
+   (dit.c:619-636, 666-695). */
+static void orc_head_row(float *row, const float *w, float eps, const float *ct, const float *st) {
+    float ms = 0.0f;
+    for (int d = 0; d < 64; d++) {
+        const float sq = row[d] * row[d];
+        ms = ms + sq;
+    }
+    const float inv = 1.0f / sqrtf(ms / 64.0f + eps);
+    if (!ct) {
+        for (int d = 0; d < 64; d++) row[d] = row[d] * (inv * w[d]);
+        return;
+    }
+    for (int p = 0; p < 32; p++) {
+        const float x0 = row[2 * p] * (inv * w[2 * p]);
+        const float x1 = row[2 * p + 1] * (inv * w[2 * p + 1]);
+        const float a = x0 * ct[p], b = x1 * st[p];
+        const float e = x0 * st[p], f = x1 * ct[p];
+        row[2 * p] = a - b;
+        row[2 * p + 1] = e + f;
+    }
+}
+
+/* q, k [B*S, heads*64] in place.  rope != 0: head_rmsnorm_rope_pair
+   (dit.c:638-706), the first heads/2 heads rotated by position s; rope == 0:
+   head_rmsnorm (dit.c:619-636) on q alone (k may be NULL). */
+int orc_head_norm_rope(float *q, const float *qw, float *k, const float *kw, int B, int S,
+                       int heads, float eps, int rope) {
+    float *ct = NULL, *st = NULL;
+    if (rope) {
+        ct = malloc(sizeof(float) * (size_t)S * 32);
+        st = malloc(sizeof(float) * (size_t)S * 32);
+        if (!ct || !st) {
+            free(ct);
+            free(st);
+            return -1;
+        }
+        orc_rope_table(S, ct, st);
+    }
+    const int D = heads * 64;
+    for (int b = 0; b < B; b++)
+        for (int s = 0; s < S; s++)
+            for (int h = 0; h < heads; h++) {
+                const size_t off = ((size_t)b * S + s) * D + (size_t)h * 64;
+                const int rot = rope && h < heads / 2;
+                const float *c = rot ? ct + (size_t)s * 32 : NULL;
+                const float *sn = rot ? st + (size_t)s * 32 : NULL;
+                orc_head_row(q + off, qw + h * 64, eps, c, sn);
+                if (k) orc_head_row(k + off, kw + h * 64, eps, c, sn);
+            }
+    free(ct);
+    free(st);
+    return 0;
+}
+
 /* ---- gated residual: dit.c:1013-1020, 1032-1039 ------------------------ */
 
 void orc_gated_residual(int conv, float *x, const float *gate,

@@ -93,6 +93,9 @@ void orc_fp32_digests(int threads, unsigned long long *sqrt_digest,
                       unsigned long long *recip_digest);
 void orc_adaln_apply(const float *x, const float *shift, const float *scale, int B, int S, int D,
                      float eps, float *h);
+void orc_rope_table(int S, float *cos_t, float *sin_t);
+int orc_head_norm_rope(float *q, const float *qw, float *k, const float *kw, int B, int S,
+                       int heads, float eps, int rope);
 
 /* dit.c:1013-1020 / 1032-1039: x[b,s,:] += gate[b,:] * branch[b,s,:].
    Strict: two roundings.  Fast-math: one FMA (vfmadd132ps). */

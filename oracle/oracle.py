@@ -65,6 +65,10 @@ class Oracle:
         L.orc_adaln_apply.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_float,
                                       _f32p]
         L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_rope_table.argtypes = [C.c_int, _f32p, _f32p]
+        L.orc_head_norm_rope.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int,
+                                         C.c_float, C.c_int]
+        L.orc_head_norm_rope.restype = C.c_int
         L.orc_conv1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p,
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int,
                                       _f32p, _u8p, _f32p, _i32p, C.c_int]
@@ -186,6 +190,26 @@ class Oracle:
                                  eps, _p(h, _f32p))
         return h
 
+    def rope_table(self, S):
+        """(cos, sin) [S, 32] of head_rmsnorm_rope_pair (dit.c:641-657, 697-703)."""
+        c = np.empty((S, 32), np.float32)
+        s = np.empty((S, 32), np.float32)
+        self.lib.orc_rope_table(S, _p(c, _f32p), _p(s, _f32p))
+        return c, s
+
+    def head_norm_rope(self, q, qw, k, kw, B, S, eps, rope=True):
+        """dit.c:638-706 (rope) or dit.c:619-636 (no rope, k may be None) on
+        copies of q, k [B*S, heads*64]; returns (q, k)."""
+        q = np.array(q, np.float32, copy=True)
+        heads = q.shape[-1] // 64
+        kk = None if k is None else np.array(k, np.float32, copy=True)
+        rc = self.lib.orc_head_norm_rope(_p(q, _f32p), _p(_f32(qw), _f32p),
+                                         None if kk is None else _p(kk, _f32p),
+                                         None if kw is None else _p(_f32(kw), _f32p),
+                                         B, S, heads, eps, 1 if rope else 0)
+        assert rc == 0
+        return q, kk
+
     def gated_residual(self, conv, x, gate, branch, B, S):
         x = np.array(x, np.float32, copy=True)
         D = x.shape[-1]
@@ -290,6 +314,26 @@ class Reference:
                                                C.c_int, C.c_int, _f32p, _f32p,
                                                C.POINTER(C.c_int)]
         L.ref_dit_adaln_zero_rank.restype = C.c_int
+        L.ref_head_rmsnorm_rope_pair.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int,
+                                                 C.c_float, C.POINTER(C.c_int),
+                                                 C.POINTER(C.c_int)]
+        L.ref_head_rmsnorm.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_float]
+
+    def head_rmsnorm_rope_pair(self, q, qw, k, kw, B, S, eps):
+        """dit.c:638-706 on copies of q, k [B*S, MODEL_DIM]: (q, k, heads)."""
+        q, k = np.array(q, np.float32, copy=True), np.array(k, np.float32, copy=True)
+        dim, heads = C.c_int(0), C.c_int(0)
+        self.lib.ref_head_rmsnorm_rope_pair(_p(q, _f32p), _p(_f32(qw), _f32p), _p(k, _f32p),
+                                            _p(_f32(kw), _f32p), B, S, eps, C.byref(dim),
+                                            C.byref(heads))
+        assert dim.value == q.shape[-1], (dim.value, q.shape)
+        return q, k, heads.value
+
+    def head_rmsnorm(self, x, w, B, S, eps):
+        """dit.c:619-636 on a copy of x [B*S, MODEL_DIM]."""
+        x = np.array(x, np.float32, copy=True)
+        self.lib.ref_head_rmsnorm(_p(x, _f32p), _p(_f32(w), _f32p), B, S, eps)
+        return x
 
     def dit_adaln_zero_rank(self, eps, x, cond, shift_bias, scale_bias, gate_bias, B, S):
         """iro_dit_adaln (dit.c:614) with zero low-rank linears: (h, gate, D)."""

@@ -18,6 +18,7 @@ still pinned bit-exactly at its own boundary from the GPU's hidden state.
 import numpy as np
 import pytest
 
+import iro_hip
 from iro_synth import gauss, heavy_tail, rms_rows
 from parity_util import assert_bits_equal, rel_err
 
@@ -155,3 +156,56 @@ def test_adaln_apply(ctx, oracle, B, S, D):
     ctx.dit_adaln_apply(ctx.to_device(x), B, S, D, ctx.to_device(shift), ctx.to_device(scale),
                         1e-6, h)
     assert_bits_equal(h.numpy(), oracle.adaln_apply(x, shift, scale, B, S, 1e-6), "adaLN h")
+
+
+@pytest.mark.parametrize("B,S,D", [(3, 750, 1024), (2, 40, 1280), (1, 1, 64), (3, 7, 192)])
+def test_qk_norm_rope(ctx, oracle, B, S, D):
+    """dit.c:638-706 on the device, in place on q and k: bit-identical to the
+    oracle's restatement (pinned bit for bit against the strict reference
+    build in tests/test_oracle_pins.py), rotated and plain heads, positions
+    across the rotation table, zero, tiny and large head rows."""
+    q = gauss(640, (B * S, D))
+    k = gauss(641, (B * S, D))
+    q[0, :64] = 0.0
+    if B * S > 2:
+        k[1, :64] = 1e-20
+        q[2, -64:] *= 1e4
+    qw, kw = gauss(642, (D,), 0.2) + 1.0, gauss(643, (D,), 0.2) + 1.0
+    qd, kd = ctx.to_device(q), ctx.to_device(k)
+    ctx.dit_qk_norm_rope(qd, ctx.to_device(qw), kd, ctx.to_device(kw), B, S, D, 1e-6)
+    want_q, want_k = oracle.head_norm_rope(q, qw, k, kw, B, S, 1e-6)
+    assert_bits_equal(qd.numpy(), want_q, "q")
+    assert_bits_equal(kd.numpy(), want_k, "k")
+
+
+def test_qk_norm_rope_table_grows(ctx, oracle):
+    """A call with more positions than any before rebuilds the context's
+    rotation table; shorter calls after it use the prefix."""
+    D = 1280
+    qw, kw = gauss(652, (D,), 0.2) + 1.0, gauss(653, (D,), 0.2) + 1.0
+    qwd, kwd = ctx.to_device(qw), ctx.to_device(kw)
+    for (B, S) in [(1, 300), (1, 2500), (2, 100)]:
+        q, k = gauss(650 + S, (B * S, D)), gauss(651 + S, (B * S, D))
+        qd, kd = ctx.to_device(q), ctx.to_device(k)
+        ctx.dit_qk_norm_rope(qd, qwd, kd, kwd, B, S, D, 1e-6)
+        want_q, want_k = oracle.head_norm_rope(q, qw, k, kw, B, S, 1e-6)
+        assert_bits_equal(qd.numpy(), want_q, f"q S={S}")
+        assert_bits_equal(kd.numpy(), want_k, f"k S={S}")
+
+
+@pytest.mark.parametrize("B,T,D", [(3, 64, 1280), (1, 5, 1024)])
+def test_head_rmsnorm(ctx, oracle, B, T, D):
+    """dit.c:619-636 (text and speaker keys): no rotation, one tensor."""
+    x = gauss(660, (B * T, D))
+    x[0, 64:128] = 0.0
+    w = gauss(661, (D,), 0.2) + 1.0
+    xd = ctx.to_device(x)
+    ctx.dit_head_rmsnorm(xd, ctx.to_device(w), B, T, D, 1e-6)
+    want, _ = oracle.head_norm_rope(x, w, None, None, B, T, 1e-6, rope=False)
+    assert_bits_equal(xd.numpy(), want, "x")
+
+
+def test_qk_norm_rope_rejects_bad_shapes(ctx):
+    q = ctx.empty((4, 100), np.float32)
+    with pytest.raises(iro_hip.HipError):
+        ctx.dit_qk_norm_rope(q, q, q, q, 1, 4, 100, 1e-6)
