@@ -498,6 +498,86 @@ int orc_head_norm_rope(float *q, const float *qw, float *k, const float *kw, int
     return 0;
 }
 
+/* ---- attention core: dit.c:808-870 with the scalar ops (ops.c:577-600,
+   681-703, 754-766, 786-789) ---------------------------------------------- */
+
+/* Per batch b and head h: the joined keys are the S latent tokens of b, then
+   the context rows ci < C whose mask[b*C + ci] is set, in order (context row
+   ci of batch b is row ci of the shared context when context_batch == 1, else
+   row b*C + ci).  score = sum_d q[d] k[d] in index order, times 1/sqrtf(64);
+   softmax per query row: max by strict replacement from the first score,
+   p = expf(score - max), sum of p in key order, p / sum; out[n] = sum_j p_j
+   v_j[n] in key order; mix = out * (1 / (1 + expf(-gate))).  q, k, v, gate,
+   mix [B*S, D]; ck, cv [(context_batch == 1 ? 1 : B) * C, D]. */
+int orc_attention_core(const float *q, const float *k, const float *v, const float *gate, int B,
+                       int S, int D, const float *ck, const float *cv, const uint8_t *mask, int C,
+                       int context_batch, float *mix) {
+    const int heads = D / 64;
+    const float scale = 1.0f / sqrtf(64.0f);
+    const float **kr = malloc(sizeof(float *) * (size_t)(S + C));
+    const float **vr = malloc(sizeof(float *) * (size_t)(S + C));
+    float *sc = malloc(sizeof(float) * (size_t)(S + C));
+    if (!kr || !vr || !sc) {
+        free(kr);
+        free(vr);
+        free(sc);
+        return -1;
+    }
+    for (int b = 0; b < B; b++) {
+        for (int h = 0; h < heads; h++) {
+            int J = 0;
+            for (int t = 0; t < S; t++) {
+                kr[J] = k + ((size_t)b * S + t) * D + h * 64;
+                vr[J++] = v + ((size_t)b * S + t) * D + h * 64;
+            }
+            const size_t crow = context_batch == 1 ? 0 : (size_t)b * C;
+            for (int ci = 0; ci < C; ci++) {
+                if (!mask[(size_t)b * C + ci]) continue;
+                kr[J] = ck + (crow + ci) * D + h * 64;
+                vr[J++] = cv + (crow + ci) * D + h * 64;
+            }
+            for (int s = 0; s < S; s++) {
+                const float *qs = q + ((size_t)b * S + s) * D + h * 64;
+                for (int j = 0; j < J; j++) {
+                    float acc = 0.0f;
+                    for (int d = 0; d < 64; d++) {
+                        const float pr = qs[d] * kr[j][d];
+                        acc = acc + pr;
+                    }
+                    sc[j] = acc * scale;
+                }
+                float mx = sc[0];
+                for (int j = 1; j < J; j++)
+                    if (sc[j] > mx) mx = sc[j];
+                float sum = 0.0f;
+                for (int j = 0; j < J; j++) {
+                    sc[j] = expf(sc[j] - mx);
+                    sum = sum + sc[j];
+                }
+                for (int j = 0; j < J; j++) sc[j] = sc[j] / sum;
+                float *out = mix + ((size_t)b * S + s) * D + h * 64;
+                for (int n = 0; n < 64; n++) {
+                    float acc = 0.0f;
+                    for (int j = 0; j < J; j++) {
+                        const float pr = sc[j] * vr[j][n];
+                        acc = acc + pr;
+                    }
+                    out[n] = acc;
+                }
+            }
+        }
+    }
+    const size_t n = (size_t)B * S * D;
+    for (size_t i = 0; i < n; i++) {
+        const float r = 1.0f / (1.0f + expf(-gate[i]));
+        mix[i] = mix[i] * r;
+    }
+    free(kr);
+    free(vr);
+    free(sc);
+    return 0;
+}
+
 /* ---- gated residual: dit.c:1013-1020, 1032-1039 ------------------------ */
 
 void orc_gated_residual(int conv, float *x, const float *gate,

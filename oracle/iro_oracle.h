@@ -96,6 +96,9 @@ void orc_adaln_apply(const float *x, const float *shift, const float *scale, int
 void orc_rope_table(int S, float *cos_t, float *sin_t);
 int orc_head_norm_rope(float *q, const float *qw, float *k, const float *kw, int B, int S,
                        int heads, float eps, int rope);
+int orc_attention_core(const float *q, const float *k, const float *v, const float *gate, int B,
+                       int S, int D, const float *ck, const float *cv, const uint8_t *mask, int C,
+                       int context_batch, float *mix);
 
 /* dit.c:1013-1020 / 1032-1039: x[b,s,:] += gate[b,:] * branch[b,s,:].
    Strict: two roundings.  Fast-math: one FMA (vfmadd132ps). */

@@ -69,6 +69,9 @@ class Oracle:
         L.orc_head_norm_rope.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int,
                                          C.c_float, C.c_int]
         L.orc_head_norm_rope.restype = C.c_int
+        L.orc_attention_core.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int,
+                                         _f32p, _f32p, _u8p, C.c_int, C.c_int, _f32p]
+        L.orc_attention_core.restype = C.c_int
         L.orc_conv1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p,
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int,
                                       _f32p, _u8p, _f32p, _i32p, C.c_int]
@@ -210,6 +213,20 @@ class Oracle:
         assert rc == 0
         return q, kk
 
+    def attention_core(self, q, k, v, gate, B, S, ck, cv, mask, context_batch):
+        """dit.c:808-870 (scalar ops): mix [B*S, D] from q, k, v, gate [B*S, D],
+        context rows ck, cv [(1 or B) * C, D] and mask [B, C]."""
+        q, k, v, gate, ck, cv = (_f32(a) for a in (q, k, v, gate, ck, cv))
+        mask = np.ascontiguousarray(mask, np.uint8)
+        D = q.shape[-1]
+        C = mask.shape[-1]
+        mix = np.empty_like(q)
+        rc = self.lib.orc_attention_core(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p),
+                                         _p(gate, _f32p), B, S, D, _p(ck, _f32p), _p(cv, _f32p),
+                                         _p(mask, _u8p), C, context_batch, _p(mix, _f32p))
+        assert rc == 0
+        return mix
+
     def gated_residual(self, conv, x, gate, branch, B, S):
         x = np.array(x, np.float32, copy=True)
         D = x.shape[-1]
@@ -318,6 +335,24 @@ class Reference:
                                                  C.c_float, C.POINTER(C.c_int),
                                                  C.POINTER(C.c_int)]
         L.ref_head_rmsnorm.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_float]
+        L.ref_dit_attention_identity.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _u8p,
+                                                 C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                                 _f32p]
+        L.ref_dit_attention_identity.restype = C.c_int
+
+    def dit_attention_identity(self, x, q_norm, k_norm, ck, cv, mask, B, S, shared, eps):
+        """iro_dit_attention(_shared_context) (dit.c:895-911) with identity
+        projections: the attention core on (normed x, normed x, x, gate x)."""
+        x = _f32(x)
+        mask = np.ascontiguousarray(mask, np.uint8)
+        out = np.empty_like(x)
+        rc = self.lib.ref_dit_attention_identity(_p(x, _f32p), _p(_f32(q_norm), _f32p),
+                                                 _p(_f32(k_norm), _f32p), _p(_f32(ck), _f32p),
+                                                 _p(_f32(cv), _f32p), _p(mask, _u8p), B, S,
+                                                 mask.shape[-1], int(bool(shared)), eps,
+                                                 _p(out, _f32p))
+        assert rc == 0
+        return out
 
     def head_rmsnorm_rope_pair(self, q, qw, k, kw, B, S, eps):
         """dit.c:638-706 on copies of q, k [B*S, MODEL_DIM]: (q, k, heads)."""

@@ -357,3 +357,29 @@ def test_rope_table_closed_form(oracle):
     assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
     assert np.abs(c - np.cos(ang)).max() < 2e-6
     assert np.abs(s - np.sin(ang)).max() < 2e-6
+
+
+@pytest.mark.parametrize("shared", [0, 1])
+def test_attention_core_equals_reference_strict_build(oracle, shared):
+    """iro_dit_attention / iro_dit_attention_shared_context (dit.c:895-911) of
+    the strict (scalar) reference build with identity projections equal the
+    oracle's head norm + RoPE followed by its attention core on (q, k, v,
+    gate) = (normed x, normed x, x, x), bit for bit: context rows masked in
+    and out (one batch with none), scores with a large spread so some
+    softmax terms underflow to zero."""
+    B, S, C, D, eps = 2, 24, 9, 1280, 1e-6
+    x = gauss(670, (B * S, D))
+    x[3] *= 30.0
+    qn, kn = gauss(671, (D,), 0.2) + 1.0, gauss(672, (D,), 0.2) + 1.0
+    rows = 1 if shared else B
+    ck, cv = gauss(673, (rows * C, D)), gauss(674, (rows * C, D))
+    mask = np.zeros((B, C), np.uint8)
+    mask[0, [0, 2, 3, 8]] = 1
+    got = _ref("strict").dit_attention_identity(x, qn, kn, ck, cv, mask, B, S, shared, eps)
+    q, k = oracle.head_norm_rope(x, qn, x, kn, B, S, eps)
+    want = oracle.attention_core(q, k, x, x, B, S, ck, cv, mask, 1 if shared else B)
+    # The identity Wo adds its zero terms from +0 (ops.c:221-234 scalar linear),
+    # which turns a -0 of the core (a gate whose sigmoid underflows) into +0.
+    want = want + np.float32(0.0)
+    assert (want == 0).any()  # the underflowing gates are exercised
+    assert _eq(got, want)
