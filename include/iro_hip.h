@@ -236,6 +236,33 @@ int iro_hip_dit_qk_norm_rope(IroHipContext *ctx, float *q, const float *q_weight
 int iro_hip_dit_head_rmsnorm(IroHipContext *ctx, float *x, const float *weight, int B, int S,
                              int D, float eps);
 
+/* The joined-key layout of one utterance's attention context
+   (dit.c:815-843): per batch b, the context rows ci < C whose
+   mask[b*C + ci] (host memory) is set, in order -- row ci of the shared
+   context when context_batch == 1 (iro_dit_attention_shared_context,
+   dit.c:903-911), row b*C + ci when context_batch == B (iro_dit_attention,
+   dit.c:895-901).  Made once per utterance (the mask does not change across
+   layers and sampler steps); it allocates and uploads.  Destroy it before
+   its context. */
+typedef struct IroHipAttnContext IroHipAttnContext;
+int iro_hip_dit_attn_context_create(IroHipContext *ctx, const uint8_t *mask, int B, int C,
+                                    int context_batch, IroHipAttnContext **out);
+void iro_hip_dit_attn_context_destroy(IroHipAttnContext *actx);
+
+/* dit.c:808-870, the attention core between head_rmsnorm_rope_pair and Wo,
+   as the reference's scalar build computes it (ops.c:577-600 scores, 754-766
+   softmax, 681-703 P@V, 786-789 gate): per batch b and head h, the joined
+   keys are the S tokens of b (rows of k, v) then the kept context rows (of
+   context_k, context_v, [(context_batch == 1 ? 1 : B) * C, D]);
+   mix[b*S + s, h*64 + n] = sum_j softmax(q.k_j / 8)_j v_j[n], every sum in
+   the scalar build's order, times 1 / (1 + expf(-gate)).  q, k, v, gate, mix
+   [B*S, D], D = heads * 64, all 16-byte aligned device memory.  Bit-identical
+   to the scalar build.  Workspace: 4 * B * heads * S * (S + kept rows,
+   rounded up to 128) bytes of scores. */
+int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *actx, const float *q,
+                          const float *k, const float *v, const float *gate, int B, int S, int D,
+                          const float *context_k, const float *context_v, float *mix);
+
 /* ---- the int8 linear stack of one Euler step --------------------------- */
 
 /* The int8 projections of `blocks` DiT blocks (dit.h:51-58 IroDiTInt8,

@@ -1,0 +1,370 @@
+// iro_attn.hip -- the fp32 attention core of a DiT block on gfx950, as the
+// reference's scalar build computes it (dit.c:808-870 with ops.c:577-600,
+// 681-703, 754-766, 786-789).
+//
+// Every sum runs in the scalar build's order, so the result is bit-identical
+// to it: a score is a 64-term dot product in index order, times 1/sqrtf(64);
+// a softmax row takes its maximum by strict replacement from the first score,
+// p = expf(score - max) (glibc's expf), the sum of p in key order, and p / sum;
+// each output element is the sum over keys, in key order, of p * v; the mix
+// is then scaled by 1 / (1 + expf(-gate)).  The joined keys of batch b are its
+// S latent tokens, then the context rows its mask keeps, in order.
+//
+// Three kernels per call:
+//   attn_scores   64 queries x 128 keys per block, 32 dot-product chains per
+//                 thread from LDS tiles; scores to a workspace [B*H, S, Jp],
+//                 and the maximum of each row's 128-key tile
+//   attn_softmax  RW rows per wave: the row maximum from the tile maxima,
+//                 p = expf(score - max) written in place, the key-order sum
+//                 of p by one lane per row (through LDS)
+//   attn_pv       64 queries x 64 dims per block: p / sum staged per 32-key
+//                 chunk, 16 key-order chains per thread, the gate applied at
+//                 the store
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "iro_expf.h"
+#include "iro_hip.h"
+#include "iro_internal.h"
+
+struct IroHipAttnContext {
+    IroHipContext *ctx = nullptr;
+    int B = 0, C = 0, context_batch = 0;
+    int max_valid = 0;           // largest number of kept context rows of any batch
+    int *rows = nullptr;         // [B][C]: source row of joined key S + i (device)
+    int *nvalid = nullptr;       // [B]: kept context rows (device)
+    std::vector<int> nvalid_h;   // the same, on the host
+};
+
+namespace iro {
+namespace {
+
+constexpr int kQT = 64;     // queries per score / PV block
+constexpr int kKT = 128;    // keys per score block
+constexpr int kPitch = 68;  // LDS row pitch (floats) of 64-wide tiles
+constexpr int kPVK = 32;    // keys per PV chunk
+
+// The source of joined key j of batch b, head column h*64.
+__device__ __forceinline__ const float *key_row(const float *self, const float *ctxr,
+                                                const int *rows, int b, int S, int C, int D,
+                                                int j) {
+    return j < S ? self + ((size_t)b * S + j) * D : ctxr + (size_t)rows[b * C + (j - S)] * D;
+}
+
+__global__ __launch_bounds__(256) void attn_scores_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ ck,
+    const int *__restrict__ rows, const int *__restrict__ nvalid, int S, int D, int H, int C,
+    int Jp, float *__restrict__ sc, float *__restrict__ pmax) {
+    __shared__ __attribute__((aligned(16))) float Qs[kQT * kPitch];
+    __shared__ __attribute__((aligned(16))) float Ks[kKT * kPitch];
+    const int bh = blockIdx.z, b = bh / H, h = bh - b * H;
+    const int J = S + nvalid[b];
+    const int k0 = blockIdx.x * kKT;
+    if (k0 >= J) return;
+    const int q0 = blockIdx.y * kQT;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
+        const int s = q0 + r < S ? q0 + r : S - 1;
+        *reinterpret_cast<float4 *>(&Qs[r * kPitch + c4]) =
+            *reinterpret_cast<const float4 *>(q + ((size_t)b * S + s) * D + h * 64 + c4);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
+        const int j = k0 + r < J ? k0 + r : J - 1;
+        *reinterpret_cast<float4 *>(&Ks[r * kPitch + c4]) = *reinterpret_cast<const float4 *>(
+            key_row(k, ck, rows, b, S, C, D, j) + h * 64 + c4);
+    }
+    __syncthreads();
+    // Thread: queries 4 tq .. 4 tq + 3, keys tk + 16 jj (jj < 8).
+    const int tq = tid >> 4, tk = tid & 15;
+    float acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) acc[i][jj] = 0.0f;
+#pragma unroll 2
+    for (int d4 = 0; d4 < 16; ++d4) {
+        float4 qv[4], kv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            qv[i] = *reinterpret_cast<const float4 *>(&Qs[(tq * 4 + i) * kPitch + d4 * 4]);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+            kv[jj] = *reinterpret_cast<const float4 *>(&Ks[(tk + 16 * jj) * kPitch + d4 * 4]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                acc[i][jj] = acc[i][jj] + qv[i].x * kv[jj].x;
+                acc[i][jj] = acc[i][jj] + qv[i].y * kv[jj].y;
+                acc[i][jj] = acc[i][jj] + qv[i].z * kv[jj].z;
+                acc[i][jj] = acc[i][jj] + qv[i].w * kv[jj].w;
+            }
+    }
+    const int NKT = Jp / kKT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int s = q0 + tq * 4 + i;
+        float m = -__builtin_inff();
+        float *dst = sc + ((size_t)bh * S + (s < S ? s : S - 1)) * Jp;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            const int j = k0 + tk + 16 * jj;
+            const float v = acc[i][jj] * 0.125f;  // 1 / sqrtf(64)
+            if (j < J) {
+                m = __builtin_fmaxf(m, v);
+                if (s < S) dst[j] = v;
+            }
+        }
+        // Tile maximum over the 16 lanes of this query row (fmaxf ignores NaN;
+        // the softmax kernel restores the first score's NaN rule).
+        m = __builtin_fmaxf(m, __shfl_xor(m, 1));
+        m = __builtin_fmaxf(m, __shfl_xor(m, 2));
+        m = __builtin_fmaxf(m, __shfl_xor(m, 4));
+        m = __builtin_fmaxf(m, __shfl_xor(m, 8));
+        if (tk == 0 && s < S) pmax[((size_t)bh * S + s) * NKT + blockIdx.x] = m;
+    }
+}
+
+// RW rows per wave, rows g = (b*H + h) * S + s.
+template <int RW>
+__global__ __launch_bounds__(64) void attn_softmax_kernel(float *__restrict__ sc,
+                                                          const float *__restrict__ pmax,
+                                                          const int *__restrict__ nvalid, int R,
+                                                          int S, int H, int Jp,
+                                                          float *__restrict__ sums) {
+    __shared__ uint64_t exptab[32];
+    __shared__ float tile[RW * 65];
+    __shared__ float mx_s[RW];
+    __shared__ int J_s[RW];
+    const int lane = threadIdx.x;
+    if (lane < 32) exptab[lane] = kExp2Tab[lane];
+    const int g0 = blockIdx.x * RW;
+    const int NKT = Jp / kKT;
+    int Jl = 0;
+    if (lane < RW) {
+        const int g = g0 + lane < R ? g0 + lane : R - 1;
+        Jl = S + nvalid[(g / S) / H];
+        // The scalar loop's maximum: the first score if it is NaN, else the
+        // largest score (the tile maxima skip NaN; a zero's sign does not
+        // change x - max for any x).
+        float m = -__builtin_inff();
+        for (int t = 0; t < (Jl + kKT - 1) / kKT; ++t) m = __builtin_fmaxf(m, pmax[(size_t)g * NKT + t]);
+        const float x0 = sc[(size_t)g * Jp];
+        mx_s[lane] = x0 != x0 ? x0 : m;
+        J_s[lane] = g0 + lane < R ? Jl : 0;
+    }
+    __syncthreads();
+    int Jw = 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) Jw = J_s[r] > Jw ? J_s[r] : Jw;
+    float sum = 0.0f;
+    for (int c0 = 0; c0 < Jw; c0 += 64) {
+        const int col = c0 + lane;
+        float x[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+            x[r] = col < J_s[r] ? sc[(size_t)(g0 + r) * Jp + col] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            if (col < J_s[r]) {
+                const float p = expf_glibc(x[r] - mx_s[r], exptab);
+                sc[(size_t)(g0 + r) * Jp + col] = p;
+                tile[r * 65 + lane] = p;
+            }
+        }
+        __syncthreads();
+        if (lane < RW) {
+            const int n = Jl - c0 < 64 ? Jl - c0 : 64;
+            const float *tr = &tile[lane * 65];
+            for (int i = 0; i < n; ++i) sum = sum + tr[i];
+        }
+        __syncthreads();
+    }
+    if (lane < RW && g0 + lane < R) sums[g0 + lane] = sum;
+}
+
+__global__ __launch_bounds__(256) void attn_pv_kernel(
+    const float *__restrict__ sc, const float *__restrict__ sums, const float *__restrict__ v,
+    const float *__restrict__ cv, const int *__restrict__ rows, const int *__restrict__ nvalid,
+    const float *__restrict__ gate, int S, int D, int H, int C, int Jp,
+    float *__restrict__ mix) {
+    __shared__ uint64_t exptab[32];
+    __shared__ __attribute__((aligned(16))) float Ps[kPVK * kPitch];  // [key][query]
+    __shared__ __attribute__((aligned(16))) float Vs[kPVK * kPitch];  // [key][dim]
+    __shared__ float sum_s[kQT];
+    const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+    const int J = S + nvalid[b];
+    const int q0 = blockIdx.x * kQT;
+    const int tid = threadIdx.x;
+    if (tid < 32) exptab[tid] = kExp2Tab[tid];
+    if (tid < kQT) {
+        const int s = q0 + tid < S ? q0 + tid : S - 1;
+        sum_s[tid] = sums[(size_t)bh * S + s];
+    }
+    // Staging: P element (query (tid >> 5) + 8 i, key tid & 31); V float4s
+    // tid and tid + 256 of the chunk's 32 x 64 tile.
+    const int kj = tid & 31, qi0 = tid >> 5;
+    float pr[8];
+    float4 vr[2];
+    auto load = [&](int kc) {
+        const int j = kc + kj < J ? kc + kj : J - 1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int s = q0 + qi0 + 8 * i < S ? q0 + qi0 + 8 * i : S - 1;
+            pr[i] = sc[((size_t)bh * S + s) * Jp + j];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
+            const int jv = kc + r < J ? kc + r : J - 1;
+            vr[i] = *reinterpret_cast<const float4 *>(key_row(v, cv, rows, b, S, C, D, jv) +
+                                                      h * 64 + c4);
+        }
+    };
+    const int tq = tid >> 4, tn = tid & 15;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][e] = 0.0f;
+    load(0);
+    __syncthreads();  // sum_s
+    for (int kc = 0; kc < J; kc += kPVK) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) Ps[kj * kPitch + qi0 + 8 * i] = pr[i] / sum_s[qi0 + 8 * i];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
+            *reinterpret_cast<float4 *>(&Vs[r * kPitch + c4]) = vr[i];
+        }
+        __syncthreads();
+        if (kc + kPVK < J) load(kc + kPVK);
+        const int nk = J - kc < kPVK ? J - kc : kPVK;
+        for (int kk = 0; kk < nk; ++kk) {
+            const float4 pv = *reinterpret_cast<const float4 *>(&Ps[kk * kPitch + tq * 4]);
+            const float4 vv = *reinterpret_cast<const float4 *>(&Vs[kk * kPitch + tn * 4]);
+            const float p4[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[i][0] = acc[i][0] + p4[i] * vv.x;
+                acc[i][1] = acc[i][1] + p4[i] * vv.y;
+                acc[i][2] = acc[i][2] + p4[i] * vv.z;
+                acc[i][3] = acc[i][3] + p4[i] * vv.w;
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int s = q0 + tq * 4 + i;
+        if (s >= S) continue;
+        const size_t off = ((size_t)b * S + s) * D + h * 64 + tn * 4;
+        const float4 g = *reinterpret_cast<const float4 *>(gate + off);
+        const float g4[4] = {g.x, g.y, g.z, g.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float r = 1.0f / (1.0f + expf_glibc(-g4[e], exptab));
+            o[e] = acc[i][e] * r;
+        }
+        *reinterpret_cast<float4 *>(mix + off) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+}  // namespace
+}  // namespace iro
+
+using namespace iro;
+
+extern "C" {
+
+int iro_hip_dit_attn_context_create(IroHipContext *ctx, const uint8_t *mask, int B, int C,
+                                    int context_batch, IroHipAttnContext **out) {
+    if (!ctx || !out || !mask || B <= 0 || C <= 0 || (context_batch != 1 && context_batch != B))
+        return set_error(ctx, "dit_attn_context: invalid arguments");
+    *out = nullptr;
+    IroHipAttnContext *a = new (std::nothrow) IroHipAttnContext();
+    if (!a) return set_error(ctx, "dit_attn_context: out of host memory");
+    a->ctx = ctx;
+    a->B = B;
+    a->C = C;
+    a->context_batch = context_batch;
+    std::vector<int> rows((size_t)B * C, 0);
+    a->nvalid_h.assign(B, 0);
+    for (int b = 0; b < B; ++b) {
+        const int crow = context_batch == 1 ? 0 : b * C;
+        int n = 0;
+        for (int ci = 0; ci < C; ++ci)
+            if (mask[(size_t)b * C + ci]) rows[(size_t)b * C + n++] = crow + ci;
+        a->nvalid_h[b] = n;
+        a->max_valid = n > a->max_valid ? n : a->max_valid;
+    }
+    if (hipMalloc(&a->rows, rows.size() * sizeof(int)) != hipSuccess ||
+        hipMalloc(&a->nvalid, (size_t)B * sizeof(int)) != hipSuccess ||
+        hipMemcpyAsync(a->rows, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice,
+                       ctx->stream) != hipSuccess ||
+        hipMemcpyAsync(a->nvalid, a->nvalid_h.data(), (size_t)B * sizeof(int),
+                       hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        iro_hip_dit_attn_context_destroy(a);
+        return set_error(ctx, "dit_attn_context: device allocation or upload failed");
+    }
+    *out = a;
+    return 0;
+}
+
+void iro_hip_dit_attn_context_destroy(IroHipAttnContext *a) {
+    if (!a) return;
+    if (a->ctx && a->ctx->stream) (void)hipStreamSynchronize(a->ctx->stream);
+    if (a->rows) (void)hipFree(a->rows);
+    if (a->nvalid) (void)hipFree(a->nvalid);
+    delete a;
+}
+
+int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *a, const float *q,
+                          const float *k, const float *v, const float *gate, int B, int S, int D,
+                          const float *context_k, const float *context_v, float *mix) {
+    if (!ctx || !a || a->ctx != ctx || B != a->B || S <= 0 || D <= 0 || D % 64 || !q || !k ||
+        !v || !gate || !mix || !context_k || !context_v)
+        return set_error(ctx, "dit_attention: invalid arguments (D a multiple of 64, the "
+                              "attention context made for this B on this context)");
+    if (((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)v) | ((uintptr_t)gate) |
+          ((uintptr_t)mix) | ((uintptr_t)context_k) | ((uintptr_t)context_v)) & 15) != 0)
+        return set_error(ctx, "dit_attention: every tensor must be 16-byte aligned");
+    const int H = D / 64;
+    const long long Jmax = (long long)S + a->max_valid;
+    const long long Jp = (Jmax + kKT - 1) / kKT * kKT;
+    const long long R = (long long)B * H * S;
+    if (R > INT32_MAX / 2 || Jp > INT32_MAX / 2 || (long long)S > 65535LL * kQT ||
+        (long long)B * H > 65535)
+        return set_error(ctx, "dit_attention: shape too large");
+    Workspace ws{ctx};
+    const size_t o_sc = ws.reserve((size_t)R * Jp * sizeof(float));
+    const size_t o_pm = ws.reserve((size_t)R * (Jp / kKT) * sizeof(float));
+    const size_t o_sum = ws.reserve((size_t)R * sizeof(float));
+    if (ws.commit()) return -1;
+    float *sc = ws.at<float>(o_sc), *pm = ws.at<float>(o_pm), *sums = ws.at<float>(o_sum);
+    const int C = a->C;
+    hipLaunchKernelGGL(attn_scores_kernel, dim3((unsigned)(Jp / kKT), (S + kQT - 1) / kQT, B * H),
+                       dim3(256), 0, ctx->stream, q, k, context_k, a->rows, a->nvalid, S, D, H, C,
+                       (int)Jp, sc, pm);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    constexpr int RW = 16;
+    hipLaunchKernelGGL((attn_softmax_kernel<RW>), dim3((unsigned)((R + RW - 1) / RW)), dim3(64), 0,
+                       ctx->stream, sc, pm, a->nvalid, (int)R, S, H, (int)Jp, sums);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    hipLaunchKernelGGL(attn_pv_kernel, dim3((S + kQT - 1) / kQT, B * H), dim3(256), 0, ctx->stream,
+                       sc, sums, v, context_v, a->rows, a->nvalid, gate, S, D, H, C, (int)Jp, mix);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+}  // extern "C"

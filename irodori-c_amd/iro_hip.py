@@ -108,6 +108,9 @@ def load() -> C.CDLL:
         "iro_hip_dit_adaln_apply": ([_vp, _vp, _i, _i, _i, _vp, _vp, C.c_float, _vp], _i),
         "iro_hip_dit_qk_norm_rope": ([_vp, _vp, _vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
         "iro_hip_dit_head_rmsnorm": ([_vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
+        "iro_hip_dit_attn_context_create": ([_vp, _vp, _i, _i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_dit_attn_context_destroy": ([_vp], None),
+        "iro_hip_dit_attention": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp], _i),
         "iro_hip_selfcheck_fp32": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_profile_enable": ([_vp, _i], _i),
         "iro_hip_profile_reset": ([_vp], _i),
@@ -182,6 +185,19 @@ class DeviceArray:
         if self.ptr:
             self.ctx.lib.iro_hip_free(self.ctx.h, self.vp)
             self.ptr = None
+
+
+class AttnContext:
+    """A device joined-key layout (iro_hip_dit_attn_context_create); destroy it
+    before its Context is closed."""
+
+    def __init__(self, ctx: "Context", h, B: int, C_: int):
+        self.ctx, self.h, self.B, self.C = ctx, h, B, C_
+
+    def destroy(self):
+        if self.h:
+            self.ctx.lib.iro_hip_dit_attn_context_destroy(self.h)
+            self.h = None
 
 
 ST_DTYPES = ["F32", "F16", "BF16", "I64", "I32", "I16", "I8", "U8", "BOOL"]
@@ -395,6 +411,24 @@ class Context:
         """dit.c:619-636 in place on x [B*S, D]."""
         self._check(self.lib.iro_hip_dit_head_rmsnorm(self.h, x.vp, weight.vp, B, S, D, eps),
                     "dit_head_rmsnorm")
+
+    def attn_context(self, mask, context_batch: int) -> "AttnContext":
+        """The joined-key layout of mask [B, C] (host uint8) for dit_attention."""
+        mask = np.ascontiguousarray(mask, np.uint8)
+        B, Cn = mask.shape
+        h = C.c_void_p()
+        self._check(self.lib.iro_hip_dit_attn_context_create(self.h, _ptr(mask), B, Cn,
+                                                             context_batch, C.byref(h)),
+                    "dit_attn_context")
+        return AttnContext(self, h.value, B, Cn)
+
+    def dit_attention(self, actx: "AttnContext", q: DeviceArray, k: DeviceArray,
+                      v: DeviceArray, gate: DeviceArray, B: int, S: int, D: int,
+                      context_k: DeviceArray, context_v: DeviceArray, mix: DeviceArray):
+        """dit.c:808-870: mix [B*S, D] from q, k, v, gate and the context rows."""
+        self._check(self.lib.iro_hip_dit_attention(self.h, actx.h, q.vp, k.vp, v.vp, gate.vp, B,
+                                                   S, D, context_k.vp, context_v.vp, mix.vp),
+                    "dit_attention")
 
     def weight_from_st(self, st: Safetensors, name: str, transposed: bool = False) -> Weight:
         h = C.c_void_p()

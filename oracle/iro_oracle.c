@@ -514,67 +514,73 @@ int orc_attention_core(const float *q, const float *k, const float *v, const flo
                        int context_batch, float *mix) {
     const int heads = D / 64;
     const float scale = 1.0f / sqrtf(64.0f);
-    const float **kr = malloc(sizeof(float *) * (size_t)(S + C));
-    const float **vr = malloc(sizeof(float *) * (size_t)(S + C));
-    float *sc = malloc(sizeof(float) * (size_t)(S + C));
-    if (!kr || !vr || !sc) {
-        free(kr);
-        free(vr);
-        free(sc);
-        return -1;
-    }
-    for (int b = 0; b < B; b++) {
-        for (int h = 0; h < heads; h++) {
-            int J = 0;
-            for (int t = 0; t < S; t++) {
-                kr[J] = k + ((size_t)b * S + t) * D + h * 64;
-                vr[J++] = v + ((size_t)b * S + t) * D + h * 64;
-            }
-            const size_t crow = context_batch == 1 ? 0 : (size_t)b * C;
-            for (int ci = 0; ci < C; ci++) {
-                if (!mask[(size_t)b * C + ci]) continue;
-                kr[J] = ck + (crow + ci) * D + h * 64;
-                vr[J++] = cv + (crow + ci) * D + h * 64;
-            }
-            for (int s = 0; s < S; s++) {
-                const float *qs = q + ((size_t)b * S + s) * D + h * 64;
-                for (int j = 0; j < J; j++) {
-                    float acc = 0.0f;
-                    for (int d = 0; d < 64; d++) {
-                        const float pr = qs[d] * kr[j][d];
-                        acc = acc + pr;
-                    }
-                    sc[j] = acc * scale;
+    int fail = 0;
+    /* (b, h) pairs are independent; each thread keeps its own key lists. */
+#pragma omp parallel
+    {
+        const float **kr = malloc(sizeof(float *) * (size_t)(S + C));
+        const float **vr = malloc(sizeof(float *) * (size_t)(S + C));
+        float *sc = malloc(sizeof(float) * (size_t)(S + C));
+        if (!kr || !vr || !sc) {
+#pragma omp atomic write
+            fail = 1;
+        }
+#pragma omp for collapse(2) schedule(dynamic)
+        for (int b = 0; b < B; b++) {
+            for (int h = 0; h < heads; h++) {
+                if (!kr || !vr || !sc) continue;
+                int J = 0;
+                for (int t = 0; t < S; t++) {
+                    kr[J] = k + ((size_t)b * S + t) * D + h * 64;
+                    vr[J++] = v + ((size_t)b * S + t) * D + h * 64;
                 }
-                float mx = sc[0];
-                for (int j = 1; j < J; j++)
-                    if (sc[j] > mx) mx = sc[j];
-                float sum = 0.0f;
-                for (int j = 0; j < J; j++) {
-                    sc[j] = expf(sc[j] - mx);
-                    sum = sum + sc[j];
+                const size_t crow = context_batch == 1 ? 0 : (size_t)b * C;
+                for (int ci = 0; ci < C; ci++) {
+                    if (!mask[(size_t)b * C + ci]) continue;
+                    kr[J] = ck + (crow + ci) * D + h * 64;
+                    vr[J++] = cv + (crow + ci) * D + h * 64;
                 }
-                for (int j = 0; j < J; j++) sc[j] = sc[j] / sum;
-                float *out = mix + ((size_t)b * S + s) * D + h * 64;
-                for (int n = 0; n < 64; n++) {
-                    float acc = 0.0f;
+                for (int s = 0; s < S; s++) {
+                    const float *qs = q + ((size_t)b * S + s) * D + h * 64;
                     for (int j = 0; j < J; j++) {
-                        const float pr = sc[j] * vr[j][n];
-                        acc = acc + pr;
+                        float acc = 0.0f;
+                        for (int d = 0; d < 64; d++) {
+                            const float pr = qs[d] * kr[j][d];
+                            acc = acc + pr;
+                        }
+                        sc[j] = acc * scale;
                     }
-                    out[n] = acc;
+                    float mx = sc[0];
+                    for (int j = 1; j < J; j++)
+                        if (sc[j] > mx) mx = sc[j];
+                    float sum = 0.0f;
+                    for (int j = 0; j < J; j++) {
+                        sc[j] = expf(sc[j] - mx);
+                        sum = sum + sc[j];
+                    }
+                    for (int j = 0; j < J; j++) sc[j] = sc[j] / sum;
+                    float *out = mix + ((size_t)b * S + s) * D + h * 64;
+                    for (int n = 0; n < 64; n++) {
+                        float acc = 0.0f;
+                        for (int j = 0; j < J; j++) {
+                            const float pr = sc[j] * vr[j][n];
+                            acc = acc + pr;
+                        }
+                        out[n] = acc;
+                    }
                 }
             }
         }
+        free(kr);
+        free(vr);
+        free(sc);
     }
+    if (fail) return -1;
     const size_t n = (size_t)B * S * D;
     for (size_t i = 0; i < n; i++) {
         const float r = 1.0f / (1.0f + expf(-gate[i]));
         mix[i] = mix[i] * r;
     }
-    free(kr);
-    free(vr);
-    free(sc);
     return 0;
 }
 

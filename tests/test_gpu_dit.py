@@ -209,3 +209,69 @@ def test_qk_norm_rope_rejects_bad_shapes(ctx):
     q = ctx.empty((4, 100), np.float32)
     with pytest.raises(iro_hip.HipError):
         ctx.dit_qk_norm_rope(q, q, q, q, 1, 4, 100, 1e-6)
+
+
+def _attn_case(seed, B, S, C, D, shared, keep):
+    """q, k, v, gate [B*S, D], context rows and a mask keeping `keep` rows of
+    batch 0 (other batches keep every other row, the last keeps none)."""
+    q, k, v, gate = (gauss(seed + i, (B * S, D)) for i in range(4))
+    rows = 1 if shared else B
+    ck, cv = gauss(seed + 4, (rows * C, D)), gauss(seed + 5, (rows * C, D))
+    mask = np.zeros((B, C), np.uint8)
+    mask[0, :keep] = 1
+    for b in range(1, B - 1):
+        mask[b, ::2] = 1
+    return q, k, v, gate, ck, cv, mask
+
+
+@pytest.mark.parametrize("B,S,C,D,shared,keep", [
+    (2, 24, 9, 1280, 0, 4),       # reference-sized heads, per-batch context
+    (3, 150, 40, 1024, 1, 40),    # shared context, ragged key tiles
+    (3, 200, 130, 1024, 0, 130),  # more than one 128-key tile of context
+    (1, 1, 1, 64, 0, 1),          # one query, one head, one context row
+    (2, 70, 3, 128, 1, 0),        # no kept context rows in any batch
+])
+def test_attention_core(ctx, oracle, B, S, C, D, shared, keep):
+    """dit.c:808-870 on the device: bit-identical to the oracle's attention
+    core (pinned bit for bit against the scalar reference build's
+    iro_dit_attention in tests/test_oracle_pins.py); large and tiny scores so
+    that softmax terms and gates underflow."""
+    q, k, v, gate, ck, cv, mask = _attn_case(680, B, S, C, D, shared, keep)
+    q[0] *= 20.0
+    gate[1 % (B * S)] *= 60.0
+    actx = ctx.attn_context(mask, 1 if shared else B)
+    try:
+        mix = ctx.empty((B * S, D), np.float32)
+        dev = [ctx.to_device(a) for a in (q, k, v, gate, ck, cv)]
+        ctx.dit_attention(actx, dev[0], dev[1], dev[2], dev[3], B, S, D, dev[4], dev[5], mix)
+        want = oracle.attention_core(q, k, v, gate, B, S, ck, cv, mask, 1 if shared else B)
+        assert_bits_equal(mix.numpy(), want, "mix")
+    finally:
+        actx.destroy()
+
+
+def test_attention_core_full_shape(ctx, oracle):
+    """The stack's shape (3 x 750 tokens, 16 heads) with up to 250 kept
+    context rows: the whole output bit for bit against the oracle."""
+    B, S, C, D = 3, 750, 300, 1024
+    q, k, v, gate, ck, cv, mask = _attn_case(690, B, S, C, D, False, 250)
+    actx = ctx.attn_context(mask, B)
+    try:
+        mix = ctx.empty((B * S, D), np.float32)
+        dev = [ctx.to_device(a) for a in (q, k, v, gate, ck, cv)]
+        ctx.dit_attention(actx, dev[0], dev[1], dev[2], dev[3], B, S, D, dev[4], dev[5], mix)
+        want = oracle.attention_core(q, k, v, gate, B, S, ck, cv, mask, B)
+        assert_bits_equal(mix.numpy(), want, "mix")
+    finally:
+        actx.destroy()
+
+
+def test_attention_rejects_mismatched_context(ctx):
+    mask = np.ones((2, 3), np.uint8)
+    actx = ctx.attn_context(mask, 2)
+    try:
+        x = ctx.empty((3 * 4, 64), np.float32)
+        with pytest.raises(iro_hip.HipError):
+            ctx.dit_attention(actx, x, x, x, x, 3, 4, 64, x, x, x)
+    finally:
+        actx.destroy()
