@@ -17,7 +17,7 @@
 //   attn_softmax  RW rows per wave: the row maximum from the tile maxima,
 //                 p = expf(score - max) written in place, the key-order sum
 //                 of p by one lane per row (through LDS)
-//   attn_pv       64 queries x 64 dims per block: p / sum staged per 32-key
+//   attn_pv       64 queries x 64 dims per block: p / sum staged per 64-key
 //                 chunk, 16 key-order chains per thread, the gate applied at
 //                 the store
 #include <hip/hip_runtime.h>
@@ -43,10 +43,10 @@ struct IroHipAttnContext {
 namespace iro {
 namespace {
 
-constexpr int kQT = 64;     // queries per score / PV block
+constexpr int kQT = 64;     // queries per score block
 constexpr int kKT = 128;    // keys per score block
 constexpr int kPitch = 68;  // LDS row pitch (floats) of 64-wide tiles
-constexpr int kPVK = 32;    // keys per PV chunk
+constexpr int kPVK = 64;    // keys per PV chunk
 
 // The source of joined key j of batch b, head column h*64.
 __device__ __forceinline__ const float *key_row(const float *self, const float *ctxr,
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) acc[i][jj] = 0.0f;
-#pragma unroll 2
+#pragma unroll 4
     for (int d4 = 0; d4 < 16; ++d4) {
         float4 qv[4], kv[8];
 #pragma unroll
@@ -156,7 +156,8 @@ __global__ __launch_bounds__(64) void attn_softmax_kernel(float *__restrict__ sc
         // largest score (the tile maxima skip NaN; a zero's sign does not
         // change x - max for any x).
         float m = -__builtin_inff();
-        for (int t = 0; t < (Jl + kKT - 1) / kKT; ++t) m = __builtin_fmaxf(m, pmax[(size_t)g * NKT + t]);
+        for (int t = 0; t < (Jl + kKT - 1) / kKT; ++t)
+            m = __builtin_fmaxf(m, pmax[(size_t)g * NKT + t]);
         const float x0 = sc[(size_t)g * Jp];
         mx_s[lane] = x0 != x0 ? x0 : m;
         J_s[lane] = g0 + lane < R ? Jl : 0;
@@ -166,12 +167,20 @@ __global__ __launch_bounds__(64) void attn_softmax_kernel(float *__restrict__ sc
 #pragma unroll
     for (int r = 0; r < RW; ++r) Jw = J_s[r] > Jw ? J_s[r] : Jw;
     float sum = 0.0f;
+    // Chunk c0's scores are loaded while chunk c0 - 64 is computed.
+    float xn[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) xn[r] = lane < J_s[r] ? sc[(size_t)(g0 + r) * Jp + lane] : 0.0f;
     for (int c0 = 0; c0 < Jw; c0 += 64) {
         const int col = c0 + lane;
         float x[RW];
 #pragma unroll
-        for (int r = 0; r < RW; ++r)
-            x[r] = col < J_s[r] ? sc[(size_t)(g0 + r) * Jp + col] : 0.0f;
+        for (int r = 0; r < RW; ++r) x[r] = xn[r];
+        if (c0 + 64 < Jw) {
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+                xn[r] = col + 64 < J_s[r] ? sc[(size_t)(g0 + r) * Jp + col + 64] : 0.0f;
+        }
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
             if (col < J_s[r]) {
@@ -191,38 +200,41 @@ __global__ __launch_bounds__(64) void attn_softmax_kernel(float *__restrict__ sc
     if (lane < RW && g0 + lane < R) sums[g0 + lane] = sum;
 }
 
+// QT queries x 64 dims per block; thread: QT/16 queries x 4 dims.
+template <int QT>
 __global__ __launch_bounds__(256) void attn_pv_kernel(
     const float *__restrict__ sc, const float *__restrict__ sums, const float *__restrict__ v,
     const float *__restrict__ cv, const int *__restrict__ rows, const int *__restrict__ nvalid,
     const float *__restrict__ gate, int S, int D, int H, int C, int Jp,
     float *__restrict__ mix) {
+    constexpr int QPT = QT / 16, PP = QT + 4, NP = QT / 4;
     __shared__ uint64_t exptab[32];
-    __shared__ __attribute__((aligned(16))) float Ps[kPVK * kPitch];  // [key][query]
+    __shared__ __attribute__((aligned(16))) float Ps[kPVK * PP];      // [key][query]
     __shared__ __attribute__((aligned(16))) float Vs[kPVK * kPitch];  // [key][dim]
-    __shared__ float sum_s[kQT];
+    __shared__ float sum_s[QT];
     const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
     const int J = S + nvalid[b];
-    const int q0 = blockIdx.x * kQT;
+    const int q0 = blockIdx.x * QT;
     const int tid = threadIdx.x;
     if (tid < 32) exptab[tid] = kExp2Tab[tid];
-    if (tid < kQT) {
+    if (tid < QT) {
         const int s = q0 + tid < S ? q0 + tid : S - 1;
         sum_s[tid] = sums[(size_t)bh * S + s];
     }
-    // Staging: P element (query (tid >> 5) + 8 i, key tid & 31); V float4s
-    // tid and tid + 256 of the chunk's 32 x 64 tile.
-    const int kj = tid & 31, qi0 = tid >> 5;
-    float pr[8];
-    float4 vr[2];
+    // Staging: P element (query (tid >> 6) + 4 i, key tid & 63); V float4s
+    // tid + 256 i of the chunk's 64 x 64 tile.
+    const int kj = tid & 63, qi0 = tid >> 6;
+    float pr[NP];
+    float4 vr[4];
     auto load = [&](int kc) {
         const int j = kc + kj < J ? kc + kj : J - 1;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int s = q0 + qi0 + 8 * i < S ? q0 + qi0 + 8 * i : S - 1;
+        for (int i = 0; i < NP; ++i) {
+            const int s = q0 + qi0 + 4 * i < S ? q0 + qi0 + 4 * i : S - 1;
             pr[i] = sc[((size_t)bh * S + s) * Jp + j];
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 4; ++i) {
             const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
             const int jv = kc + r < J ? kc + r : J - 1;
             vr[i] = *reinterpret_cast<const float4 *>(key_row(v, cv, rows, b, S, C, D, jv) +
@@ -230,41 +242,55 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
         }
     };
     const int tq = tid >> 4, tn = tid & 15;
-    float acc[4][4];
+    float acc[QPT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < QPT; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[i][e] = 0.0f;
     load(0);
     __syncthreads();  // sum_s
     for (int kc = 0; kc < J; kc += kPVK) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) Ps[kj * kPitch + qi0 + 8 * i] = pr[i] / sum_s[qi0 + 8 * i];
+        for (int i = 0; i < NP; ++i) Ps[kj * PP + qi0 + 4 * i] = pr[i] / sum_s[qi0 + 4 * i];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 4; ++i) {
             const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
             *reinterpret_cast<float4 *>(&Vs[r * kPitch + c4]) = vr[i];
         }
         __syncthreads();
         if (kc + kPVK < J) load(kc + kPVK);
-        const int nk = J - kc < kPVK ? J - kc : kPVK;
-        for (int kk = 0; kk < nk; ++kk) {
-            const float4 pv = *reinterpret_cast<const float4 *>(&Ps[kk * kPitch + tq * 4]);
-            const float4 vv = *reinterpret_cast<const float4 *>(&Vs[kk * kPitch + tn * 4]);
-            const float p4[4] = {pv.x, pv.y, pv.z, pv.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[i][0] = acc[i][0] + p4[i] * vv.x;
-                acc[i][1] = acc[i][1] + p4[i] * vv.y;
-                acc[i][2] = acc[i][2] + p4[i] * vv.z;
-                acc[i][3] = acc[i][3] + p4[i] * vv.w;
+        auto step = [&](int kk) {
+            float p[QPT];
+            if constexpr (QPT == 4) {
+                const float4 pv = *reinterpret_cast<const float4 *>(&Ps[kk * PP + tq * 4]);
+                p[0] = pv.x, p[1] = pv.y, p[2] = pv.z, p[3] = pv.w;
+            } else {
+                const float2 pv = *reinterpret_cast<const float2 *>(&Ps[kk * PP + tq * 2]);
+                p[0] = pv.x, p[1] = pv.y;
             }
+            const float4 vv = *reinterpret_cast<const float4 *>(&Vs[kk * kPitch + tn * 4]);
+#pragma unroll
+            for (int i = 0; i < QPT; ++i) {
+                acc[i][0] = acc[i][0] + p[i] * vv.x;
+                acc[i][1] = acc[i][1] + p[i] * vv.y;
+                acc[i][2] = acc[i][2] + p[i] * vv.z;
+                acc[i][3] = acc[i][3] + p[i] * vv.w;
+            }
+        };
+        const int nk = J - kc < kPVK ? J - kc : kPVK;
+        if (nk == kPVK) {
+            // Full chunk: unrolled, so the LDS reads of later keys go out
+            // ahead of the additions of earlier ones.
+#pragma unroll 16
+            for (int kk = 0; kk < kPVK; ++kk) step(kk);
+        } else {
+            for (int kk = 0; kk < nk; ++kk) step(kk);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int s = q0 + tq * 4 + i;
+    for (int i = 0; i < QPT; ++i) {
+        const int s = q0 + tq * QPT + i;
         if (s >= S) continue;
         const size_t off = ((size_t)b * S + s) * D + h * 64 + tn * 4;
         const float4 g = *reinterpret_cast<const float4 *>(gate + off);
@@ -343,7 +369,7 @@ int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *a, const 
     const long long Jmax = (long long)S + a->max_valid;
     const long long Jp = (Jmax + kKT - 1) / kKT * kKT;
     const long long R = (long long)B * H * S;
-    if (R > INT32_MAX / 2 || Jp > INT32_MAX / 2 || (long long)S > 65535LL * kQT ||
+    if (R > INT32_MAX / 2 || Jp > INT32_MAX / 2 || (long long)S > 65535LL * 32 ||
         (long long)B * H > 65535)
         return set_error(ctx, "dit_attention: shape too large");
     Workspace ws{ctx};
@@ -357,12 +383,14 @@ int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *a, const 
                        dim3(256), 0, ctx->stream, q, k, context_k, a->rows, a->nvalid, S, D, H, C,
                        (int)Jp, sc, pm);
     IRO_HIP_CHECK_LAUNCH(ctx);
-    constexpr int RW = 16;
+    constexpr int RW = 8;  // rows per softmax wave (measured: 8 < 16 < 32 in time)
     hipLaunchKernelGGL((attn_softmax_kernel<RW>), dim3((unsigned)((R + RW - 1) / RW)), dim3(64), 0,
                        ctx->stream, sc, pm, a->nvalid, (int)R, S, H, (int)Jp, sums);
     IRO_HIP_CHECK_LAUNCH(ctx);
-    hipLaunchKernelGGL(attn_pv_kernel, dim3((S + kQT - 1) / kQT, B * H), dim3(256), 0, ctx->stream,
-                       sc, sums, v, context_v, a->rows, a->nvalid, gate, S, D, H, C, (int)Jp, mix);
+    constexpr int PQT = 32;  // 4.5 waves per SIMD at 3 x 750 queries, 16 heads
+    hipLaunchKernelGGL((attn_pv_kernel<PQT>), dim3((S + PQT - 1) / PQT, B * H), dim3(256), 0,
+                       ctx->stream, sc, sums, v, context_v, a->rows, a->nvalid, gate, S, D, H, C,
+                       (int)Jp, mix);
     IRO_HIP_CHECK_LAUNCH(ctx);
     return 0;
 }

@@ -511,12 +511,12 @@ int orc_head_norm_rope(float *q, const float *qw, float *k, const float *kw, int
    mix [B*S, D]; ck, cv [(context_batch == 1 ? 1 : B) * C, D]. */
 int orc_attention_core(const float *q, const float *k, const float *v, const float *gate, int B,
                        int S, int D, const float *ck, const float *cv, const uint8_t *mask, int C,
-                       int context_batch, float *mix) {
+                       int context_batch, float *mix, int threads) {
     const int heads = D / 64;
     const float scale = 1.0f / sqrtf(64.0f);
     int fail = 0;
     /* (b, h) pairs are independent; each thread keeps its own key lists. */
-#pragma omp parallel
+#pragma omp parallel num_threads(threads)
     {
         const float **kr = malloc(sizeof(float *) * (size_t)(S + C));
         const float **vr = malloc(sizeof(float *) * (size_t)(S + C));

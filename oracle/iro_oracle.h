@@ -98,7 +98,7 @@ int orc_head_norm_rope(float *q, const float *qw, float *k, const float *kw, int
                        int heads, float eps, int rope);
 int orc_attention_core(const float *q, const float *k, const float *v, const float *gate, int B,
                        int S, int D, const float *ck, const float *cv, const uint8_t *mask, int C,
-                       int context_batch, float *mix);
+                       int context_batch, float *mix, int threads);
 
 /* dit.c:1013-1020 / 1032-1039: x[b,s,:] += gate[b,:] * branch[b,s,:].
    Strict: two roundings.  Fast-math: one FMA (vfmadd132ps). */

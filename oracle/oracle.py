@@ -70,7 +70,7 @@ class Oracle:
                                          C.c_float, C.c_int]
         L.orc_head_norm_rope.restype = C.c_int
         L.orc_attention_core.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int,
-                                         _f32p, _f32p, _u8p, C.c_int, C.c_int, _f32p]
+                                         _f32p, _f32p, _u8p, C.c_int, C.c_int, _f32p, C.c_int]
         L.orc_attention_core.restype = C.c_int
         L.orc_conv1d_int8.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p,
                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int,
@@ -223,7 +223,8 @@ class Oracle:
         mix = np.empty_like(q)
         rc = self.lib.orc_attention_core(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p),
                                          _p(gate, _f32p), B, S, D, _p(ck, _f32p), _p(cv, _f32p),
-                                         _p(mask, _u8p), C, context_batch, _p(mix, _f32p))
+                                         _p(mask, _u8p), C, context_batch, _p(mix, _f32p),
+                                         self.threads)
         assert rc == 0
         return mix
 
