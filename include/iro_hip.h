@@ -298,6 +298,22 @@ void iro_hip_dit_stack_destroy(IroHipDiTStack *s);
    The profiler (iro_hip_profile_enable) always runs steps directly. */
 int iro_hip_dit_stack_use_graph(IroHipDiTStack *s, int on);
 
+/* One DiT block forward (dit.c:984-1040 dit_block) on the device, in place on
+   x [B*S, D], with this stack's int8 weights of `block`: adaLN apply, fused
+   QKVG, QK-norm + half-RoPE, the attention core with the context of actx,
+   Wo with x += gate * branch, adaLN apply, W1/W3 + SiLU gate, W2 with
+   x += gate * branch -- the reference's order and arithmetic at every step,
+   so x is bit-identical to iro_dit_block of the scalar build given the same
+   adaLN parameters.  ada_attn and ada_mlp are [3, B, D] device arrays:
+   shift, scale and the tanhf'd gate of dit_adaln (dit.c:580-588) for each
+   half; q_norm, k_norm [D].  Uses the stack's activation buffers; not
+   capturable (the attention workspace may grow). */
+int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int B, int S,
+                                    const float *ada_attn, const float *ada_mlp,
+                                    const float *q_norm, const float *k_norm, float eps,
+                                    const IroHipAttnContext *actx, const float *context_k,
+                                    const float *context_v);
+
 /* ---- DACVAE int8 Conv1d (dacvae.c:543-688, no snake) ------------------- */
 
 /* input [T, C] fp32 time-major, weight [N, kernel*C] (tap-major K as

@@ -596,6 +596,7 @@ struct IroHipDiTStack {
     int cap_rows = 0, cap_branches = 0;
     float *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *hidden = nullptr;
     float *mod = nullptr;
+    float *h = nullptr, *mix = nullptr;  // block forward: normed input, attention output
     // graph of the last step's launches
     int use_graph = 1;
     hipGraph_t graph = nullptr;
@@ -612,7 +613,7 @@ using namespace iro;
 namespace {
 
 void stack_free_acts(IroHipDiTStack *s) {
-    for (float **p : {&s->q, &s->k, &s->v, &s->g, &s->hidden, &s->mod}) {
+    for (float **p : {&s->q, &s->k, &s->v, &s->g, &s->hidden, &s->mod, &s->h, &s->mix}) {
         if (*p) (void)hipFree(*p);
         *p = nullptr;
     }
@@ -638,6 +639,8 @@ int stack_reserve(IroHipDiTStack *s, int M, int B) {
     if (e == hipSuccess) e = hipMalloc(&s->k, md);
     if (e == hipSuccess) e = hipMalloc(&s->v, md);
     if (e == hipSuccess) e = hipMalloc(&s->g, md);
+    if (e == hipSuccess) e = hipMalloc(&s->h, md);
+    if (e == hipSuccess) e = hipMalloc(&s->mix, md);
     if (e == hipSuccess) e = hipMalloc(&s->hidden, sizeof(float) * (size_t)M * s->H);
     if (e == hipSuccess)
         e = hipMalloc(&s->mod, sizeof(float) * (size_t)B * s->blocks * s->ada_np);
@@ -962,6 +965,40 @@ int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B
     s->graph = graph;
     s->gexec = exec;
     IRO_HIP_TRY(ctx, hipGraphLaunch(s->gexec, ctx->stream));
+    return ctx->has_err ? -1 : 0;
+}
+
+int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int B, int S,
+                                    const float *ada_attn, const float *ada_mlp,
+                                    const float *q_norm, const float *k_norm, float eps,
+                                    const IroHipAttnContext *actx, const float *context_k,
+                                    const float *context_v) {
+    if (!s || !x || B <= 0 || S <= 0 || !ada_attn || !ada_mlp || !q_norm || !k_norm || !actx ||
+        block < 0 || block >= s->blocks)
+        return set_error(s ? s->ctx : nullptr, "dit_block_forward: invalid arguments");
+    IroHipContext *ctx = s->ctx;
+    if (!s->ada_set[block]) return set_error(ctx, "dit_block_forward: block %d has no weights", block);
+    const int M = B * S, D = s->D, rm = s->residual_mask;
+    if (stack_reserve(s, M, B)) return -1;
+    const size_t BD = (size_t)B * D;
+    // dit.c:1003-1006: h = RMSNorm-modulate(x) with the attention shift/scale.
+    if (iro_hip_dit_adaln_apply(ctx, x, B, S, D, ada_attn, ada_attn + BD, eps, s->h)) return -1;
+    // dit.c:785-792: one quantization of h, Q/K/V/gate from the fused weight.
+    if (qkvg_impl(ctx, s->h, M, s->qkvg[block], s->q, s->k, s->v, s->g, rm & 1)) return -1;
+    // dit.c:803, 808-870, 872: norm + RoPE, attention core, sigmoid gate.
+    if (iro_hip_dit_qk_norm_rope(ctx, s->q, q_norm, s->k, k_norm, B, S, D, eps)) return -1;
+    if (iro_hip_dit_attention(ctx, actx, s->q, s->k, s->v, s->g, B, S, D, context_k, context_v,
+                              s->mix))
+        return -1;
+    // dit.c:878-881, 1012-1020: Wo, then x += gate * branch.
+    if (linear_gated_impl(ctx, s->mix, M, D, s->wo[block], rm & 2, nullptr, 0, x,
+                          ada_attn + 2 * BD, D, S))
+        return -1;
+    // dit.c:1022-1039: the MLP half.
+    if (iro_hip_dit_adaln_apply(ctx, x, B, S, D, ada_mlp, ada_mlp + BD, eps, s->h)) return -1;
+    if (swiglu_impl(ctx, s->h, M, s->w13[block], s->w2[block], rm & 4, rm & 8, s->hidden, nullptr,
+                    x, ada_mlp + 2 * BD, D, S))
+        return -1;
     return ctx->has_err ? -1 : 0;
 }
 

@@ -105,6 +105,8 @@ def load() -> C.CDLL:
         "iro_hip_dit_stack_destroy": ([_vp], None),
         "iro_hip_selfcheck_silu": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_stack_use_graph": ([_vp, _i], _i),
+        "iro_hip_dit_stack_block_forward": ([_vp, _i, _vp, _i, _i, _vp, _vp, _vp, _vp, C.c_float,
+                                             _vp, _vp, _vp], _i),
         "iro_hip_dit_adaln_apply": ([_vp, _vp, _i, _i, _i, _vp, _vp, C.c_float, _vp], _i),
         "iro_hip_dit_qk_norm_rope": ([_vp, _vp, _vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
         "iro_hip_dit_head_rmsnorm": ([_vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
@@ -579,6 +581,14 @@ class DiTStack:
     def step(self, x: DeviceArray, cond: DeviceArray, B: int, S: int):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_step(self.h, x.vp, cond.vp, B, S),
                         "dit_stack_step")
+
+    def block_forward(self, block: int, x: DeviceArray, B: int, S: int, ada_attn: DeviceArray,
+                      ada_mlp: DeviceArray, q_norm: DeviceArray, k_norm: DeviceArray, eps: float,
+                      actx: "AttnContext", context_k: DeviceArray, context_v: DeviceArray):
+        """dit.c:984-1040: one DiT block in place on x [B*S, D]."""
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_block_forward(
+            self.h, block, x.vp, B, S, ada_attn.vp, ada_mlp.vp, q_norm.vp, k_norm.vp, eps,
+            actx.h, context_k.vp, context_v.vp), "dit_block_forward")
 
     def use_graph(self, on: bool):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_use_graph(self.h, int(bool(on))),

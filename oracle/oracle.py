@@ -341,6 +341,24 @@ class Reference:
                                                  _f32p]
         L.ref_dit_attention_identity.restype = C.c_int
 
+    def dit_block_zero_adaln(self, x, cond, ada, w, ck, cv, mask, B, S, eps, use_int8=True):
+        """iro_dit_block (dit.c:1042-1047) of one layer with zero adaLN low-rank
+        weights: ada [6, D] biases, w = (wq, wk, wv, wgate, wo, q_norm, k_norm,
+        w1, w3, w2); returns the updated x."""
+        x = np.array(x, np.float32, copy=True)
+        mask = np.ascontiguousarray(mask, np.uint8)
+        dims = (C.c_int * 2)()
+        ws = [_f32(a) for a in w]
+        self.lib.ref_dit_block_zero_adaln.argtypes = ([_f32p] * 15 + [_u8p] + [C.c_int] * 3 +
+                                                     [C.c_float, C.c_int, C.POINTER(C.c_int)])
+        self.lib.ref_dit_block_zero_adaln.restype = C.c_int
+        rc = self.lib.ref_dit_block_zero_adaln(
+            _p(x, _f32p), _p(_f32(cond), _f32p), _p(_f32(ada), _f32p),
+            *[_p(a, _f32p) for a in ws], _p(_f32(ck), _f32p), _p(_f32(cv), _f32p),
+            _p(mask, _u8p), B, S, mask.shape[-1], eps, int(bool(use_int8)), dims)
+        assert rc == 0 and dims[0] == x.shape[-1], (rc, dims[0])
+        return x
+
     def dit_attention_identity(self, x, q_norm, k_norm, ck, cv, mask, B, S, shared, eps):
         """iro_dit_attention(_shared_context) (dit.c:895-911) with identity
         projections: the attention core on (normed x, normed x, x, gate x)."""
