@@ -410,6 +410,159 @@ void orc_adaln_apply(const float *x, const float *shift, const float *scale, int
     }
 }
 
+/* ---- glibc expm1f / tanhf and the adaLN parameters: dit.c:543-588 ------- */
+
+static inline uint32_t orc_fbits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+static inline float orc_bitsf(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* expm1f and tanhf as glibc 2.35 computes them: the float port of fdlibm 5.3's
+   s_expm1f.c (argument reduction by ln2 in two pieces, a degree-5 rational
+   correction in x^2/2 with the published Q1..Q5) and s_tanhf.c (tanh through
+   expm1 of 2|x|).  Equal to libm on every float input
+   (tests/test_oracle_pins.py::test_tanhf_restatement_equals_libm_on_every_float). */
+float orc_expm1f(float x) {
+    const float one = 1.0f, tiny = 1.0e-30f, huge = 1.0e+30f;
+    const float o_threshold = 8.8721679688e+01f, ln2_hi = 6.9313812256e-01f,
+                ln2_lo = 9.0580006145e-06f, invln2 = 1.4426950216e+00f;
+    const float Q1 = -3.3333335072e-02f, Q2 = 1.5873016091e-03f, Q3 = -7.9365076090e-05f,
+                Q4 = 4.0082177293e-06f, Q5 = -2.0109921195e-07f;
+    float y, hi, lo, c = 0, t, e, hxs, hfx, r1;
+    int32_t k, xsb;
+    uint32_t hx = orc_fbits(x);
+    xsb = hx & 0x80000000;
+    y = xsb == 0 ? x : -x;
+    hx &= 0x7fffffff;
+    if (hx >= 0x4195b844) {
+        if (hx >= 0x42b17218) {
+            if (hx > 0x7f800000) return x + x;
+            if (hx == 0x7f800000) return xsb == 0 ? x : -1.0f;
+            if (x > o_threshold) return huge * huge;
+        }
+        if (xsb != 0) return tiny - one;
+    }
+    if (hx > 0x3eb17218) {
+        if (hx < 0x3F851592) {
+            if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+            else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+        } else {
+            k = invln2 * x + (xsb == 0 ? 0.5f : -0.5f);
+            t = k;
+            hi = x - t * ln2_hi;
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000) {
+        t = huge + x;
+        return x - (t - (huge + x));
+    } else k = 0;
+    hfx = 0.5f * x;
+    hxs = x * hfx;
+    r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    t = 3.0f - r1 * hfx;
+    e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = (x * (e - c) - c);
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return one + 2.0f * (x - e);
+    }
+    if (k <= -2 || k > 56) {
+        y = one - (e - x);
+        y = orc_bitsf(orc_fbits(y) + ((uint32_t)k << 23));
+        return y - one;
+    }
+    t = one;
+    if (k < 23) {
+        t = orc_bitsf(0x3f800000 - (0x1000000 >> k));
+        y = t - (e - x);
+        y = orc_bitsf(orc_fbits(y) + ((uint32_t)k << 23));
+    } else {
+        t = orc_bitsf((uint32_t)(0x7f - k) << 23);
+        y = x - (e + t);
+        y += one;
+        y = orc_bitsf(orc_fbits(y) + ((uint32_t)k << 23));
+    }
+    return y;
+}
+float orc_tanhf(float x) {
+    const float one = 1.0f, two = 2.0f, tiny = 1.0e-30f;
+    float t, z;
+    int32_t jx = (int32_t)orc_fbits(x), ix = jx & 0x7fffffff;
+    if (ix >= 0x7f800000) return jx >= 0 ? one / x + one : one / x - one;
+    if (ix < 0x41b00000) {
+        if (ix == 0) return x;
+        if (ix < 0x24000000) return x * (one + x);
+        if (ix >= 0x3f800000) {
+            t = orc_expm1f(two * fabsf(x));
+            z = one - two / (t + two);
+        } else {
+            t = orc_expm1f(-two * fabsf(x));
+            z = -t / (t + two);
+        }
+    } else z = one - tiny;
+    return jx >= 0 ? z : -z;
+}
+
+long long orc_tanhf_mismatches(int threads) {
+    long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static) num_threads(threads)
+    for (long long i = 0; i < (1LL << 32); i++) {
+        const float x = orc_bitsf((uint32_t)i);
+        const float a = orc_tanhf(x), b = tanhf(x);
+        if (orc_fbits(a) != orc_fbits(b) && !(a != a && b != b)) bad++;
+    }
+    return bad;
+}
+
+/* dit.c:543-558 adaln_branch for branches 0..2 of one adaLN, then the gate's
+   tanhf (dit.c:588): act = silu(cond slice) as x / (1 + expf(-x));
+   low[r] = sum_d act[d] down[r][d] in index order (+ 0, the scalar linear's
+   absent bias); out[n] = (sum_r low[r] up[n][r] in index order) + bias[n],
+   then + cond slice[n]; gate = tanhf(out).  cond [B, 3D]; down[i] [R, D],
+   up[i] [D, R], bias[i] [D]; out [3, B, D]: shift, scale, gate. */
+void orc_adaln_params(const float *cond, int B, int D, int R, const float *const *down,
+                      const float *const *up, const float *const *bias, float *out) {
+    float *act = malloc(sizeof(float) * (size_t)D);
+    float *low = malloc(sizeof(float) * (size_t)R);
+    for (int br = 0; br < 3; br++)
+        for (int b = 0; b < B; b++) {
+            const float *in = cond + (size_t)b * 3 * D + (size_t)br * D;
+            for (int d = 0; d < D; d++) act[d] = in[d] / (1.0f + expf(-in[d]));
+            for (int r = 0; r < R; r++) {
+                float acc = 0.0f;
+                for (int d = 0; d < D; d++) {
+                    const float p = act[d] * down[br][(size_t)r * D + d];
+                    acc = acc + p;
+                }
+                low[r] = acc + 0.0f;
+            }
+            float *o = out + ((size_t)br * B + b) * D;
+            for (int n = 0; n < D; n++) {
+                float acc = 0.0f;
+                for (int r = 0; r < R; r++) {
+                    const float p = low[r] * up[br][(size_t)n * R + r];
+                    acc = acc + p;
+                }
+                const float y = acc + bias[br][n];
+                o[n] = y + in[n];
+                if (br == 2) o[n] = orc_tanhf(o[n]);
+            }
+        }
+    free(act);
+    free(low);
+}
+
 /* ---- per-head RMSNorm and half-RoPE: dit.c:619-706 ---------------------- */
 
 /* The rotation table of head_rmsnorm_rope_pair (dit.c:641-657, 697-703): per

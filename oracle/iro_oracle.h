@@ -93,6 +93,11 @@ void orc_fp32_digests(int threads, unsigned long long *sqrt_digest,
                       unsigned long long *recip_digest);
 void orc_adaln_apply(const float *x, const float *shift, const float *scale, int B, int S, int D,
                      float eps, float *h);
+float orc_expm1f(float x);
+float orc_tanhf(float x);
+long long orc_tanhf_mismatches(int threads);
+void orc_adaln_params(const float *cond, int B, int D, int R, const float *const *down,
+                      const float *const *up, const float *const *bias, float *out);
 void orc_rope_table(int S, float *cos_t, float *sin_t);
 int orc_head_norm_rope(float *q, const float *qw, float *k, const float *kw, int B, int S,
                        int heads, float eps, int rope);

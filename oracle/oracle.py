@@ -66,6 +66,12 @@ class Oracle:
                                       _f32p]
         L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
         L.orc_rope_table.argtypes = [C.c_int, _f32p, _f32p]
+        L.orc_tanhf.argtypes = [C.c_float]
+        L.orc_tanhf.restype = C.c_float
+        L.orc_tanhf_mismatches.argtypes = [C.c_int]
+        L.orc_tanhf_mismatches.restype = C.c_longlong
+        L.orc_adaln_params.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.POINTER(_f32p),
+                                       C.POINTER(_f32p), C.POINTER(_f32p), _f32p]
         L.orc_head_norm_rope.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int,
                                          C.c_float, C.c_int]
         L.orc_head_norm_rope.restype = C.c_int
@@ -192,6 +198,23 @@ class Oracle:
         self.lib.orc_adaln_apply(_p(x, _f32p), _p(shift, _f32p), _p(scale, _f32p), B, S, D,
                                  eps, _p(h, _f32p))
         return h
+
+    def tanhf_mismatches(self):
+        """Inputs (of all 2^32) where the fdlibm tanhf restatement differs from libm."""
+        return self.lib.orc_tanhf_mismatches(self.threads)
+
+    def adaln_params(self, cond, down, up, bias):
+        """dit.c:543-588 for one adaLN: [3, B, D] (shift, scale, tanhf gate) from
+        cond [B, 3D] and three (down [R, D], up [D, R], bias [D]) branches."""
+        cond = _f32(cond)
+        B, D = cond.shape[0], cond.shape[1] // 3
+        R = down[0].shape[0]
+        ds, us, bs = [_f32(a) for a in down], [_f32(a) for a in up], [_f32(a) for a in bias]
+        out = np.empty((3, B, D), np.float32)
+        arr = lambda xs: (_f32p * 3)(*[_p(a, _f32p) for a in xs])
+        self.lib.orc_adaln_params(_p(cond, _f32p), B, D, R, arr(ds), arr(us), arr(bs),
+                                  _p(out, _f32p))
+        return out
 
     def rope_table(self, S):
         """(cos, sin) [S, 32] of head_rmsnorm_rope_pair (dit.c:641-657, 697-703)."""
@@ -358,6 +381,22 @@ class Reference:
             _p(mask, _u8p), B, S, mask.shape[-1], eps, int(bool(use_int8)), dims)
         assert rc == 0 and dims[0] == x.shape[-1], (rc, dims[0])
         return x
+
+    def dit_adaln_full(self, eps, x, cond, w, B, S):
+        """iro_dit_adaln (dit.c:614) with low-rank weights w (9 arrays, dit.h
+        order): (h [B*S, D], gate [B, D])."""
+        x, cond = _f32(x), _f32(cond)
+        ws = [_f32(a) for a in w]
+        h = np.empty_like(x)
+        gate = np.empty((B, x.shape[-1]), np.float32)
+        self.lib.ref_dit_adaln_full.argtypes = [C.c_float, _f32p, _f32p, C.POINTER(_f32p),
+                                                C.c_int, C.c_int, _f32p, _f32p]
+        self.lib.ref_dit_adaln_full.restype = C.c_int
+        rc = self.lib.ref_dit_adaln_full(eps, _p(x, _f32p), _p(cond, _f32p),
+                                         (_f32p * 9)(*[_p(a, _f32p) for a in ws]), B, S,
+                                         _p(h, _f32p), _p(gate, _f32p))
+        assert rc == 0
+        return h, gate
 
     def dit_attention_identity(self, x, q_norm, k_norm, ck, cv, mask, B, S, shared, eps):
         """iro_dit_attention(_shared_context) (dit.c:895-911) with identity

@@ -99,3 +99,13 @@ out:
     free(z);
     return rc;
 }
+
+/* iro_dit_adaln (dit.c:614-617) with the given low-rank weights: w holds
+   shift_down, shift_up, shift_bias, scale_down, scale_up, scale_bias,
+   gate_down, gate_up, gate_bias (dit.h:11-23 order).  h [B*S, MODEL_DIM],
+   gate [B, MODEL_DIM]. */
+int ref_dit_adaln_full(float eps, const float *x, const float *cond, const float *const *w,
+                       int B, int S, float *h, float *gate) {
+    IroAdaLN a = {w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7], w[8]};
+    return iro_dit_adaln(&a, eps, x, cond, B, S, h, gate);
+}

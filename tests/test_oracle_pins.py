@@ -383,3 +383,30 @@ def test_attention_core_equals_reference_strict_build(oracle, shared):
     want = want + np.float32(0.0)
     assert (want == 0).any()  # the underflowing gates are exercised
     assert _eq(got, want)
+
+
+def test_tanhf_restatement_equals_libm_on_every_float(oracle):
+    """The fdlibm tanhf/expm1f restatement (glibc 2.35's algorithm) equals the
+    C library's tanhf on all 2^32 float inputs (NaNs compared as NaN)."""
+    assert oracle.tanhf_mismatches() == 0
+
+
+def test_adaln_params_equal_reference_strict_build(oracle):
+    """iro_dit_adaln (dit.c:614) of the strict reference build with seeded
+    low-rank weights: its h equals the oracle's adaLN apply on the oracle's
+    shift/scale, and its gate equals the oracle's tanhf gate, bit for bit
+    (SiLU of cond, the rank-192 down and up linears in index order, bias and
+    cond slice, tanhf)."""
+    D, R, B, S, eps = 1280, 192, 3, 20, 1e-6
+    x = gauss(720, (B * S, D))
+    cond = gauss(721, (B, 3 * D), 0.8)
+    w = []
+    for br in range(3):
+        w += [gauss(722 + 3 * br, (R, D), 0.05), gauss(723 + 3 * br, (D, R), 0.05),
+              gauss(724 + 3 * br, (D,), 0.1)]
+    w[8] = w[8] * 80.0  # gate biases: some tanhf saturate to +-1
+    h, gate = _ref("strict").dit_adaln_full(eps, x, cond, w, B, S)
+    p = oracle.adaln_params(cond, w[0::3], w[1::3], w[2::3])
+    assert _eq(gate, p[2])
+    assert _eq(h, oracle.adaln_apply(x, p[0], p[1], B, S, eps))
+    assert (np.abs(p[2]) == 1.0).any()
