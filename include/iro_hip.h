@@ -209,6 +209,24 @@ int iro_hip_weight_load(IroHipContext *ctx, const char *path, IroHipWeight **out
 
 /* ---- fp32 neighbours ------------------------------------------------------ */
 
+/* dit.c:543-588, the parameters of n_adaln (1 or 2) adaLNs from cond [B, 3D]:
+   for adaLN a and branch br (shift, scale, gate), act = silu(cond[:, br*D:
+   (br+1)*D]) as x / (1 + expf(-x)); low = act @ down^T (down [R, D]) summed
+   in index order; out = (low @ up^T (up [D, R]) in index order + bias) +
+   the cond slice; the gate branch then through glibc's tanhf.  weights: a
+   host array of 9 * n_adaln device pointers, per adaLN in dit.h's IroAdaLN
+   order (shift_down, shift_up, shift_bias, scale_down, ..., gate_bias).
+   out [n_adaln][3][B][D] device memory -- the shift, scale and gate that
+   iro_hip_dit_adaln_apply and the gated residuals take.  Bit-identical to the
+   scalar build. */
+int iro_hip_dit_adaln_params(IroHipContext *ctx, const float *cond, int B, int D, int R,
+                             const float *const *weights, int n_adaln, float *out);
+
+/* The device tanhf on all 2^32 float inputs, hashed as the oracle's
+   orc_tanhf_digest hashes libm's (a known-answer check of the restatement;
+   takes a few seconds). */
+int iro_hip_selfcheck_tanhf(IroHipContext *ctx, unsigned long long *digest);
+
 /* dit.c:593-606, the apply step of dit_adaln: h = x * inv * (1 + scale[b])
    + shift[b] for row r of x [B*S, D] (b = r / S, shift/scale [B, D]) with
    inv = 1 / sqrtf(mean(x^2) + eps), the sum of squares taken in index order

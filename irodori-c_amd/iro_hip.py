@@ -111,6 +111,8 @@ def load() -> C.CDLL:
         "iro_hip_dit_qk_norm_rope": ([_vp, _vp, _vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
         "iro_hip_dit_head_rmsnorm": ([_vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
         "iro_hip_dit_attn_context_create": ([_vp, _vp, _i, _i, _i, C.POINTER(_vp)], _i),
+        "iro_hip_dit_adaln_params": ([_vp, _vp, _i, _i, _i, C.POINTER(_vp), _i, _vp], _i),
+        "iro_hip_selfcheck_tanhf": ([_vp, C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_attn_context_destroy": ([_vp], None),
         "iro_hip_dit_attention": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp], _i),
         "iro_hip_selfcheck_fp32": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
@@ -413,6 +415,19 @@ class Context:
         """dit.c:619-636 in place on x [B*S, D]."""
         self._check(self.lib.iro_hip_dit_head_rmsnorm(self.h, x.vp, weight.vp, B, S, D, eps),
                     "dit_head_rmsnorm")
+
+    def dit_adaln_params(self, cond: DeviceArray, B: int, D: int, R: int, weights,
+                         out: DeviceArray):
+        """dit.c:543-588: out [len(weights) // 9, 3, B, D] from cond [B, 3D]."""
+        n = len(weights) // 9
+        arr = (_vp * len(weights))(*[w.vp for w in weights])
+        self._check(self.lib.iro_hip_dit_adaln_params(self.h, cond.vp, B, D, R, arr, n, out.vp),
+                    "dit_adaln_params")
+
+    def selfcheck_tanhf(self) -> int:
+        d = C.c_ulonglong(0)
+        self._check(self.lib.iro_hip_selfcheck_tanhf(self.h, C.byref(d)), "selfcheck_tanhf")
+        return int(d.value)
 
     def attn_context(self, mask, context_batch: int) -> "AttnContext":
         """The joined-key layout of mask [B, C] (host uint8) for dit_attention."""

@@ -525,6 +525,20 @@ long long orc_tanhf_mismatches(int threads) {
     return bad;
 }
 
+/* The tanhf digest of the device self-check: sum over all 2^32 inputs u of
+   (u * K1) ^ (bits(tanhf(u)) * K2), NaN results as 0x7FC00000. */
+unsigned long long orc_tanhf_digest(int threads) {
+    unsigned long long h = 0;
+#pragma omp parallel for reduction(+ : h) schedule(static) num_threads(threads)
+    for (long long i = 0; i < (1LL << 32); i++) {
+        const float t = orc_tanhf(orc_bitsf((uint32_t)i));
+        const uint32_t ut = t != t ? 0x7FC00000u : orc_fbits(t);
+        h += ((unsigned long long)(uint32_t)i * 0x9E3779B97F4A7C15ull) ^
+             ((unsigned long long)ut * 0xC2B2AE3D27D4EB4Full);
+    }
+    return h;
+}
+
 /* dit.c:543-558 adaln_branch for branches 0..2 of one adaLN, then the gate's
    tanhf (dit.c:588): act = silu(cond slice) as x / (1 + expf(-x));
    low[r] = sum_d act[d] down[r][d] in index order (+ 0, the scalar linear's

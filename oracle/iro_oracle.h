@@ -96,6 +96,7 @@ void orc_adaln_apply(const float *x, const float *shift, const float *scale, int
 float orc_expm1f(float x);
 float orc_tanhf(float x);
 long long orc_tanhf_mismatches(int threads);
+unsigned long long orc_tanhf_digest(int threads);
 void orc_adaln_params(const float *cond, int B, int D, int R, const float *const *down,
                       const float *const *up, const float *const *bias, float *out);
 void orc_rope_table(int S, float *cos_t, float *sin_t);

@@ -70,6 +70,8 @@ class Oracle:
         L.orc_tanhf.restype = C.c_float
         L.orc_tanhf_mismatches.argtypes = [C.c_int]
         L.orc_tanhf_mismatches.restype = C.c_longlong
+        L.orc_tanhf_digest.argtypes = [C.c_int]
+        L.orc_tanhf_digest.restype = C.c_ulonglong
         L.orc_adaln_params.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.POINTER(_f32p),
                                        C.POINTER(_f32p), C.POINTER(_f32p), _f32p]
         L.orc_head_norm_rope.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int,
@@ -202,6 +204,10 @@ class Oracle:
     def tanhf_mismatches(self):
         """Inputs (of all 2^32) where the fdlibm tanhf restatement differs from libm."""
         return self.lib.orc_tanhf_mismatches(self.threads)
+
+    def tanhf_digest(self):
+        """The device self-check's hash of tanhf over all 2^32 inputs."""
+        return int(self.lib.orc_tanhf_digest(self.threads))
 
     def adaln_params(self, cond, down, up, bias):
         """dit.c:543-588 for one adaLN: [3, B, D] (shift, scale, tanhf gate) from
@@ -364,19 +370,21 @@ class Reference:
                                                  _f32p]
         L.ref_dit_attention_identity.restype = C.c_int
 
-    def dit_block_zero_adaln(self, x, cond, ada, w, ck, cv, mask, B, S, eps, use_int8=True):
-        """iro_dit_block (dit.c:1042-1047) of one layer with zero adaLN low-rank
-        weights: ada [6, D] biases, w = (wq, wk, wv, wgate, wo, q_norm, k_norm,
-        w1, w3, w2); returns the updated x."""
+    def dit_block(self, x, cond, ada, w, ck, cv, mask, B, S, eps, use_int8=True):
+        """iro_dit_block (dit.c:1042-1047) of one layer: ada = 18 adaLN arrays
+        (attention then MLP, dit.h order), w = (wq, wk, wv, wgate, wo, q_norm,
+        k_norm, w1, w3, w2); returns the updated x."""
         x = np.array(x, np.float32, copy=True)
         mask = np.ascontiguousarray(mask, np.uint8)
-        dims = (C.c_int * 2)()
+        dims = (C.c_int * 3)()
         ws = [_f32(a) for a in w]
-        self.lib.ref_dit_block_zero_adaln.argtypes = ([_f32p] * 15 + [_u8p] + [C.c_int] * 3 +
-                                                     [C.c_float, C.c_int, C.POINTER(C.c_int)])
-        self.lib.ref_dit_block_zero_adaln.restype = C.c_int
-        rc = self.lib.ref_dit_block_zero_adaln(
-            _p(x, _f32p), _p(_f32(cond), _f32p), _p(_f32(ada), _f32p),
+        adas = [_f32(a) for a in ada]
+        self.lib.ref_dit_block.argtypes = ([_f32p, _f32p, C.POINTER(_f32p)] + [_f32p] * 12 +
+                                           [_u8p] + [C.c_int] * 3 +
+                                           [C.c_float, C.c_int, C.POINTER(C.c_int)])
+        self.lib.ref_dit_block.restype = C.c_int
+        rc = self.lib.ref_dit_block(
+            _p(x, _f32p), _p(_f32(cond), _f32p), (_f32p * 18)(*[_p(a, _f32p) for a in adas]),
             *[_p(a, _f32p) for a in ws], _p(_f32(ck), _f32p), _p(_f32(cv), _f32p),
             _p(mask, _u8p), B, S, mask.shape[-1], eps, int(bool(use_int8)), dims)
         assert rc == 0 and dims[0] == x.shape[-1], (rc, dims[0])

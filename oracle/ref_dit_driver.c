@@ -40,28 +40,23 @@ int ref_dit_attention_identity(const float *x, const float *q_norm, const float 
     return rc;
 }
 
-/* iro_dit_block (dit.c:1042-1047) of layer 0 of a DiT whose adaLN low-rank
-   weights are zero, so each branch is its bias plus its slice of cond
-   (dit.c:543-558) and the gates are tanhf of that; the attention and MLP
-   weights are the given fp32 arrays, quantized to int8 as
-   iro_dit_int8_quantize does (dit.c:235-259) when use_int8 != 0.  ada holds
-   the six bias vectors [6][MODEL_DIM]: attention shift, scale, gate, then
-   MLP shift, scale, gate.  x [B*S, MODEL_DIM] is updated in place. */
-int ref_dit_block_zero_adaln(float *x, const float *cond, const float *ada, const float *wq,
-                             const float *wk, const float *wv, const float *wgate,
-                             const float *wo, const float *q_norm, const float *k_norm,
-                             const float *w1, const float *w3, const float *w2, const float *ck,
-                             const float *cv, const uint8_t *mask, int B, int S, int C,
-                             float eps, int use_int8, int *dims) {
-    float *z = calloc((size_t)MODEL_DIM * ADALN_RANK, sizeof(float));
+/* iro_dit_block (dit.c:1042-1047) of layer 0 of a DiT with the given adaLN
+   weights (ada: 18 arrays, the attention then the MLP IroAdaLN in dit.h:11-23
+   order) and attention / MLP weights, quantized to int8 as
+   iro_dit_int8_quantize does (dit.c:235-259) when use_int8 != 0.
+   x [B*S, MODEL_DIM] is updated in place. */
+int ref_dit_block(float *x, const float *cond, const float *const *ada, const float *wq,
+                  const float *wk, const float *wv, const float *wgate, const float *wo,
+                  const float *q_norm, const float *k_norm, const float *w1, const float *w3,
+                  const float *w2, const float *ck, const float *cv, const uint8_t *mask, int B,
+                  int S, int C, float eps, int use_int8, int *dims) {
     IroDiT *d = calloc(1, sizeof(IroDiT));
     IroDiTInt8 *q8 = calloc(1, sizeof(IroDiTInt8));
     int rc = -1;
-    if (!z || !d || !q8) goto out;
-    const float *bias[6];
-    for (int i = 0; i < 6; i++) bias[i] = ada + (size_t)i * MODEL_DIM;
-    IroAdaLN att = {z, z, bias[0], z, z, bias[1], z, z, bias[2]};
-    IroAdaLN mlp = {z, z, bias[3], z, z, bias[4], z, z, bias[5]};
+    if (!d || !q8) goto out;
+    IroAdaLN att = {ada[0], ada[1], ada[2], ada[3], ada[4], ada[5], ada[6], ada[7], ada[8]};
+    IroAdaLN mlp = {ada[9], ada[10], ada[11], ada[12], ada[13], ada[14], ada[15], ada[16],
+                    ada[17]};
     d->attention_adaln[0] = att;
     d->mlp_adaln[0] = mlp;
     IroJointAttention a = {0};
@@ -92,11 +87,11 @@ int ref_dit_block_zero_adaln(float *x, const float *cond, const float *ada, cons
     rc = iro_dit_block(d, 0, x, cond, ck, cv, mask, B, S, C);
     dims[0] = MODEL_DIM;
     dims[1] = MLP_DIM;
+    dims[2] = ADALN_RANK;
 out:
     if (q8) iro_dit_int8_free(q8);
     free(q8);
     free(d);
-    free(z);
     return rc;
 }
 

@@ -194,3 +194,10 @@ def test_sqrt_and_reciprocal_on_every_float(ctx, oracle):
     """The device's sqrtf and 1 / x, which the adaLN apply uses, equal the
     host's IEEE results on all 2^32 inputs (digests of every result)."""
     assert ctx.selfcheck_fp32() == oracle.fp32_digests()
+
+
+def test_tanhf_on_every_float(ctx_strict, oracle):
+    """The device's fdlibm tanhf (the adaLN gate, dit.c:588) hashed over all
+    2^32 inputs equals the hash of the oracle's restatement, which equals
+    libm's tanhf on every input (tests/test_oracle_pins.py)."""
+    assert ctx_strict.selfcheck_tanhf() == oracle.tanhf_digest()
