@@ -116,7 +116,8 @@ __device__ float tanhf_fdlibm(float x) {
     return jx >= 0 ? z : -z;
 }
 
-// Digest of tanhf over inputs base .. base + 2^28 - 1 (the oracle's hash).
+// Digest of tanhf over inputs base .. base + 2^28 - 1: the sum over u of
+// (u * K1) ^ (bits(tanhf(u)) * K2), NaN results as 0x7FC00000.
 __global__ __launch_bounds__(256) void tanhf_selfcheck_kernel(unsigned long long *out,
                                                               unsigned base) {
     __shared__ unsigned long long part[4];
@@ -136,7 +137,7 @@ struct AdaWeights {
     const float *w[18];  // per adaLN: down, up, bias of shift, scale, gate
 };
 
-// act [3][B][D] = silu(cond[b, br*D + d]) as x / (1 + expf(-x)) (ops.c:772-775).
+// act [3][B][D] = silu(cond[b, br*D + d]) as x / (1 + expf(-x)) (ops.c:776-779).
 __global__ __launch_bounds__(256) void ada_act_kernel(const float *__restrict__ cond, int B, int D,
                                                       float *__restrict__ act) {
     __shared__ uint64_t exptab[32];
