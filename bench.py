@@ -20,8 +20,10 @@ stage 2: 90000 frames, 384->192, kernel 16, stride 8).
 `--workload adaln` the fp32 adaLN apply step of a DiT block on the same
 M = 2250 rows (one call per step), `--workload qknorm` the per-head RMSNorm
 and half-RoPE of q and k, `--workload attention` the attention core (scores,
-softmax, P@V, gate) with a context of up to 300 rows; `--workload weights`
-the int8 weight build from a safetensors checkpoint.
+softmax, P@V, gate) with a context of up to 300 rows, `--workload block` one
+whole DiT block (adaLN parameters from cond, every fp32 and int8 step) at the
+reference model's dimensions; `--workload weights` the int8 weight build
+from a safetensors checkpoint.
 
 Prints one JSON line on stdout; diagnostics go to stderr.
 """
@@ -502,6 +504,105 @@ def attention_main(args):
     print(json.dumps(out), flush=True)
 
 
+def block_main(args):
+    """One DiT block forward (dit.c:984-1040) at the reference model's
+    dimensions (hidden 1280, 20 heads, MLP 3680, adaLN rank 192): one step =
+    the adaLN parameters of both halves from cond (iro_hip_dit_adaln_params)
+    and the block (iro_hip_dit_stack_block_forward) on 3 x 750 latent tokens
+    with 300 context rows (masks keep 250, 150, 200).  Bit-identical to the
+    reference's iro_dit_block (tests/test_gpu_dit_block.py).  The CPU
+    baseline is the reference's own scalar build (oracle/_ref) on a bounded
+    sample of the same block."""
+    D, H, R, C = 1280, 3680, 192, 300
+    B, S = args.batch, args.frames
+    keep = [250, 150, 200] + [100] * max(0, B - 3)
+    mask = np.zeros((B, C), np.uint8)
+    for b in range(B):
+        mask[b, :keep[b]] = 1
+    ctx = iro_hip.Context(0, iro_hip.STRICT)
+    log("backend:", ctx.backend())
+    stack = iro_hip.DiTStack(ctx, 1, D, H, args.residual_mask)
+    w = [gauss(100 + i, (D, D), 0.03) for i in range(5)]
+    wn = [gauss(105, (D,), 0.2) + 1.0, gauss(106, (D,), 0.2) + 1.0]
+    wm = [gauss(107, (H, D), 0.03), gauss(108, (H, D), 0.03), gauss(109, (D, H), 0.02)]
+    ada = []
+    for i in range(6):
+        ada += [gauss(110 + 3 * i, (R, D), 0.05), gauss(111 + 3 * i, (D, R), 0.05),
+                gauss(112 + 3 * i, (D,), 0.1)]
+    wd = [ctx.to_device(a) for a in w + wn + wm]
+    stack.set_block(0, ctx.to_device(np.zeros((6 * D, D), np.float32)), *wd[:5], *wd[7:])
+    adad = [ctx.to_device(a) for a in ada]
+    actx = ctx.attn_context(mask, B)
+    x0 = gauss(120, (B * S, D))
+    cond = ctx.to_device(gauss(121, (B, 3 * D), 0.5))
+    ck, cv = ctx.to_device(gauss(122, (B * C, D))), ctx.to_device(gauss(123, (B * C, D)))
+    ada_attn, ada_mlp = ctx.empty((3, B, D), np.float32), ctx.empty((3, B, D), np.float32)
+    x = ctx.to_device(x0)
+
+    def step():
+        ctx.dit_adaln_params(cond, B, D, R, adad[:9], ada_attn)
+        ctx.dit_adaln_params(cond, B, D, R, adad[9:], ada_mlp)
+        stack.block_forward(0, x, B, S, ada_attn, ada_mlp, wd[5], wd[6], 1e-6, actx, ck, cv)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    t0 = time.perf_counter()
+    ctx.record(e0)
+    for _ in range(args.steps):
+        step()
+    ctx.record(e1)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.elapsed_ms(e0, e1) / args.steps
+    actx.destroy()
+    stack.destroy()
+    ctx.close()
+    rate = B * S / (ev_ms * 1e-3)
+    log(f"block: {ev_ms:.3f} ms/block events, {rate:.0f} tokens/s")
+    cpu = None
+    ref_lib = os.path.join(REPO, "oracle", "_ref", "libref_strict.so")
+    if not args.no_cpu_baseline and os.path.exists(ref_lib):
+        from oracle import Reference
+        ref = Reference("strict")
+        Bs, Ss, Cs = 1, 256, 64
+        ms = np.zeros((Bs, Cs), np.uint8)
+        ms[0, :32] = 1
+        xs, conds = gauss(124, (Bs * Ss, D)), gauss(125, (Bs, 3 * D), 0.5)
+        cks, cvs = gauss(126, (Bs * Cs, D)), gauss(127, (Bs * Cs, D))
+        t1 = time.perf_counter()
+        ref.dit_block(xs, conds, ada, w + wn + wm, cks, cvs, ms, Bs, Ss, 1e-6, use_int8=True)
+        dt = time.perf_counter() - t1
+        log(f"cpu baseline: reference block at B={Bs} S={Ss} in {dt:.2f} s")
+        cpu = {"value": round(Bs * Ss / dt, 2), "unit": "tokens/s", "cores": 1,
+               "kind": "reference", "ms_per_step": round(dt * 1e3, 1),
+               "sample": (f"the reference's iro_dit_block (scalar -O2 build, int8 weights "
+                          f"quantized in the call) on {Bs} x {Ss} tokens with {Cs} context "
+                          f"rows (32 kept), once, one thread")}
+    out = {
+        "metric": "DiT block forward tokens/s (hidden 1280, MLP 3680, 20 heads), 1 GPU",
+        "value": round(rate, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ev_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32+int8",
+        "data": "synthetic (seeded Irwin-Hall Gaussian activations and random-init weights)",
+        "config": {"workload": f"one DiT block forward incl. adaLN parameters, {B} x {S} latent "
+                               f"tokens, {C} context rows (kept {keep[:B]}), int8 QKVG/Wo/W1W3/W2",
+                   "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+                   "residual_mask": args.residual_mask, "parallelism": "single GPU"},
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def weights_main(args):
     """The weight source (safetensors.c:302-530, generate.c:526-544): one step
     = the int8 weights of one DiT block (modulation, Wq/Wk/Wv/Wgate, Wo, W1,
@@ -713,7 +814,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["stack", "weights", "adaln", "qknorm", "attention"]
+    ap.add_argument("--workload", choices=["stack", "weights", "adaln", "qknorm", "attention",
+                                           "block"]
                     + sorted(CONV_WORKLOADS)
                     + sorted(CONVT_WORKLOADS),
                     default="stack",
@@ -760,6 +862,9 @@ def main():
         return
     if args.workload == "attention":
         attention_main(args)
+        return
+    if args.workload == "block":
+        block_main(args)
         return
 
     B, S, D, H = args.batch, args.frames, args.hidden, args.mlp

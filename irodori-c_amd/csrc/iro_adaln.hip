@@ -150,33 +150,76 @@ __global__ __launch_bounds__(256) void ada_act_kernel(const float *__restrict__ 
     act[i] = x / (1.0f + expf_glibc(-x, exptab));
 }
 
+// sum_d x[d] * w[d] for d = 0 .. n-1 in index order (each product rounded,
+// then added): x in LDS (the block's shared row), w this lane's row in
+// global memory.  When w is 16-byte aligned the row streams through
+// registers 64 values at a time, the next 64 loaded while the current ones
+// are added, so the chain waits on memory once per row rather than per term.
+__device__ __forceinline__ float dot_in_order(const float *x, const float *__restrict__ w,
+                                              int n) {
+    float acc = 0.0f;
+    int d = 0;
+    if ((((uintptr_t)w) & 15) == 0) {
+        const int nc = n / 64;
+        float4 cur[16], nxt[16];
+        if (nc > 0) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) cur[j] = reinterpret_cast<const float4 *>(w)[j];
+        }
+        for (int c = 0; c < nc; ++c) {
+            if (c + 1 < nc) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    nxt[j] = reinterpret_cast<const float4 *>(w + (c + 1) * 64)[j];
+            }
+            const float *xc = x + c * 64;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                acc = acc + xc[4 * j] * cur[j].x;
+                acc = acc + xc[4 * j + 1] * cur[j].y;
+                acc = acc + xc[4 * j + 2] * cur[j].z;
+                acc = acc + xc[4 * j + 3] * cur[j].w;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) cur[j] = nxt[j];
+        }
+        d = nc * 64;
+    }
+    for (; d < n; ++d) acc = acc + x[d] * w[d];
+    return acc;
+}
+
 // low [A][3][B][R]: lane r of (adaLN a, branch br, batch b) sums act * down
-// over d in index order, then adds the scalar linear's zero bias.
+// over d in index order, then adds the scalar linear's zero bias.  The
+// block's act row is staged in LDS (D <= kAdaMaxD).
+constexpr int kAdaMaxD = 8192;
 __global__ __launch_bounds__(64) void ada_low_kernel(const float *__restrict__ act, AdaWeights w,
                                                      int B, int D, int R,
                                                      float *__restrict__ low) {
-    const int r = blockIdx.x * 64 + threadIdx.x;
+    __shared__ __attribute__((aligned(16))) float xs[kAdaMaxD];
     const int br = blockIdx.y / B, b = blockIdx.y - br * B, a = blockIdx.z;
-    if (r >= R) return;
     const float *x = act + ((size_t)br * B + b) * D;
-    const float *wr = w.w[a * 9 + br * 3] + (size_t)r * D;
-    float acc = 0.0f;
-    for (int d = 0; d < D; ++d) acc = acc + x[d] * wr[d];
+    for (int d = threadIdx.x; d < D; d += 64) xs[d] = x[d];
+    __syncthreads();
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    if (r >= R) return;
+    const float acc = dot_in_order(xs, w.w[a * 9 + br * 3] + (size_t)r * D, D);
     low[(((size_t)a * 3 + br) * B + b) * R + r] = acc + 0.0f;
 }
 
 // out [A][3][B][D]: (sum_r low * up in index order) + bias, + the cond slice;
-// the gate branch through tanhf.
+// the gate branch through tanhf.  The block's low row is staged in LDS.
 __global__ __launch_bounds__(64) void ada_out_kernel(const float *__restrict__ low,
                                                      const float *__restrict__ cond, AdaWeights w,
                                                      int B, int D, int R, float *__restrict__ out) {
-    const int n = blockIdx.x * 64 + threadIdx.x;
+    __shared__ __attribute__((aligned(16))) float ls[kAdaMaxD];
     const int br = blockIdx.y / B, b = blockIdx.y - br * B, a = blockIdx.z;
-    if (n >= D) return;
     const float *l = low + (((size_t)a * 3 + br) * B + b) * R;
-    const float *ur = w.w[a * 9 + br * 3 + 1] + (size_t)n * R;
-    float acc = 0.0f;
-    for (int r = 0; r < R; ++r) acc = acc + l[r] * ur[r];
+    for (int r = threadIdx.x; r < R; r += 64) ls[r] = l[r];
+    __syncthreads();
+    const int n = blockIdx.x * 64 + threadIdx.x;
+    if (n >= D) return;
+    const float acc = dot_in_order(ls, w.w[a * 9 + br * 3 + 1] + (size_t)n * R, R);
     const float y = acc + w.w[a * 9 + br * 3 + 2][n];
     float o = y + cond[(size_t)b * 3 * D + (size_t)br * D + n];
     if (br == 2) o = tanhf_fdlibm(o);
@@ -195,8 +238,8 @@ int iro_hip_dit_adaln_params(IroHipContext *ctx, const float *cond, int B, int D
     if (!ctx || !cond || !weights || !out || B <= 0 || D <= 0 || R <= 0 ||
         (n_adaln != 1 && n_adaln != 2))
         return set_error(ctx, "dit_adaln_params: invalid arguments");
-    if ((long long)3 * B * D > INT32_MAX / 2 || 3LL * B > 65535)
-        return set_error(ctx, "dit_adaln_params: shape too large");
+    if ((long long)3 * B * D > INT32_MAX / 2 || 3LL * B > 65535 || D > kAdaMaxD || R > kAdaMaxD)
+        return set_error(ctx, "dit_adaln_params: shape too large (D, R <= %d)", kAdaMaxD);
     AdaWeights w{};
     for (int i = 0; i < 9 * n_adaln; ++i) {
         if (!weights[i]) return set_error(ctx, "dit_adaln_params: weight %d is NULL", i);
