@@ -227,6 +227,21 @@ int iro_hip_dit_adaln_params(IroHipContext *ctx, const float *cond, int B, int D
    takes a few seconds). */
 int iro_hip_selfcheck_tanhf(IroHipContext *ctx, unsigned long long *digest);
 
+/* ops.c:221-234, iro_linear of the scalar build: y [M, N] = x [M, K] @ w
+   [N, K]^T with each output a K-order chain of rounded products, then +
+   bias[n] (bias may be NULL: + 0).  Device memory.  Bit-identical to the
+   scalar build (the DiT's input / output projections, dit.c:532-540 and
+   1070-1089, and the context K/V projections, dit.c:708-735). */
+int iro_hip_linear_f32(IroHipContext *ctx, const float *x, int M, int K, const float *w, int N,
+                       const float *bias, float *y);
+
+/* ops.c:738-747, iro_rmsnorm: y = (x * inv) * w[d], inv = 1 / sqrtf(mean of
+   x^2 in index order + eps), rows of D (D % 4 == 0, D <= 2048, 16-byte
+   aligned).  Bit-identical to the scalar build (the DiT's output norm,
+   dit.c:1082). */
+int iro_hip_rmsnorm_f32(IroHipContext *ctx, const float *x, int M, int D, const float *w,
+                        float eps, float *y);
+
 /* dit.c:593-606, the apply step of dit_adaln: h = x * inv * (1 + scale[b])
    + shift[b] for row r of x [B*S, D] (b = r / S, shift/scale [B, D]) with
    inv = 1 / sqrtf(mean(x^2) + eps), the sum of squares taken in index order

@@ -300,7 +300,9 @@ __global__ __launch_bounds__(64) void adaln_rows_kernel(const float *__restrict_
 // off the chain -- while the later chunks are still in flight.  The chain is
 // the floor (one dependent add per column, about 4 ns each on gfx950); h is
 // computed from the registers, so x crosses HBM once.
-template <int RW, int NJ>
+// NORM: the plain RMSNorm of ops.c:738-747 instead -- h = (x * inv) * w[d]
+// with w passed as scale (one row, S = M) and no shift.
+template <int RW, int NJ, bool NORM = false>
 __global__ __launch_bounds__(64) void adaln_reg_kernel(const float *__restrict__ x,
                                                        const float *__restrict__ shift,
                                                        const float *__restrict__ scale, int M,
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(64) void adaln_reg_kernel(const float *__restrict__
             int col = j * 256 + lane * 4;
             col = col < D ? col : D - 4;
             cs[r][j] = *reinterpret_cast<const float4 *>(scale + (size_t)b * D + col);
-            t[r][j] = *reinterpret_cast<const float4 *>(shift + (size_t)b * D + col);
+            if (!NORM) t[r][j] = *reinterpret_cast<const float4 *>(shift + (size_t)b * D + col);
         }
     }
     float ms = 0.0f;
@@ -385,10 +387,17 @@ __global__ __launch_bounds__(64) void adaln_reg_kernel(const float *__restrict__
             const int col = j * 256 + lane * 4;
             if (!live || col >= D) continue;
             float4 o;
-            o.x = ((v[r][j].x * ir) * (1.0f + cs[r][j].x)) + t[r][j].x;
-            o.y = ((v[r][j].y * ir) * (1.0f + cs[r][j].y)) + t[r][j].y;
-            o.z = ((v[r][j].z * ir) * (1.0f + cs[r][j].z)) + t[r][j].z;
-            o.w = ((v[r][j].w * ir) * (1.0f + cs[r][j].w)) + t[r][j].w;
+            if (NORM) {
+                o.x = (v[r][j].x * ir) * cs[r][j].x;
+                o.y = (v[r][j].y * ir) * cs[r][j].y;
+                o.z = (v[r][j].z * ir) * cs[r][j].z;
+                o.w = (v[r][j].w * ir) * cs[r][j].w;
+            } else {
+                o.x = ((v[r][j].x * ir) * (1.0f + cs[r][j].x)) + t[r][j].x;
+                o.y = ((v[r][j].y * ir) * (1.0f + cs[r][j].y)) + t[r][j].y;
+                o.z = ((v[r][j].z * ir) * (1.0f + cs[r][j].z)) + t[r][j].z;
+                o.w = ((v[r][j].w * ir) * (1.0f + cs[r][j].w)) + t[r][j].w;
+            }
             *reinterpret_cast<float4 *>(hr + col) = o;
         }
     }
@@ -850,6 +859,32 @@ int iro_hip_dit_qk_norm_rope(IroHipContext *ctx, float *q, const float *q_weight
 int iro_hip_dit_head_rmsnorm(IroHipContext *ctx, float *x, const float *weight, int B, int S,
                              int D, float eps) {
     return head_norm(ctx, x, weight, nullptr, nullptr, B, S, D, eps, false, "dit_head_rmsnorm");
+}
+
+int iro_hip_rmsnorm_f32(IroHipContext *ctx, const float *x, int M, int D, const float *w,
+                        float eps, float *y) {
+    if (!ctx || !x || !w || !y || M < 0 || D <= 0)
+        return set_error(ctx, "rmsnorm_f32: invalid arguments");
+    if (M == 0) return 0;
+    if (D % 4 || D > 2048 ||
+        ((((uintptr_t)x) | ((uintptr_t)w) | ((uintptr_t)y)) & 15) != 0)
+        return set_error(ctx, "rmsnorm_f32: needs D %% 4 == 0, D <= 2048 and 16-byte aligned rows");
+    const int nj = (D + 255) / 256;
+    const size_t pitch_bytes = ((size_t)D + 4) * sizeof(float);
+#define IRO_NORM_LAUNCH(RWV, NJV)                                                              \
+    hipLaunchKernelGGL((adaln_reg_kernel<RWV, NJV, true>), dim3((M + RWV - 1) / RWV), dim3(64), \
+                       RWV * pitch_bytes, ctx->stream, x, nullptr, w, M, M, D, eps, y)
+    if (nj <= 2)
+        IRO_NORM_LAUNCH(2, 2);
+    else if (nj <= 4)
+        IRO_NORM_LAUNCH(2, 4);
+    else if (nj <= 5)
+        IRO_NORM_LAUNCH(2, 5);
+    else
+        IRO_NORM_LAUNCH(1, 8);
+#undef IRO_NORM_LAUNCH
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
 }
 
 int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int residual_mask,

@@ -112,6 +112,8 @@ def load() -> C.CDLL:
         "iro_hip_dit_head_rmsnorm": ([_vp, _vp, _vp, _i, _i, _i, C.c_float], _i),
         "iro_hip_dit_attn_context_create": ([_vp, _vp, _i, _i, _i, C.POINTER(_vp)], _i),
         "iro_hip_dit_adaln_params": ([_vp, _vp, _i, _i, _i, C.POINTER(_vp), _i, _vp], _i),
+        "iro_hip_linear_f32": ([_vp, _vp, _i, _i, _vp, _i, _vp, _vp], _i),
+        "iro_hip_rmsnorm_f32": ([_vp, _vp, _i, _i, _vp, C.c_float, _vp], _i),
         "iro_hip_selfcheck_tanhf": ([_vp, C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_attn_context_destroy": ([_vp], None),
         "iro_hip_dit_attention": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp], _i),
@@ -189,6 +191,26 @@ class DeviceArray:
         if self.ptr:
             self.ctx.lib.iro_hip_free(self.ctx.h, self.vp)
             self.ptr = None
+
+    def view(self, offset: int, shape) -> "DeviceView":
+        """A window of this allocation from element `offset` (no ownership)."""
+        v = DeviceView(self.ctx, shape, self.dtype, self.ptr + offset * self.dtype.itemsize)
+        assert offset >= 0 and offset * self.dtype.itemsize + v.nbytes <= self.nbytes
+        return v
+
+
+class DeviceView(DeviceArray):
+    """A non-owning window into a DeviceArray (freed with its parent)."""
+
+    def __init__(self, ctx: "Context", shape, dtype, ptr: int):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.ptr = ptr
+
+    def free(self):
+        self.ptr = None
 
 
 class AttnContext:
@@ -423,6 +445,18 @@ class Context:
         arr = (_vp * len(weights))(*[w.vp for w in weights])
         self._check(self.lib.iro_hip_dit_adaln_params(self.h, cond.vp, B, D, R, arr, n, out.vp),
                     "dit_adaln_params")
+
+    def linear_f32(self, x: DeviceArray, M: int, K: int, w: DeviceArray, N: int, bias, y):
+        """ops.c:221-234: y [M, N] = x @ w^T (+ bias), K-order chains."""
+        self._check(self.lib.iro_hip_linear_f32(self.h, x.vp, M, K, w.vp, N,
+                                                None if bias is None else bias.vp, y.vp),
+                    "linear_f32")
+
+    def rmsnorm_f32(self, x: DeviceArray, M: int, D: int, w: DeviceArray, eps: float,
+                    y: DeviceArray):
+        """ops.c:738-747: y = (x * inv) * w."""
+        self._check(self.lib.iro_hip_rmsnorm_f32(self.h, x.vp, M, D, w.vp, eps, y.vp),
+                    "rmsnorm_f32")
 
     def selfcheck_tanhf(self) -> int:
         d = C.c_ulonglong(0)

@@ -751,6 +751,37 @@ int orc_attention_core(const float *q, const float *k, const float *v, const flo
     return 0;
 }
 
+/* ---- fp32 linear and RMSNorm of the scalar build: ops.c:221-234, 738-747 */
+
+void orc_linear_f32(const float *x, int M, int K, const float *w, int N, const float *bias,
+                    float *y) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) {
+                const float p = x[(size_t)m * K + k] * w[(size_t)n * K + k];
+                acc = acc + p;
+            }
+            y[(size_t)m * N + n] = acc + (bias ? bias[n] : 0.0f);
+        }
+}
+
+void orc_rmsnorm(const float *x, int M, int D, const float *w, float eps, float *y) {
+    for (int m = 0; m < M; m++) {
+        const float *r = x + (size_t)m * D;
+        float ms = 0.0f;
+        for (int d = 0; d < D; d++) {
+            const float sq = r[d] * r[d];
+            ms = ms + sq;
+        }
+        const float inv = 1.0f / sqrtf(ms / (float)D + eps);
+        for (int d = 0; d < D; d++) {
+            const float t = r[d] * inv;
+            y[(size_t)m * D + d] = t * w[d];
+        }
+    }
+}
+
 /* ---- gated residual: dit.c:1013-1020, 1032-1039 ------------------------ */
 
 void orc_gated_residual(int conv, float *x, const float *gate,

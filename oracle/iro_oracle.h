@@ -93,6 +93,9 @@ void orc_fp32_digests(int threads, unsigned long long *sqrt_digest,
                       unsigned long long *recip_digest);
 void orc_adaln_apply(const float *x, const float *shift, const float *scale, int B, int S, int D,
                      float eps, float *h);
+void orc_linear_f32(const float *x, int M, int K, const float *w, int N, const float *bias,
+                    float *y);
+void orc_rmsnorm(const float *x, int M, int D, const float *w, float eps, float *y);
 float orc_expm1f(float x);
 float orc_tanhf(float x);
 long long orc_tanhf_mismatches(int threads);

@@ -66,6 +66,8 @@ class Oracle:
                                       _f32p]
         L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
         L.orc_rope_table.argtypes = [C.c_int, _f32p, _f32p]
+        L.orc_linear_f32.argtypes = [_f32p, C.c_int, C.c_int, _f32p, C.c_int, _f32p, _f32p]
+        L.orc_rmsnorm.argtypes = [_f32p, C.c_int, C.c_int, _f32p, C.c_float, _f32p]
         L.orc_tanhf.argtypes = [C.c_float]
         L.orc_tanhf.restype = C.c_float
         L.orc_tanhf_mismatches.argtypes = [C.c_int]
@@ -200,6 +202,24 @@ class Oracle:
         self.lib.orc_adaln_apply(_p(x, _f32p), _p(shift, _f32p), _p(scale, _f32p), B, S, D,
                                  eps, _p(h, _f32p))
         return h
+
+    def linear_f32(self, x, w, bias=None):
+        """ops.c:221-234: x [M, K] @ w [N, K]^T in K order, + bias (or + 0)."""
+        x, w = _f32(x), _f32(w)
+        M, K = x.shape
+        N = w.shape[0]
+        y = np.empty((M, N), np.float32)
+        self.lib.orc_linear_f32(_p(x, _f32p), M, K, _p(w, _f32p), N,
+                                None if bias is None else _p(_f32(bias), _f32p), _p(y, _f32p))
+        return y
+
+    def rmsnorm(self, x, w, eps):
+        """ops.c:738-747."""
+        x = _f32(x)
+        y = np.empty_like(x)
+        self.lib.orc_rmsnorm(_p(x, _f32p), x.shape[0], x.shape[1], _p(_f32(w), _f32p), eps,
+                             _p(y, _f32p))
+        return y
 
     def tanhf_mismatches(self):
         """Inputs (of all 2^32) where the fdlibm tanhf restatement differs from libm."""
@@ -389,6 +409,48 @@ class Reference:
             _p(mask, _u8p), B, S, mask.shape[-1], eps, int(bool(use_int8)), dims)
         assert rc == 0 and dims[0] == x.shape[-1], (rc, dims[0])
         return x
+
+    def linear_f32(self, x, w, bias=None):
+        """The scalar build's iro_linear (ops.c:236-254)."""
+        x, w = _f32(x), _f32(w)
+        M, K = x.shape
+        N = w.shape[0]
+        y = np.empty((M, N), np.float32)
+        self.lib.iro_linear.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
+        self.lib.iro_linear(_p(x, _f32p), _p(w, _f32p),
+                            None if bias is None else _p(_f32(bias), _f32p), _p(y, _f32p), M, K, N)
+        return y
+
+    def rmsnorm(self, x, w, eps):
+        """The scalar build's iro_rmsnorm (ops.c:738-747)."""
+        x = _f32(x)
+        y = np.empty_like(x)
+        self.lib.iro_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_float]
+        self.lib.iro_rmsnorm(_p(x, _f32p), _p(_f32(w), _f32p), _p(y, _f32p), x.shape[0],
+                             x.shape[1], eps)
+        return y
+
+    def dit_step(self, x, cond, head, ada, blk, ck, cv, mask, B, S, eps):
+        """The sampler's DiT evaluation (sampler.c:259-278): input projection
+        of x [S, 32], broadcast to B rows, len(ada) // 18 shared-context
+        blocks, output head; returns velocity [B*S, 32]."""
+        mask = np.ascontiguousarray(mask, np.uint8)
+        heads_ = [_f32(a) for a in head]
+        adas = [_f32(a) for a in ada]
+        blks = [_f32(a) for a in blk]
+        layers = len(adas) // 18
+        vel = np.empty((B * S, 32), np.float32)
+        self.lib.ref_dit_step.argtypes = [_f32p, _f32p, C.POINTER(_f32p), C.POINTER(_f32p),
+                                          C.POINTER(_f32p), C.c_int, _f32p, _f32p, _u8p,
+                                          C.c_int, C.c_int, C.c_int, C.c_float, _f32p]
+        self.lib.ref_dit_step.restype = C.c_int
+        rc = self.lib.ref_dit_step(
+            _p(_f32(x), _f32p), _p(_f32(cond), _f32p), (_f32p * 5)(*[_p(a, _f32p) for a in heads_]),
+            (_f32p * len(adas))(*[_p(a, _f32p) for a in adas]),
+            (_f32p * len(blks))(*[_p(a, _f32p) for a in blks]), layers, _p(_f32(ck), _f32p),
+            _p(_f32(cv), _f32p), _p(mask, _u8p), B, S, mask.shape[-1], eps, _p(vel, _f32p))
+        assert rc == 0
+        return vel
 
     def dit_adaln_full(self, eps, x, cond, w, B, S):
         """iro_dit_adaln (dit.c:614) with low-rank weights w (9 arrays, dit.h

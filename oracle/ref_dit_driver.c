@@ -104,3 +104,71 @@ int ref_dit_adaln_full(float eps, const float *x, const float *cond, const float
     IroAdaLN a = {w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7], w[8]};
     return iro_dit_adaln(&a, eps, x, cond, B, S, h, gate);
 }
+
+/* The DiT evaluation of one sampler step (sampler.c:259-278) over `layers`
+   layers with the shared context: iro_dit_input on one latent row set
+   x [S, LATENT_DIM] (dit.c:532-540), broadcast to B rows, then
+   iro_dit_block_shared_context per layer (dit.c:1063-1068), then
+   iro_dit_output (dit.c:1070-1089) into velocity [B*S, LATENT_DIM].  head:
+   in_w, in_b, out_norm, out_w, out_b; per layer l: ada[18 l ...] (attention
+   then MLP IroAdaLN arrays) and blk[10 l ...] (wq, wk, wv, wgate, wo,
+   q_norm, k_norm, w1, w3, w2), int8-quantized as iro_dit_int8_quantize does. */
+int ref_dit_step(const float *x, const float *cond, const float *const *head,
+                 const float *const *ada, const float *const *blk, int layers, const float *ck,
+                 const float *cv, const uint8_t *mask, int B, int S, int C, float eps,
+                 float *velocity) {
+    if (layers < 1 || layers > IRO_DIT_LAYERS) return -1;
+    IroDiT *d = calloc(1, sizeof(IroDiT));
+    IroDiTInt8 *q8 = calloc(1, sizeof(IroDiTInt8));
+    float *proj = malloc(sizeof(float) * (size_t)B * S * MODEL_DIM);
+    int rc = -1;
+    if (!d || !q8 || !proj) goto out;
+    d->in_w = head[0];
+    d->in_b = head[1];
+    d->out_norm = head[2];
+    d->out_w = head[3];
+    d->out_b = head[4];
+    d->norm_eps = eps;
+    for (int l = 0; l < layers; l++) {
+        const float *const *a = ada + 18 * l;
+        const float *const *w = blk + 10 * l;
+        IroAdaLN att = {a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7], a[8]};
+        IroAdaLN mlp = {a[9], a[10], a[11], a[12], a[13], a[14], a[15], a[16], a[17]};
+        d->attention_adaln[l] = att;
+        d->mlp_adaln[l] = mlp;
+        IroJointAttention at = {0};
+        at.wq = w[0];
+        at.wk = w[1];
+        at.wv = w[2];
+        at.gate = w[3];
+        at.wo = w[4];
+        at.q_norm = w[5];
+        at.k_norm = w[6];
+        d->attention[l] = at;
+        IroSwiGLU m = {w[7], w[9], w[8]};
+        d->mlp[l] = m;
+        IroDiTInt8Layer *q = &q8->layer[l];
+        if (iro_int8_weight_quantize(&q->wq, w[0], MODEL_DIM, MODEL_DIM) ||
+            iro_int8_weight_quantize(&q->wk, w[1], MODEL_DIM, MODEL_DIM) ||
+            iro_int8_weight_quantize(&q->wv, w[2], MODEL_DIM, MODEL_DIM) ||
+            iro_int8_weight_quantize(&q->gate, w[3], MODEL_DIM, MODEL_DIM) ||
+            iro_int8_weight_quantize(&q->wo, w[4], MODEL_DIM, MODEL_DIM) ||
+            iro_int8_weight_quantize(&q->w1, w[7], MLP_DIM, MODEL_DIM) ||
+            iro_int8_weight_quantize(&q->w3, w[8], MLP_DIM, MODEL_DIM) ||
+            iro_int8_weight_quantize(&q->w2, w[9], MODEL_DIM, MLP_DIM))
+            goto out;
+    }
+    d->int8 = q8;
+    if (iro_dit_input(d, x, 1, S, proj)) goto out;
+    for (int b = 1; b < B; b++)
+        memcpy(proj + (size_t)b * S * MODEL_DIM, proj, sizeof(float) * (size_t)S * MODEL_DIM);
+    for (int l = 0; l < layers; l++)
+        if (iro_dit_block_shared_context(d, l, proj, cond, ck, cv, mask, B, S, C)) goto out;
+    rc = iro_dit_output(d, proj, B, S, velocity);
+out:
+    if (q8) iro_dit_int8_free(q8);
+    free(q8);
+    free(d);
+    free(proj);
+    return rc;
+}

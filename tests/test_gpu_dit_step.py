@@ -1,0 +1,68 @@
+"""The DiT evaluation of one sampler step on the device against the
+reference's own (sampler.c:259-278).
+
+tests/golden/dit_step_ref.npz holds the velocity of the reference's scalar
+build (made by tests/golden/make_step_golden.py from oracle/_ref) over two
+layers with distinct weights: the input projection of one latent row set
+(iro_dit_input), broadcast to the three CFG rows, two
+iro_dit_block_shared_context calls with a masked shared context, and the
+output head (iro_dit_output: RMSNorm and the 1280 -> 32 projection).  The
+device runs iro_hip_linear_f32, two adaLN parameter / block forward pairs,
+iro_hip_rmsnorm_f32 and iro_hip_linear_f32, and must give the same bits.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import iro_hip
+from parity_util import assert_bits_equal
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+import make_step_golden as golden  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def test_dit_step_matches_reference(ctx_strict):
+    ctx = ctx_strict
+    g = np.load(os.path.join(HERE, "golden", "dit_step_ref.npz"))
+    x, cond, head, ada, blk, ck, cv, mask = golden.step_inputs()
+    assert golden.input_digest(x, cond, head, ada, blk, ck, cv) == str(g["inputs_sha256"]), \
+        "seeded inputs changed; regenerate the fixture"
+    B, S, D, H, R, LAT, L = golden.B, golden.S, golden.D, golden.H, golden.R, golden.LAT, \
+        golden.LAYERS
+    stack = iro_hip.DiTStack(ctx, L, D, H, 8)
+    actx = ctx.attn_context(mask, 1)
+    try:
+        zeros = ctx.to_device(np.zeros((6 * D, D), np.float32))
+        blkd = [ctx.to_device(a) for a in blk]
+        for l in range(L):
+            w = blkd[10 * l:10 * l + 10]
+            stack.set_block(l, zeros, w[0], w[1], w[2], w[3], w[4], w[7], w[8], w[9])
+        adad = [ctx.to_device(a) for a in ada]
+        headd = [ctx.to_device(a) for a in head]
+        condd, ckd, cvd = ctx.to_device(cond), ctx.to_device(ck), ctx.to_device(cv)
+        xd = ctx.to_device(x)
+        proj = ctx.empty((B * S, D), np.float32)
+        first = proj.view(0, (S, D))
+        ctx.linear_f32(xd, S, LAT, headd[0], D, headd[1], first)
+        for b in range(1, B):
+            ctx.copy(proj.view(b * S * D, (S, D)), first)
+        params = ctx.empty((2, 3, B, D), np.float32)
+        for l in range(L):
+            ctx.dit_adaln_params(condd, B, D, R, adad[18 * l:18 * l + 18], params)
+            w = blkd[10 * l:10 * l + 10]
+            stack.block_forward(l, proj, B, S, params.view(0, (3, B, D)),
+                                params.view(3 * B * D, (3, B, D)), w[5], w[6], golden.EPS, actx,
+                                ckd, cvd)
+        norm = ctx.empty((B * S, D), np.float32)
+        ctx.rmsnorm_f32(proj, B * S, D, headd[2], golden.EPS, norm)
+        vel = ctx.empty((B * S, LAT), np.float32)
+        ctx.linear_f32(norm, B * S, D, headd[3], LAT, headd[4], vel)
+        assert_bits_equal(vel.numpy(), g["velocity"], "velocity")
+    finally:
+        actx.destroy()
+        stack.destroy()

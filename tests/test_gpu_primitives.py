@@ -201,3 +201,31 @@ def test_tanhf_on_every_float(ctx_strict, oracle):
     2^32 inputs equals the hash of the oracle's restatement, which equals
     libm's tanhf on every input (tests/test_oracle_pins.py)."""
     assert ctx_strict.selfcheck_tanhf() == oracle.tanhf_digest()
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(750, 32, 1280, True), (48, 1280, 32, True),
+                                        (200, 512, 1280, False), (3, 100, 130, True),
+                                        (1, 1, 1, False)])
+def test_linear_f32(ctx, oracle, M, K, N, bias):
+    """ops.c:221-234 on the device: K-order chains, bit for bit against the
+    oracle (pinned against the scalar reference build); zero rows and -0
+    weights included."""
+    x, w = gauss(750, (M, K)), gauss(751, (N, K), 0.05)
+    x[0, :] = 0.0
+    if N > 1:
+        w[1, :] = -w[1, :] * 0.0
+    b = gauss(752, (N,), 0.1) if bias else None
+    y = ctx.empty((M, N), np.float32)
+    ctx.linear_f32(ctx.to_device(x), M, K, ctx.to_device(w), N,
+                   None if b is None else ctx.to_device(b), y)
+    assert_bits_equal(y.numpy(), oracle.linear_f32(x, w, b), "y")
+
+
+@pytest.mark.parametrize("M,D", [(60, 1280), (2250, 1024), (1, 64)])
+def test_rmsnorm_f32(ctx, oracle, M, D):
+    """ops.c:738-747 on the device, bit for bit against the oracle."""
+    x, w = gauss(753, (M, D)), gauss(754, (D,), 0.2) + 1.0
+    x[0] = 0.0
+    y = ctx.empty((M, D), np.float32)
+    ctx.rmsnorm_f32(ctx.to_device(x), M, D, ctx.to_device(w), 1e-6, y)
+    assert_bits_equal(y.numpy(), oracle.rmsnorm(x, w, 1e-6), "y")

@@ -410,3 +410,24 @@ def test_adaln_params_equal_reference_strict_build(oracle):
     assert _eq(gate, p[2])
     assert _eq(h, oracle.adaln_apply(x, p[0], p[1], B, S, eps))
     assert (np.abs(p[2]) == 1.0).any()
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(40, 32, 1280, True), (24, 1280, 32, True),
+                                        (17, 512, 1280, False), (3, 100, 130, True)])
+def test_linear_f32_equals_reference_strict_build(oracle, M, K, N, bias):
+    """The scalar build's iro_linear (ops.c:236-254 -> 221-234) equals the
+    oracle's K-order restatement bit for bit, with and without bias (the
+    no-bias form adds +0, which turns a -0 sum into +0)."""
+    x, w = gauss(740, (M, K)), gauss(741, (N, K), 0.05)
+    x[0, :] = 0.0
+    w[1, :] = -w[1, :] * 0.0  # -0 weights: the sums of row 0 are +0 - 0
+    b = gauss(742, (N,), 0.1) if bias else None
+    assert _eq(_ref("strict").linear_f32(x, w, b), oracle.linear_f32(x, w, b))
+
+
+def test_rmsnorm_equals_reference_strict_build(oracle):
+    """The scalar build's iro_rmsnorm (ops.c:738-747) equals the oracle's."""
+    x, w = gauss(743, (30, 1280)), gauss(744, (1280,), 0.2) + 1.0
+    x[0] = 0.0
+    x[1] *= 1e-20
+    assert _eq(_ref("strict").rmsnorm(x, w, 1e-6), oracle.rmsnorm(x, w, 1e-6))
