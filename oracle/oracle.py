@@ -452,6 +452,24 @@ class Reference:
         assert rc == 0
         return vel
 
+    def dit_context_kv(self, kind, x, wk, wv, k_norm, B, T, eps):
+        """iro_dit_text_kv (kind 0) / iro_dit_speaker_kv (kind 1), dit.c:708-726:
+        (k, v) [B*T, MODEL_DIM]."""
+        x = _f32(x)
+        D = wk.shape[0]
+        k = np.empty((B * T, D), np.float32)
+        v = np.empty((B * T, D), np.float32)
+        dim = C.c_int(0)
+        self.lib.ref_dit_context_kv.argtypes = [C.c_int, _f32p, _f32p, _f32p, _f32p, C.c_int,
+                                                C.c_int, C.c_float, _f32p, _f32p,
+                                                C.POINTER(C.c_int)]
+        self.lib.ref_dit_context_kv.restype = C.c_int
+        rc = self.lib.ref_dit_context_kv(kind, _p(x, _f32p), _p(_f32(wk), _f32p),
+                                         _p(_f32(wv), _f32p), _p(_f32(k_norm), _f32p), B, T, eps,
+                                         _p(k, _f32p), _p(v, _f32p), C.byref(dim))
+        assert rc == 0 and dim.value == x.shape[-1], (rc, dim.value)
+        return k, v
+
     def dit_adaln_full(self, eps, x, cond, w, B, S):
         """iro_dit_adaln (dit.c:614) with low-rank weights w (9 arrays, dit.h
         order): (h [B*S, D], gate [B, D])."""

@@ -172,3 +172,22 @@ out:
     free(proj);
     return rc;
 }
+
+/* iro_dit_text_kv / iro_dit_speaker_kv (dit.c:708-726): kind 0 = text
+   (TEXT_DIM inputs), 1 = speaker (SPEAKER_DIM). */
+int ref_dit_context_kv(int kind, const float *in, const float *wk, const float *wv,
+                       const float *k_norm, int B, int T, float eps, float *k, float *v,
+                       int *in_dim) {
+    IroJointAttention a = {0};
+    a.k_norm = k_norm;
+    if (kind == 0) {
+        a.wk_text = wk;
+        a.wv_text = wv;
+        *in_dim = TEXT_DIM;
+        return iro_dit_text_kv(&a, eps, in, B, T, k, v);
+    }
+    a.wk_speaker = wk;
+    a.wv_speaker = wv;
+    *in_dim = SPEAKER_DIM;
+    return iro_dit_speaker_kv(&a, eps, in, B, T, k, v);
+}

@@ -275,3 +275,24 @@ def test_attention_rejects_mismatched_context(ctx):
             ctx.dit_attention(actx, x, x, x, x, 3, 4, 64, x, x, x)
     finally:
         actx.destroy()
+
+
+@pytest.mark.parametrize("K,T", [(512, 120), (768, 16)])
+def test_context_kv(ctx, oracle, K, T):
+    """dit.c:708-726 on the device: iro_hip_linear_f32 for K and V (no bias),
+    iro_hip_dit_head_rmsnorm on K; bit for bit against the oracle's
+    composition (pinned against iro_dit_text_kv / iro_dit_speaker_kv of the
+    scalar reference build in tests/test_oracle_pins.py)."""
+    D, eps = 1280, 1e-6
+    x = gauss(770, (T, K))
+    wk, wv = gauss(771, (D, K), 0.05), gauss(772, (D, K), 0.05)
+    kn = gauss(773, (D,), 0.2) + 1.0
+    xd = ctx.to_device(x)
+    k, v = ctx.empty((T, D), np.float32), ctx.empty((T, D), np.float32)
+    ctx.linear_f32(xd, T, K, ctx.to_device(wk), D, None, k)
+    ctx.linear_f32(xd, T, K, ctx.to_device(wv), D, None, v)
+    ctx.dit_head_rmsnorm(k, ctx.to_device(kn), 1, T, D, eps)
+    want_k, _ = oracle.head_norm_rope(oracle.linear_f32(x, wk), kn, None, None, 1, T, eps,
+                                      rope=False)
+    assert_bits_equal(k.numpy(), want_k, "k")
+    assert_bits_equal(v.numpy(), oracle.linear_f32(x, wv), "v")

@@ -431,3 +431,18 @@ def test_rmsnorm_equals_reference_strict_build(oracle):
     x[0] = 0.0
     x[1] *= 1e-20
     assert _eq(_ref("strict").rmsnorm(x, w, 1e-6), oracle.rmsnorm(x, w, 1e-6))
+
+
+@pytest.mark.parametrize("kind,K", [(0, 512), (1, 768)])
+def test_context_kv_equals_reference_strict_build(oracle, kind, K):
+    """iro_dit_text_kv / iro_dit_speaker_kv (dit.c:708-726) of the strict
+    reference build equal the oracle's K-order linears (no bias) followed by
+    its head RMSNorm of the keys, bit for bit."""
+    D, B, T, eps = 1280, 1, 23, 1e-6
+    x = gauss(760 + kind, (B * T, K))
+    wk, wv = gauss(762, (D, K), 0.05), gauss(763, (D, K), 0.05)
+    kn = gauss(764, (D,), 0.2) + 1.0
+    k, v = _ref("strict").dit_context_kv(kind, x, wk, wv, kn, B, T, eps)
+    ok, _ = oracle.head_norm_rope(oracle.linear_f32(x, wk), kn, None, None, B, T, eps, rope=False)
+    assert _eq(k, ok)
+    assert _eq(v, oracle.linear_f32(x, wv))
