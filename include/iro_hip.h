@@ -235,6 +235,22 @@ int iro_hip_selfcheck_tanhf(IroHipContext *ctx, unsigned long long *digest);
 int iro_hip_linear_f32(IroHipContext *ctx, const float *x, int M, int K, const float *w, int N,
                        const float *bias, float *y);
 
+/* sampler.c:281-297, the CFG combine and Euler update of one sampler step,
+   on device memory: state [len] += guided * dt with guided = v + sum over
+   the unconditional rows k of scale_k * (v - v_k), where velocity holds
+   `batch` rows of len values (row 0 conditional; batch 1..4) and
+   text_row / speaker_row / caption_row are the unconditional rows (1 ..
+   batch-1, or -1 when that branch has no CFG row; sampler.c:133-139).  With
+   use_cfg == 0 (sampler.c:247-249) guided = v, batch may be 1 and the rows
+   (1..3 or -1) are not read.  dt = timestep_next -
+   timestep as sampler.c:243-246, 281 computes it.  Bit-identical to the
+   strict build, and to the fast-math build's reassociated form under
+   IRO_HIP_GCC_FASTMATH.  Replaces the host loop between iro_dit_output and
+   the next step of sample_euler, so the state stays on the device. */
+int iro_hip_euler_update(IroHipContext *ctx, float *state, const float *velocity, int len,
+                         int batch, int use_cfg, int text_row, int speaker_row, int caption_row,
+                         float scale_text, float scale_speaker, float scale_caption, float dt);
+
 /* ops.c:738-747, iro_rmsnorm: y = (x * inv) * w[d], inv = 1 / sqrtf(mean of
    x^2 in index order + eps), rows of D (D % 4 == 0, D <= 2048, 16-byte
    aligned).  Bit-identical to the scalar build (the DiT's output norm,

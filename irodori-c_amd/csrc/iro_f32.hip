@@ -80,6 +80,49 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
     }
 }
 
+// sampler.c:281-297, the CFG combine and Euler update after the DiT
+// velocity of a step: guided = v + sum_k s_k * (v - v_k) over the active
+// unconditional rows k (text, speaker, caption order), state += guided * dt.
+// The strict build rounds every op in source order (this file is compiled
+// with -ffp-contract=off); the fast-math build's GCC reassociates the CFG
+// sum and fuses the products (pinned against its traces): 1 term
+// fma(s0, d0, v); 2 terms v + fma(s1, d1, s0 d0); 3 terms
+// fma(s2, d2, v) + fma(s1, d1, s0 d0); then state = fma(guided, dt, state).
+struct EulerTerms {
+    int n;                // active terms, 0..3
+    int off[3];           // element offset of each term's row: row * len
+    float s[3];
+};
+
+template <int CONV>
+__global__ __launch_bounds__(256) void euler_update_kernel(float *__restrict__ state,
+                                                           const float *__restrict__ vel,
+                                                           long long len, EulerTerms t, float dt) {
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < len; i += stride) {
+        const float v = vel[i];
+        float d[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            if (k < t.n) d[k] = v - vel[t.off[k] + i];
+        float g = v;
+        if (CONV == 0) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                if (k < t.n) g = g + t.s[k] * d[k];
+            state[i] = state[i] + g * dt;
+        } else {
+            if (t.n == 1)
+                g = __builtin_fmaf(t.s[0], d[0], v);
+            else if (t.n == 2)
+                g = v + __builtin_fmaf(t.s[1], d[1], t.s[0] * d[0]);
+            else if (t.n == 3)
+                g = __builtin_fmaf(t.s[2], d[2], v) + __builtin_fmaf(t.s[1], d[1], t.s[0] * d[0]);
+            state[i] = __builtin_fmaf(g, dt, state[i]);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace iro
 
@@ -96,6 +139,39 @@ int iro_hip_linear_f32(IroHipContext *ctx, const float *x, int M, int K, const f
         return set_error(ctx, "linear_f32: too many rows");
     hipLaunchKernelGGL(linear_f32_kernel, dim3((N + kLN - 1) / kLN, (M + kLM - 1) / kLM),
                        dim3(256), 0, ctx->stream, x, M, K, w, N, bias, y);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
+int iro_hip_euler_update(IroHipContext *ctx, float *state, const float *velocity, int len,
+                         int batch, int use_cfg, int text_row, int speaker_row, int caption_row,
+                         float scale_text, float scale_speaker, float scale_caption, float dt) {
+    if (!ctx || len < 0 || batch < 1 || batch > 4 || (len && (!state || !velocity)))
+        return set_error(ctx, "euler_update: invalid arguments");
+    const int rows[3] = {text_row, speaker_row, caption_row};
+    const float scales[3] = {scale_text, scale_speaker, scale_caption};
+    EulerTerms t{};
+    for (int k = 0; k < 3; ++k) {
+        // Rows index the velocity only on CFG steps; a plain step (batch 1)
+        // keeps the sampler's row numbers unused.
+        if (rows[k] < -1 || rows[k] == 0 || rows[k] > 3 || (use_cfg && rows[k] >= batch))
+            return set_error(ctx, "euler_update: CFG row %d outside 1..%d", rows[k],
+                             use_cfg ? batch - 1 : 3);
+        if (use_cfg && rows[k] > 0) {
+            t.off[t.n] = rows[k] * len;
+            t.s[t.n] = scales[k];
+            ++t.n;
+        }
+    }
+    if ((long long)batch * len > INT32_MAX) return set_error(ctx, "euler_update: too many values");
+    if (len == 0) return 0;
+    const unsigned grid = (unsigned)((len + 255) / 256 < 1024 ? (len + 255) / 256 : 1024);
+    if (ctx->convention == IRO_HIP_GCC_FASTMATH)
+        hipLaunchKernelGGL(euler_update_kernel<1>, dim3(grid), dim3(256), 0, ctx->stream, state,
+                           velocity, (long long)len, t, dt);
+    else
+        hipLaunchKernelGGL(euler_update_kernel<0>, dim3(grid), dim3(256), 0, ctx->stream, state,
+                           velocity, (long long)len, t, dt);
     IRO_HIP_CHECK_LAUNCH(ctx);
     return 0;
 }

@@ -114,6 +114,8 @@ def load() -> C.CDLL:
         "iro_hip_dit_adaln_params": ([_vp, _vp, _i, _i, _i, C.POINTER(_vp), _i, _vp], _i),
         "iro_hip_linear_f32": ([_vp, _vp, _i, _i, _vp, _i, _vp, _vp], _i),
         "iro_hip_rmsnorm_f32": ([_vp, _vp, _i, _i, _vp, C.c_float, _vp], _i),
+        "iro_hip_euler_update": ([_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, C.c_float, C.c_float,
+                                  C.c_float, C.c_float], _i),
         "iro_hip_selfcheck_tanhf": ([_vp, C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_attn_context_destroy": ([_vp], None),
         "iro_hip_dit_attention": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp], _i),
@@ -457,6 +459,16 @@ class Context:
         """ops.c:738-747: y = (x * inv) * w."""
         self._check(self.lib.iro_hip_rmsnorm_f32(self.h, x.vp, M, D, w.vp, eps, y.vp),
                     "rmsnorm_f32")
+
+    def euler_update(self, state: DeviceArray, velocity: DeviceArray, length: int, batch: int,
+                     use_cfg: bool, rows, scales, dt: float):
+        """sampler.c:281-297: state [length] += guided * dt in place; velocity
+        [batch, length]; rows = (text, speaker, caption) unconditional rows,
+        -1 when absent; scales the three CFG scales."""
+        self._check(self.lib.iro_hip_euler_update(self.h, state.vp, velocity.vp, length, batch,
+                                                  int(bool(use_cfg)), *[int(r) for r in rows],
+                                                  *[float(x) for x in scales], float(dt)),
+                    "euler_update")
 
     def selfcheck_tanhf(self) -> int:
         d = C.c_ulonglong(0)

@@ -1033,3 +1033,39 @@ int orc_conv1x1_skip_int8(int conv, const float *hidden, const float *skip,
     free(q1); free(q2); free(s1); free(s2); free(z1); free(z2); free(rem); free(work);
     return ok ? 0 : -1;
 }
+
+/* sampler.c:281-297 (see iro_oracle.h). */
+void orc_euler_update(int conv, float *state, const float *velocity, size_t n, int use_cfg,
+                      int text_row, int speaker_row, int caption_row, float scale_text,
+                      float scale_speaker, float scale_caption, float dt) {
+    const int rows[3] = {text_row, speaker_row, caption_row};
+    const float scales[3] = {scale_text, scale_speaker, scale_caption};
+    int act_row[3];
+    float act_scale[3];
+    int terms = 0;
+    for (int k = 0; k < 3; k++)
+        if (use_cfg && rows[k] >= 0) {
+            act_row[terms] = rows[k];
+            act_scale[terms] = scales[k];
+            terms++;
+        }
+    for (size_t i = 0; i < n; i++) {
+        const float v = velocity[i];
+        float d[3];
+        for (int k = 0; k < terms; k++) d[k] = v - velocity[(size_t)act_row[k] * n + i];
+        if (conv != ORC_GCC_FASTMATH) {
+            float guided = v;
+            for (int k = 0; k < terms; k++) guided += act_scale[k] * d[k];
+            state[i] += guided * dt;
+            continue;
+        }
+        float guided = v;
+        if (terms == 1)
+            guided = fmaf(act_scale[0], d[0], v);
+        else if (terms == 2)
+            guided = v + fmaf(act_scale[1], d[1], act_scale[0] * d[0]);
+        else if (terms == 3)
+            guided = fmaf(act_scale[2], d[2], v) + fmaf(act_scale[1], d[1], act_scale[0] * d[0]);
+        state[i] = fmaf(guided, dt, state[i]);
+    }
+}

@@ -157,6 +157,19 @@ int orc_conv1x1_skip_int8(int conv, const float *hidden, const float *skip,
                           const float *bias, int residual, float *output,
                           int threads);
 
+/* sampler.c:281-297: the CFG combine and Euler update of one sampler step.
+   velocity holds the step's CFG rows of n values each (row 0 conditional);
+   text_row / speaker_row / caption_row are the unconditional rows (-1 when
+   that branch has no CFG row) and apply only when use_cfg.  Strict: every
+   op rounds in source order.  Fast: the CFG terms p_k = s_k * (v - v_k)
+   (active terms in text, speaker, caption order) are combined as GCC 11
+   reassociates them under -ffast-math (pinned against the fast build's
+   traces): 1 term fma(s0, d0, v); 2 terms v + fma(s1, d1, p0); 3 terms
+   fma(s2, d2, v) + fma(s1, d1, p0); then state = fma(guided, dt, state). */
+void orc_euler_update(int conv, float *state, const float *velocity, size_t n, int use_cfg,
+                      int text_row, int speaker_row, int caption_row, float scale_text,
+                      float scale_speaker, float scale_caption, float dt);
+
 /* dacvae.c:340-348 (iro_conv1d_output_length). */
 int orc_conv1d_output_length(int T, int kernel, int stride, int dilation,
                              int padding);

@@ -67,6 +67,9 @@ class Oracle:
         L.orc_gated_residual.argtypes = [C.c_int, _f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int]
         L.orc_rope_table.argtypes = [C.c_int, _f32p, _f32p]
         L.orc_linear_f32.argtypes = [_f32p, C.c_int, C.c_int, _f32p, C.c_int, _f32p, _f32p]
+        L.orc_euler_update.argtypes = [C.c_int, _f32p, _f32p, C.c_size_t, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_float, C.c_float, C.c_float,
+                                       C.c_float]
         L.orc_rmsnorm.argtypes = [_f32p, C.c_int, C.c_int, _f32p, C.c_float, _f32p]
         L.orc_tanhf.argtypes = [C.c_float]
         L.orc_tanhf.restype = C.c_float
@@ -183,6 +186,15 @@ class Oracle:
         g = _f32(g)
         self.lib.orc_silu_mul(_p(a, _f32p), _p(g, _f32p), a.size)
         return a
+
+    def euler_update(self, conv, state, velocity, use_cfg, rows, scales, dt):
+        """sampler.c:281-297: returns the next state; velocity [batch, n],
+        rows = (text_row, speaker_row, caption_row) with -1 for absent."""
+        st = np.array(state, np.float32, copy=True).reshape(-1)
+        vel = _f32(velocity)
+        self.lib.orc_euler_update(conv, _p(st, _f32p), _p(vel, _f32p), st.size, int(use_cfg),
+                                  *[int(r) for r in rows], *[float(x) for x in scales], float(dt))
+        return st
 
     def expf_mismatches(self):
         return self.lib.orc_expf_mismatches(self.threads)
@@ -451,6 +463,42 @@ class Reference:
             _p(_f32(cv), _f32p), _p(mask, _u8p), B, S, mask.shape[-1], eps, _p(vel, _f32p))
         assert rc == 0
         return vel
+
+    def sample_euler(self, pool, eps, text, text_mask, speaker, caption, noise, cfg):
+        """The reference's whole Euler sampler (sampler.c:101-324) on a DiT
+        whose every weight aliases `pool` (at least 3*1280*1280 floats),
+        with a trace of every step.  cfg = (steps, init_scale, cfg_scale_text,
+        cfg_scale_speaker, cfg_scale_caption, cfg_min_t, cfg_max_t).  Returns
+        (output [S*32], x_t [steps, 4, S*32], velocity [steps, 4, S*32],
+        batch [steps], timestep [steps]); row 0 of x_t[s] is the state that
+        enters step s."""
+        noise = _f32(noise)
+        S = noise.shape[0]
+        steps = int(cfg[0])
+        n = S * 32
+        cfgv = np.asarray(cfg, np.float32)
+        out = np.zeros(n, np.float32)
+        xt = np.zeros((steps, 4, n), np.float32)
+        vel = np.zeros((steps, 4, n), np.float32)
+        bt = np.zeros(steps, np.int32)
+        ts = np.zeros(steps, np.float32)
+        L = self.lib
+        L.ref_sample_euler.argtypes = [_f32p, C.c_float, _f32p, _u8p, C.c_int, _f32p, C.c_int,
+                                       _f32p, C.c_int, _f32p, C.c_int, _f32p, _f32p, _f32p,
+                                       _f32p, _i32p, _f32p]
+        L.ref_sample_euler.restype = C.c_int
+        pool = _f32(pool)
+        assert pool.size >= 3 * 1280 * 1280
+        text, caption_ = _f32(text), None if caption is None else _f32(caption)
+        speaker_ = None if speaker is None else _f32(speaker)
+        rc = L.ref_sample_euler(
+            _p(pool, _f32p), eps, _p(text, _f32p), _p(np.ascontiguousarray(text_mask, np.uint8), _u8p),
+            text.shape[0], _p(speaker_, _f32p), 0 if speaker_ is None else speaker_.shape[0],
+            _p(caption_, _f32p), 0 if caption_ is None else caption_.shape[0], _p(noise, _f32p),
+            S, _p(cfgv, _f32p), _p(out, _f32p), _p(xt, _f32p), _p(vel, _f32p), _p(bt, _i32p),
+            _p(ts, _f32p))
+        assert rc == 0, "ref_sample_euler failed"
+        return out, xt, vel, bt, ts
 
     def dit_context_kv(self, kind, x, wk, wv, k_norm, B, T, eps):
         """iro_dit_text_kv (kind 0) / iro_dit_speaker_kv (kind 1), dit.c:708-726:
