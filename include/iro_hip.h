@@ -363,6 +363,50 @@ int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int 
                                     const IroHipAttnContext *actx, const float *context_k,
                                     const float *context_v);
 
+/* The fp32 parameters of one DiT layer that a sampler step reads besides the
+   stack's int8 weights (dit.h:11-35): the attention then the MLP IroAdaLN
+   (shift_down, shift_up, shift_bias, scale_down, scale_up, scale_bias,
+   gate_down, gate_up, gate_bias each), the head norms [D], and the layer's
+   cached context keys and values ([C, D] shared by the CFG rows, or
+   [B*C, D] per row, as the attention context says; sampler.c:215-236 fills
+   them once per utterance).  Device arrays, borrowed until the layer is set
+   again or the stack is destroyed. */
+typedef struct {
+    const float *adaln[18];
+    const float *q_norm, *k_norm;
+    const float *context_k, *context_v;
+} IroHipDiTLayerF32;
+
+/* The DiT's input and output heads (dit.c:146-150: in_proj [D, latent] and
+   bias [D], out_norm [D], out_proj [latent, D] and bias [latent]), the adaLN
+   rank (ADALN_RANK, dit.c:16) and the norm epsilon; device arrays, borrowed. */
+typedef struct {
+    const float *in_w, *in_b, *out_norm, *out_w, *out_b;
+    int latent;
+    int rank;
+    float eps;
+} IroHipDiTHead;
+
+int iro_hip_dit_stack_set_layer_f32(IroHipDiTStack *s, int layer, const IroHipDiTLayerF32 *p);
+int iro_hip_dit_stack_set_head(IroHipDiTStack *s, const IroHipDiTHead *head);
+
+/* One Euler step of sample_euler (sampler.c:259-297) on the device, with
+   every layer's weights set: the input projection of state [S, latent]
+   (iro_dit_input), broadcast to the `batch` CFG rows, every layer's adaLN
+   parameters from cond [batch, 3D] (the caller uploads iro_dit_condition's
+   row, broadcast, as sampler.c:262-266 does) and block forward with the
+   context of actx (iro_dit_block_shared_context), the output RMSNorm and
+   projection into velocity [batch*S, latent] (iro_dit_output; the trace
+   callback's velocity), then the CFG combine and Euler update of state in
+   place (iro_hip_euler_update's arguments).  Each part is bit-identical to
+   the reference's scalar build, so the step is too; only cond crosses PCIe
+   per step. */
+int iro_hip_dit_sampler_step(IroHipDiTStack *s, float *state, const float *cond, int batch,
+                             int S, const IroHipAttnContext *actx, int use_cfg, int text_row,
+                             int speaker_row, int caption_row, float scale_text,
+                             float scale_speaker, float scale_caption, float dt,
+                             float *velocity);
+
 /* ---- DACVAE int8 Conv1d (dacvae.c:543-688, no snake) ------------------- */
 
 /* input [T, C] fp32 time-major, weight [N, kernel*C] (tap-major K as

@@ -606,6 +606,11 @@ struct IroHipDiTStack {
     float *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *hidden = nullptr;
     float *mod = nullptr;
     float *h = nullptr, *mix = nullptr;  // block forward: normed input, attention output
+    float *proj = nullptr, *params = nullptr;  // sampler step: hidden rows, adaLN parameters
+    std::vector<IroHipDiTLayerF32> f32;        // sampler step: per-layer fp32 parameters
+    std::vector<char> f32_set;
+    IroHipDiTHead head{};
+    int head_set = 0;
     // graph of the last step's launches
     int use_graph = 1;
     hipGraph_t graph = nullptr;
@@ -622,7 +627,8 @@ using namespace iro;
 namespace {
 
 void stack_free_acts(IroHipDiTStack *s) {
-    for (float **p : {&s->q, &s->k, &s->v, &s->g, &s->hidden, &s->mod, &s->h, &s->mix}) {
+    for (float **p : {&s->q, &s->k, &s->v, &s->g, &s->hidden, &s->mod, &s->h, &s->mix,
+                      &s->proj, &s->params}) {
         if (*p) (void)hipFree(*p);
         *p = nullptr;
     }
@@ -650,6 +656,8 @@ int stack_reserve(IroHipDiTStack *s, int M, int B) {
     if (e == hipSuccess) e = hipMalloc(&s->g, md);
     if (e == hipSuccess) e = hipMalloc(&s->h, md);
     if (e == hipSuccess) e = hipMalloc(&s->mix, md);
+    if (e == hipSuccess) e = hipMalloc(&s->proj, md);
+    if (e == hipSuccess) e = hipMalloc(&s->params, sizeof(float) * 6 * (size_t)B * s->D);
     if (e == hipSuccess) e = hipMalloc(&s->hidden, sizeof(float) * (size_t)M * s->H);
     if (e == hipSuccess)
         e = hipMalloc(&s->mod, sizeof(float) * (size_t)B * s->blocks * s->ada_np);
@@ -904,6 +912,8 @@ int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int r
         return -1;
     }
     s->ada_set.assign(blocks, 0);
+    s->f32.assign(blocks, IroHipDiTLayerF32{});
+    s->f32_set.assign(blocks, 0);
     s->qkvg.assign(blocks, nullptr);
     s->wo.assign(blocks, nullptr);
     s->w13.assign(blocks, nullptr);
@@ -1033,6 +1043,70 @@ int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int 
     if (iro_hip_dit_adaln_apply(ctx, x, B, S, D, ada_mlp, ada_mlp + BD, eps, s->h)) return -1;
     if (swiglu_impl(ctx, s->h, M, s->w13[block], s->w2[block], rm & 4, rm & 8, s->hidden, nullptr,
                     x, ada_mlp + 2 * BD, D, S))
+        return -1;
+    return ctx->has_err ? -1 : 0;
+}
+
+int iro_hip_dit_stack_set_layer_f32(IroHipDiTStack *s, int layer, const IroHipDiTLayerF32 *p) {
+    if (!s || !p || layer < 0 || layer >= s->blocks)
+        return set_error(s ? s->ctx : nullptr, "dit_stack_set_layer_f32: invalid arguments");
+    for (int i = 0; i < 18; ++i)
+        if (!p->adaln[i]) return set_error(s->ctx, "dit_stack_set_layer_f32: adaLN array %d is NULL", i);
+    if (!p->q_norm || !p->k_norm || !p->context_k || !p->context_v)
+        return set_error(s->ctx, "dit_stack_set_layer_f32: NULL norm or context array");
+    s->f32[layer] = *p;
+    s->f32_set[layer] = 1;
+    return 0;
+}
+
+int iro_hip_dit_stack_set_head(IroHipDiTStack *s, const IroHipDiTHead *head) {
+    if (!s || !head || !head->in_w || !head->in_b || !head->out_norm || !head->out_w ||
+        !head->out_b || head->latent <= 0 || head->rank <= 0 || !(head->eps >= 0.0f))
+        return set_error(s ? s->ctx : nullptr, "dit_stack_set_head: invalid arguments");
+    s->head = *head;
+    s->head_set = 1;
+    return 0;
+}
+
+// sampler.c:259-297 with the reference's calls in its order: iro_dit_input
+// (dit.c:532-540) on the state, memcpy to the other CFG rows, per layer
+// dit_adaln x 2 (dit.c:580-588) and the block (dit.c:984-1040) with the
+// shared context, iro_dit_output (dit.c:1070-1089), the CFG / Euler update.
+int iro_hip_dit_sampler_step(IroHipDiTStack *s, float *state, const float *cond, int batch,
+                             int S, const IroHipAttnContext *actx, int use_cfg, int text_row,
+                             int speaker_row, int caption_row, float scale_text,
+                             float scale_speaker, float scale_caption, float dt,
+                             float *velocity) {
+    if (!s || !state || !cond || !actx || !velocity || batch < 1 || batch > 4 || S <= 0)
+        return set_error(s ? s->ctx : nullptr, "dit_sampler_step: invalid arguments");
+    IroHipContext *ctx = s->ctx;
+    if (!s->head_set) return set_error(ctx, "dit_sampler_step: no head set");
+    for (int l = 0; l < s->blocks; ++l)
+        if (!s->ada_set[l] || !s->f32_set[l])
+            return set_error(ctx, "dit_sampler_step: layer %d is not fully set", l);
+    const IroHipDiTHead &hd = s->head;
+    const int D = s->D, M = batch * S;
+    if (stack_reserve(s, M, batch)) return -1;
+    if (iro_hip_linear_f32(ctx, state, S, hd.latent, hd.in_w, D, hd.in_b, s->proj)) return -1;
+    const size_t rows = sizeof(float) * (size_t)S * D;
+    for (int b = 1; b < batch; ++b)
+        IRO_HIP_TRY(ctx, hipMemcpyAsync(s->proj + (size_t)b * S * D, s->proj, rows,
+                                        hipMemcpyDeviceToDevice, ctx->stream));
+    const size_t BD = (size_t)batch * D;
+    for (int l = 0; l < s->blocks; ++l) {
+        const IroHipDiTLayerF32 &p = s->f32[l];
+        if (iro_hip_dit_adaln_params(ctx, cond, batch, D, hd.rank, p.adaln, 2, s->params))
+            return -1;
+        if (iro_hip_dit_stack_block_forward(s, l, s->proj, batch, S, s->params,
+                                            s->params + 3 * BD, p.q_norm, p.k_norm, hd.eps, actx,
+                                            p.context_k, p.context_v))
+            return -1;
+    }
+    if (iro_hip_rmsnorm_f32(ctx, s->proj, M, D, hd.out_norm, hd.eps, s->h)) return -1;
+    if (iro_hip_linear_f32(ctx, s->h, M, D, hd.out_w, hd.latent, hd.out_b, velocity)) return -1;
+    if (iro_hip_euler_update(ctx, state, velocity, S * hd.latent, batch, use_cfg, text_row,
+                             speaker_row, caption_row, scale_text, scale_speaker, scale_caption,
+                             dt))
         return -1;
     return ctx->has_err ? -1 : 0;
 }

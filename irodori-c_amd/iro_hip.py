@@ -21,6 +21,18 @@ STRICT, GCC_FASTMATH = 0, 1
 
 _vp = C.c_void_p
 _i = C.c_int
+
+
+class DiTLayerF32(C.Structure):
+    """IroHipDiTLayerF32: per-layer fp32 parameters of a sampler step."""
+    _fields_ = [("adaln", _vp * 18), ("q_norm", _vp), ("k_norm", _vp), ("context_k", _vp),
+                ("context_v", _vp)]
+
+
+class DiTHead(C.Structure):
+    """IroHipDiTHead: input / output heads, adaLN rank, norm epsilon."""
+    _fields_ = [("in_w", _vp), ("in_b", _vp), ("out_norm", _vp), ("out_w", _vp), ("out_b", _vp),
+                ("latent", C.c_int), ("rank", C.c_int), ("eps", C.c_float)]
 _lib = None
 
 
@@ -105,6 +117,10 @@ def load() -> C.CDLL:
         "iro_hip_dit_stack_destroy": ([_vp], None),
         "iro_hip_selfcheck_silu": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_stack_use_graph": ([_vp, _i], _i),
+        "iro_hip_dit_stack_set_layer_f32": ([_vp, _i, C.POINTER(DiTLayerF32)], _i),
+        "iro_hip_dit_stack_set_head": ([_vp, C.POINTER(DiTHead)], _i),
+        "iro_hip_dit_sampler_step": ([_vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, C.c_float,
+                                      C.c_float, C.c_float, C.c_float, _vp], _i),
         "iro_hip_dit_stack_block_forward": ([_vp, _i, _vp, _i, _i, _vp, _vp, _vp, _vp, C.c_float,
                                              _vp, _vp, _vp], _i),
         "iro_hip_dit_adaln_apply": ([_vp, _vp, _i, _i, _i, _vp, _vp, C.c_float, _vp], _i),
@@ -650,6 +666,28 @@ class DiTStack:
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_block_forward(
             self.h, block, x.vp, B, S, ada_attn.vp, ada_mlp.vp, q_norm.vp, k_norm.vp, eps,
             actx.h, context_k.vp, context_v.vp), "dit_block_forward")
+
+    def set_layer_f32(self, layer: int, adaln, q_norm, k_norm, context_k, context_v):
+        """Borrow layer's 18 adaLN arrays, head norms and cached context K/V."""
+        p = DiTLayerF32((_vp * 18)(*[a.vp for a in adaln]), q_norm.vp, k_norm.vp, context_k.vp,
+                        context_v.vp)
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_set_layer_f32(self.h, layer, C.byref(p)),
+                        "dit_stack_set_layer_f32")
+
+    def set_head(self, in_w, in_b, out_norm, out_w, out_b, latent: int, rank: int, eps: float):
+        h = DiTHead(in_w.vp, in_b.vp, out_norm.vp, out_w.vp, out_b.vp, latent, rank, eps)
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_set_head(self.h, C.byref(h)),
+                        "dit_stack_set_head")
+
+    def sampler_step(self, state: DeviceArray, cond: DeviceArray, batch: int, S: int,
+                     actx: "AttnContext", use_cfg: bool, rows, scales, dt: float,
+                     velocity: DeviceArray):
+        """sampler.c:259-297: one Euler step; state [S, latent] updated in place,
+        velocity [batch*S, latent] receives the DiT output."""
+        self.ctx._check(self.ctx.lib.iro_hip_dit_sampler_step(
+            self.h, state.vp, cond.vp, batch, S, actx.h, int(bool(use_cfg)),
+            *[int(r) for r in rows], *[float(x) for x in scales], float(dt), velocity.vp),
+            "dit_sampler_step")
 
     def use_graph(self, on: bool):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_use_graph(self.h, int(bool(on))),
