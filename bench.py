@@ -22,7 +22,8 @@ M = 2250 rows (one call per step), `--workload qknorm` the per-head RMSNorm
 and half-RoPE of q and k, `--workload attention` the attention core (scores,
 softmax, P@V, gate) with a context of up to 300 rows, `--workload block` one
 whole DiT block (adaLN parameters from cond, every fp32 and int8 step) at the
-reference model's dimensions; `--workload weights` the int8 weight build
+reference model's dimensions, `--workload sampler-step` one whole Euler step
+of the sampler (12 such layers, heads, CFG / Euler update); `--workload weights` the int8 weight build
 from a safetensors checkpoint.
 
 Prints one JSON line on stdout; diagnostics go to stderr.
@@ -603,6 +604,107 @@ def block_main(args):
     print(json.dumps(out), flush=True)
 
 
+def sampler_step_main(args):
+    """One Euler step of the sampler (sampler.c:259-297) at the reference
+    model's dimensions (12 layers, hidden 1280, 20 heads, MLP 3680, adaLN
+    rank 192) through iro_hip_dit_sampler_step: input projection of the
+    state [750, 32], broadcast to 3 CFG rows, every layer's adaLN parameters
+    and block (300 shared context rows; masks keep 250, 150, 200), output
+    head, CFG combine and Euler update.  Each layer holds distinct weights
+    (shifted copies of one seeded set).  Bit-identical to the reference's
+    step (tests/test_gpu_dit_step.py).  No CPU baseline: the reference's
+    scalar build needs minutes for one step at this size (the block
+    workload times it per block)."""
+    D, H, R, C, L, LAT = 1280, 3680, 192, 300, args.blocks, 32
+    B, S = min(args.batch, 3), args.frames
+    keep = [250, 150, 200][:B]
+    mask = np.zeros((B, C), np.uint8)
+    for b in range(B):
+        mask[b, :keep[b]] = 1
+    ctx = iro_hip.Context(0, iro_hip.STRICT)
+    log("backend:", ctx.backend())
+    stack = iro_hip.DiTStack(ctx, L, D, H, args.residual_mask)
+    w = [gauss(100 + i, (D, D), 0.03) for i in range(5)]
+    wn = [gauss(105, (D,), 0.2) + 1.0, gauss(106, (D,), 0.2) + 1.0]
+    wm = [gauss(107, (H, D), 0.03), gauss(108, (H, D), 0.03), gauss(109, (D, H), 0.02)]
+    ada = []
+    for i in range(6):
+        ada += [gauss(110 + 3 * i, (R, D), 0.05), gauss(111 + 3 * i, (D, R), 0.05),
+                gauss(112 + 3 * i, (D,), 0.1)]
+    zeros = ctx.to_device(np.zeros((6 * D, D), np.float32))
+    ck, cv = ctx.to_device(gauss(122, (C, D))), ctx.to_device(gauss(123, (C, D)))
+    keepalive = []
+    for l in range(L):
+        wl = [ctx.to_device(np.roll(a, l, axis=-1)) for a in w + wn + wm]
+        stack.set_block(l, zeros, *wl[:5], *wl[7:])
+        adl = [ctx.to_device(np.roll(a, l, axis=-1)) for a in ada]
+        stack.set_layer_f32(l, adl, wl[5], wl[6], ck, cv)
+        keepalive += wl + adl
+    head = [gauss(130, (D, LAT), 0.2), gauss(131, (D,), 0.1), gauss(132, (D,), 0.2) + 1.0,
+            gauss(133, (LAT, D), 0.03), gauss(134, (LAT,), 0.1)]
+    headd = [ctx.to_device(a) for a in head]
+    stack.set_head(*headd, LAT, R, 1e-6)
+    actx = ctx.attn_context(mask, 1)
+    cond = ctx.to_device(np.repeat(gauss(121, (1, 3 * D), 0.5), B, axis=0))
+    state = ctx.to_device(gauss(120, (S, LAT)))
+    vel = ctx.empty((B * S, LAT), np.float32)
+    rows = (1, 2 if B > 2 else -1, -1) if B > 1 else (-1, -1, -1)
+    scales = (1.5, 0.75 if B > 2 else 0.0, 0.0)
+
+    def step():
+        stack.sampler_step(state, cond, B, S, actx, B > 1, rows, scales, -1.0 / 8, vel)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    t0 = time.perf_counter()
+    ctx.record(e0)
+    for _ in range(args.steps):
+        step()
+    ctx.record(e1)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.elapsed_ms(e0, e1) / args.steps
+    finite = bool(np.isfinite(state.numpy()).all())
+    ctx.profile(True)
+    for _ in range(args.profile_steps):
+        step()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    kernels = log_profile(prof)
+    actx.destroy()
+    stack.destroy()
+    ctx.close()
+    rate = B * S / (ev_ms * 1e-3)
+    log(f"sampler step: {ev_ms:.3f} ms/step events, {rate:.0f} tokens/s")
+    out = {
+        "metric": "Euler sampler step latency (ms) and tokens/s, DiT hidden 1280 x 12 layers, 1 GPU",
+        "value": round(rate, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ev_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32+int8",
+        "data": "synthetic (seeded Irwin-Hall Gaussian activations and random-init weights)",
+        "config": {"workload": f"one Euler sampler step: input projection, {L} DiT layers "
+                               f"(adaLN parameters + block), output head, CFG / Euler update; "
+                               f"{B} CFG rows x {S} latent frames, {C} shared context rows "
+                               f"(kept {keep}), int8 QKVG/Wo/W1W3/W2",
+                   "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+                   "residual_mask": args.residual_mask, "parallelism": "single GPU"},
+        "roofline": None,
+        "kernels": kernels,
+        "cpu_baseline": None,
+        "state_finite": finite,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def weights_main(args):
     """The weight source (safetensors.c:302-530, generate.c:526-544): one step
     = the int8 weights of one DiT block (modulation, Wq/Wk/Wv/Wgate, Wo, W1,
@@ -815,7 +917,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["stack", "weights", "adaln", "qknorm", "attention",
-                                           "block"]
+                                           "block", "sampler-step"]
                     + sorted(CONV_WORKLOADS)
                     + sorted(CONVT_WORKLOADS),
                     default="stack",
@@ -863,6 +965,8 @@ def main():
     if args.workload == "attention":
         attention_main(args)
         return
+    if args.workload == "sampler-step":
+        return sampler_step_main(args)
     if args.workload == "block":
         block_main(args)
         return
