@@ -205,7 +205,8 @@ def test_tanhf_on_every_float(ctx_strict, oracle):
 
 @pytest.mark.parametrize("M,K,N,bias", [(750, 32, 1280, True), (48, 1280, 32, True),
                                         (200, 512, 1280, False), (3, 100, 130, True),
-                                        (1, 1, 1, False)])
+                                        (1, 1, 1, False), (2250, 1280, 32, True),
+                                        (37, 300, 50, False), (9, 1000, 64, True)])
 def test_linear_f32(ctx, oracle, M, K, N, bias):
     """ops.c:221-234 on the device: K-order chains, bit for bit against the
     oracle (pinned against the scalar reference build); zero rows and -0
