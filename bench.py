@@ -87,36 +87,130 @@ def base_weights(D, H, seed=1000):
     return [gauss(seed + i, s, 0.02) for i, s in enumerate(shapes)]
 
 
-def cpu_baseline(args, base, x0, cond, D, H, ops_per_step):
+def cpu_topology(limit=16):
+    """The host's CPU model, nproc, and the physical cores of the NUMA node of
+    the first CPU this process may run on (one hardware thread per core,
+    within the process's affinity, at most `limit`)."""
+    allowed = sorted(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+
+    def cpulist(text):
+        out = []
+        for part in text.strip().split(","):
+            if "-" in part:
+                a, b = part.split("-")
+                out += range(int(a), int(b) + 1)
+            elif part:
+                out.append(int(part))
+        return out
+
+    node, node_cpus = 0, set(allowed)
+    base = "/sys/devices/system/node"
+    if os.path.isdir(base):
+        for d in sorted(os.listdir(base)):
+            if d.startswith("node") and d[4:].isdigit():
+                try:
+                    cpus = set(cpulist(open(os.path.join(base, d, "cpulist")).read()))
+                except OSError:
+                    continue
+                if allowed[0] in cpus:
+                    node, node_cpus = int(d[4:]), cpus
+                    break
+    cores, seen = [], set()
+    for c in allowed:
+        if c not in node_cpus:
+            continue
+        try:
+            sib = open(f"/sys/devices/system/cpu/cpu{c}/topology/thread_siblings_list").read()
+            key = min(cpulist(sib))
+        except OSError:
+            key = c
+        if key not in seen:
+            seen.add(key)
+            cores.append(c)
+    return {"cpu_model": model, "nproc": os.cpu_count(), "allowed_cpus": len(allowed),
+            "numa_node": node, "physical_cores_used": cores[:limit]}
+
+
+def _median_block_seconds(cpu, conv, wq, x0, cond, args, D, H, repeats=5):
+    """One warm-up block, then the median wall time of `repeats` blocks, each
+    from the same input rows (block-0 weights)."""
+    times = []
+    for i in range(repeats + 1):
+        x = np.array(x0, copy=True)
+        t0 = time.perf_counter()
+        cpu.dit_block(conv, wq, x, cond, args.batch, args.frames, D, H, args.residual_mask)
+        if i:
+            times.append(time.perf_counter() - t0)
+    return float(np.median(times)), times
+
+
+def cpu_baseline(args, base, x0, cond, D, H, ops_per_step, x_gpu):
+    """The reference's oneMKL int8 path on the host (oracle/cpu_baseline.c):
+    one whole step of all blocks with the GPU's weights, compared bit for bit
+    with the GPU's x; then the median of 5 blocks after a warm-up on all
+    physical cores of one NUMA node (pinned) and on one pinned core, each
+    scaled to a step."""
     from oracle import CpuBaseline, Oracle
-    threads = min(16, len(os.sched_getaffinity(0)))
-    cpu = CpuBaseline(threads)
-    o = Oracle()
+    topo = cpu_topology()
+    cores = topo["physical_cores_used"]
+    saved = os.sched_getaffinity(0)
     conv = 0 if args.convention == "strict" else 1
-    wq = [o.weight_quantize(conv, w) for w in block_weights(base, 0)]
-    x = np.array(x0, copy=True)
-    t = np.zeros(3)
-    n = 0
-    start = time.perf_counter()
-    while True:
-        t += cpu.dit_block(conv, wq, x, cond, args.batch, args.frames, D, H, args.residual_mask)
-        n += 1
-        if time.perf_counter() - start >= args.cpu_seconds or n >= 12 * 8:
-            break
-    wall = time.perf_counter() - start
-    step_s = wall / n * args.blocks
-    log(f"cpu baseline: {n} blocks in {wall:.2f}s on {threads} threads ({cpu.backend}); "
-        f"quantize {t[0]:.2f}s gemm {t[1]:.2f}s epilogue {t[2]:.2f}s")
+    o = Oracle()
+    try:
+        os.sched_setaffinity(0, cores)
+        cpu = CpuBaseline(len(cores))
+        # parity at the bench's own configuration: every block's weights
+        x = np.array(x0, copy=True)
+        t0 = time.perf_counter()
+        for b in range(args.blocks):
+            wq = [o.weight_quantize(conv, w) for w in block_weights(base, b)]
+            cpu.dit_block(conv, wq, x, cond, args.batch, args.frames, D, H, args.residual_mask)
+        log(f"cpu baseline: full {args.blocks}-block step (parity) in "
+            f"{time.perf_counter() - t0:.2f}s")
+        if x_gpu is None:
+            parity = {"status": "not compared"}
+        else:
+            ndiff = int(np.count_nonzero(x.view(np.int32) != x_gpu.view(np.int32)))
+            parity = {"status": "bit-exact" if ndiff == 0 else "MISMATCH",
+                      "elements_differing": ndiff, "elements": int(x.size),
+                      "compared": f"x after one {args.blocks}-block step on the GPU (graph "
+                                  f"replay) vs the host's step, {args.convention} rounding"}
+        wq0 = [o.weight_quantize(conv, w) for w in block_weights(base, 0)]
+        med_all, t_all = _median_block_seconds(cpu, conv, wq0, x0, cond, args, D, H)
+        os.sched_setaffinity(0, cores[:1])
+        cpu1 = CpuBaseline(1)
+        med_one, t_one = _median_block_seconds(cpu1, conv, wq0, x0, cond, args, D, H)
+    finally:
+        os.sched_setaffinity(0, saved)
+    step_all, step_one = med_all * args.blocks, med_one * args.blocks
+    log(f"cpu baseline ({cpu.backend}): block median {med_all * 1e3:.1f} ms on {len(cores)} "
+        f"cores, {med_one * 1e3:.1f} ms on 1 core; parity {parity['status']}")
     return {
-        "value": round(ops_per_step / step_s / 1e12, 4),
+        "value": round(ops_per_step / step_all / 1e12, 4),
         "unit": "TOPS",
-        "cores": threads,
+        "cores": len(cores),
         "kind": "port",
-        "ms_per_step": round(step_s * 1e3, 2),
+        "ms_per_step": round(step_all * 1e3, 2),
+        "one_core": {"value": round(ops_per_step / step_one / 1e12, 4), "unit": "TOPS",
+                     "ms_per_step": round(step_one * 1e3, 2), "cores": 1},
         "backend": cpu.backend,
-        "sample": (f"{n} DiT blocks (block-0 weights) of the 12-block step at M={x0.shape[0]}, "
+        **topo,
+        "timing": "median of 5 DiT blocks after 1 warm-up (block-0 weights, same input rows), "
+                  "x blocks; process pinned to the listed cores (sched_setaffinity)",
+        "sample": (f"one DiT block of the {args.blocks}-block step at M={x0.shape[0]} (the "
+                   f"modulation, QKVG, Wo, W1/W3 + SiLU, two-term W2 and both gated residuals), "
                    f"scaled x{args.blocks}; quantize/epilogue single-threaded as ops.c, GEMM on "
-                   f"{threads} threads"),
+                   f"{len(cores)} MKL threads (and on 1)"),
+        "parity": parity,
     }
 
 
@@ -1028,12 +1122,14 @@ def main():
     kernels = log_profile(prof)
     roof = roofline_of(prof)
     stack_bytes = stack.nbytes()
+    # x after one step (the profiled steps restart from x_init too)
+    x_gpu = x.numpy()
     stack.destroy()
     ctx.close()
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(args, base, x0, cond, D, H, ops)
+        cpu = cpu_baseline(args, base, x0, cond, D, H, ops, x_gpu)
 
     value = ops * args.steps / wall / 1e12
     out = {
@@ -1060,7 +1156,10 @@ def main():
         },
         "roofline": roof,
         "kernels": kernels,
+        "kernels_source": ("per-kernel HIP events around each launch of directly launched "
+                           "(not graph-replayed) steps after the timed region"),
         "cpu_baseline": cpu,
+        "parity": cpu["parity"]["status"] if cpu else "not compared (--no-cpu-baseline)",
         "x_finite": finite,
     }
     print(json.dumps(out), flush=True)

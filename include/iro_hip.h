@@ -305,7 +305,8 @@ void iro_hip_dit_attn_context_destroy(IroHipAttnContext *actx);
    context_k, context_v, [(context_batch == 1 ? 1 : B) * C, D]);
    mix[b*S + s, h*64 + n] = sum_j softmax(q.k_j / 8)_j v_j[n], every sum in
    the scalar build's order, times 1 / (1 + expf(-gate)).  q, k, v, gate, mix
-   [B*S, D], D = heads * 64, all 16-byte aligned device memory.  Bit-identical
+   [B*S, D], D = heads * 64, all 16-byte aligned device memory.  B may be below
+   actx's batch (rows 0 .. B-1 of its mask are used).  Bit-identical
    to the scalar build.  Workspace: 4 * B * heads * S * (S + kept rows,
    rounded up to 128) bytes of scores. */
 int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *actx, const float *q,
@@ -322,7 +323,9 @@ typedef struct IroHipDiTStack IroHipDiTStack;
 int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int residual_mask,
                              IroHipDiTStack **out);
 /* Device fp32 weights of one block: ada [6D,D] (modulation linear),
-   wq/wk/wv/wgate/wo [D,D], w1/w3 [H,D], w2 [D,H]. */
+   wq/wk/wv/wgate/wo [D,D], w1/w3 [H,D], w2 [D,H].  ada may be NULL: only
+   iro_hip_dit_stack_step reads the modulation weight (the block forward and
+   the sampler step take fp32 adaLN parameters, dit.c:543-588). */
 int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, const float *wq,
                                 const float *wk, const float *wv, const float *wgate,
                                 const float *wo, const float *w1, const float *w3,
@@ -400,7 +403,9 @@ int iro_hip_dit_stack_set_head(IroHipDiTStack *s, const IroHipDiTHead *head);
    callback's velocity), then the CFG combine and Euler update of state in
    place (iro_hip_euler_update's arguments).  Each part is bit-identical to
    the reference's scalar build, so the step is too; only cond crosses PCIe
-   per step. */
+   per step.  batch may be below actx's batch: a plain step (use_cfg 0,
+   batch 1, sampler.c:247-249) reads mask row 0 of the CFG context, as the
+   reference does.  Every argument is checked before the first launch. */
 int iro_hip_dit_sampler_step(IroHipDiTStack *s, float *state, const float *cond, int batch,
                              int S, const IroHipAttnContext *actx, int use_cfg, int text_row,
                              int speaker_row, int caption_row, float scale_text,

@@ -14,6 +14,20 @@
 namespace iro {
 namespace {
 
+/* The expm1f / tanhf below follow fdlibm's s_expm1f.c and s_tanhf.c, whose
+ * notice is preserved as its licence asks:
+ *
+ * ====================================================
+ * Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+ *
+ * Developed at SunPro, a Sun Microsystems, Inc. business.
+ * Permission to use, copy, modify, and distribute this
+ * software is freely granted, provided that this notice
+ * is preserved.
+ * ====================================================
+ *
+ * (float conversion by Ian Lance Taylor, Cygnus Support.)
+ */
 // expm1f and tanhf as glibc 2.35 computes them: the float port of fdlibm
 // 5.3's s_expm1f.c (reduction by ln2 in a high and a low part, the rational
 // correction with coefficients Q1..Q5 in x^2/2) and s_tanhf.c (tanh from

@@ -31,14 +31,6 @@
 #include "iro_hip.h"
 #include "iro_internal.h"
 
-struct IroHipAttnContext {
-    IroHipContext *ctx = nullptr;
-    int B = 0, C = 0, context_batch = 0;
-    int max_valid = 0;           // largest number of kept context rows of any batch
-    int *rows = nullptr;         // [B][C]: source row of joined key S + i (device)
-    int *nvalid = nullptr;       // [B]: kept context rows (device)
-    std::vector<int> nvalid_h;   // the same, on the host
-};
 
 namespace iro {
 namespace {
@@ -358,10 +350,13 @@ void iro_hip_dit_attn_context_destroy(IroHipAttnContext *a) {
 int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *a, const float *q,
                           const float *k, const float *v, const float *gate, int B, int S, int D,
                           const float *context_k, const float *context_v, float *mix) {
-    if (!ctx || !a || a->ctx != ctx || B != a->B || S <= 0 || D <= 0 || D % 64 || !q || !k ||
-        !v || !gate || !mix || !context_k || !context_v)
-        return set_error(ctx, "dit_attention: invalid arguments (D a multiple of 64, the "
-                              "attention context made for this B on this context)");
+    // B may be below the context's batch: rows 0 .. B-1 of its mask are used,
+    // as the sampler's plain steps (batch 1, sampler.c:247-249) read row 0
+    // of the CFG mask.
+    if (!ctx || !a || a->ctx != ctx || B < 1 || B > a->B || S <= 0 || D <= 0 || D % 64 || !q ||
+        !k || !v || !gate || !mix || !context_k || !context_v)
+        return set_error(ctx, "dit_attention: invalid arguments (D a multiple of 64, B at most "
+                              "the batch of an attention context made on this context)");
     if (((((uintptr_t)q) | ((uintptr_t)k) | ((uintptr_t)v) | ((uintptr_t)gate) |
           ((uintptr_t)mix) | ((uintptr_t)context_k) | ((uintptr_t)context_v)) & 15) != 0)
         return set_error(ctx, "dit_attention: every tensor must be 16-byte aligned");

@@ -600,7 +600,8 @@ struct IroHipDiTStack {
     int residual_mask = 8;
     IroHipWeight *ada_all = nullptr;
     int ada_np = 0;
-    std::vector<char> ada_set;
+    std::vector<char> ada_set;  // block has its modulation weight (the stack step reads it)
+    std::vector<char> w_set;    // block has its QKVG, Wo, W1/W3 and W2 weights
     std::vector<IroHipWeight *> qkvg, wo, w13, w2;
     int cap_rows = 0, cap_branches = 0;
     float *q = nullptr, *k = nullptr, *v = nullptr, *g = nullptr, *hidden = nullptr;
@@ -912,6 +913,7 @@ int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int r
         return -1;
     }
     s->ada_set.assign(blocks, 0);
+    s->w_set.assign(blocks, 0);
     s->f32.assign(blocks, IroHipDiTLayerF32{});
     s->f32_set.assign(blocks, 0);
     s->qkvg.assign(blocks, nullptr);
@@ -928,7 +930,7 @@ int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, 
                                 const float *w2) {
     if (!s || block < 0 || block >= s->blocks) return -1;
     IroHipContext *ctx = s->ctx;
-    if (!ada || !wq || !wk || !wv || !wgate || !wo || !w1 || !w3 || !w2)
+    if (!wq || !wk || !wv || !wgate || !wo || !w1 || !w3 || !w2)
         return set_error(ctx, "dit_stack: missing block weight");
     const int D = s->D, H = s->H;
     const float *qkvg_parts[4] = {wq, wk, wv, wgate};
@@ -936,22 +938,26 @@ int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, 
     const float *w13_parts[2] = {w1, w3};
     const int w13_n[2] = {H, H};
     IroHipWeight *na = nullptr, *nq = nullptr, *no = nullptr, *n13 = nullptr, *n2 = nullptr;
-    if (iro_hip_weight_create(ctx, ada, 6 * D, D, &na) ||
+    // The modulation weight is optional: the sampler step and the block
+    // forward take the fp32 adaLN parameters instead (dit.c:543-588 has no
+    // int8 modulation linear), so only the linear-stack step needs it.
+    if ((ada && (iro_hip_weight_create(ctx, ada, 6 * D, D, &na) ||
+                 weight_rows_copy(ctx, s->ada_all, block * s->ada_np, na))) ||
         iro_hip_weight_create_fused(ctx, qkvg_parts, qkvg_n, 4, D, 0, &nq) ||
         iro_hip_weight_create(ctx, wo, D, D, &no) ||
         iro_hip_weight_create_fused(ctx, w13_parts, w13_n, 2, D, 1, &n13) ||
-        iro_hip_weight_create(ctx, w2, D, H, &n2) ||
-        weight_rows_copy(ctx, s->ada_all, block * s->ada_np, na)) {
+        iro_hip_weight_create(ctx, w2, D, H, &n2)) {
         for (IroHipWeight *w : {na, nq, no, n13, n2}) iro_hip_weight_destroy(w);
         return -1;
     }
-    iro_hip_weight_destroy(na);  // drains the stream: its rows are copied
+    if (na) iro_hip_weight_destroy(na);  // drains the stream: its rows are copied
     for (auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2}) iro_hip_weight_destroy((*v)[block]);
     s->qkvg[block] = nq;
     s->wo[block] = no;
     s->w13[block] = n13;
     s->w2[block] = n2;
-    s->ada_set[block] = 1;
+    s->ada_set[block] = ada != nullptr;
+    s->w_set[block] = 1;
     stack_drop_graph(s);
     return 0;
 }
@@ -966,7 +972,8 @@ int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B
     if (!s || !x || !cond || B <= 0 || S <= 0) return -1;
     IroHipContext *ctx = s->ctx;
     for (int b = 0; b < s->blocks; ++b)
-        if (!s->ada_set[b]) return set_error(ctx, "dit_stack: block %d has no weights", b);
+        if (!s->ada_set[b] || !s->w_set[b])
+            return set_error(ctx, "dit_stack: block %d has no weights or no modulation weight", b);
     if (stack_reserve(s, B * S, B)) return -1;
     const bool same = s->gx == x && s->gcond == cond && s->gB == B && s->gS == S &&
                       s->gepoch == ctx->ws_epoch;
@@ -1022,7 +1029,7 @@ int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int 
         block < 0 || block >= s->blocks)
         return set_error(s ? s->ctx : nullptr, "dit_block_forward: invalid arguments");
     IroHipContext *ctx = s->ctx;
-    if (!s->ada_set[block]) return set_error(ctx, "dit_block_forward: block %d has no weights", block);
+    if (!s->w_set[block]) return set_error(ctx, "dit_block_forward: block %d has no weights", block);
     const int M = B * S, D = s->D, rm = s->residual_mask;
     if (stack_reserve(s, M, B)) return -1;
     const size_t BD = (size_t)B * D;
@@ -1082,8 +1089,20 @@ int iro_hip_dit_sampler_step(IroHipDiTStack *s, float *state, const float *cond,
     IroHipContext *ctx = s->ctx;
     if (!s->head_set) return set_error(ctx, "dit_sampler_step: no head set");
     for (int l = 0; l < s->blocks; ++l)
-        if (!s->ada_set[l] || !s->f32_set[l])
+        if (!s->w_set[l] || !s->f32_set[l])
             return set_error(ctx, "dit_sampler_step: layer %d is not fully set", l);
+    // Everything the step reads is checked before its first launch: a plain
+    // step (batch 1) may use a context made for the CFG batch (its mask row
+    // 0), and the CFG rows must index this step's velocity rows.
+    if (actx->ctx != ctx || batch > actx->B)
+        return set_error(ctx, "dit_sampler_step: batch %d exceeds the attention context's %d",
+                         batch, actx->B);
+    if (use_cfg && batch < 2)
+        return set_error(ctx, "dit_sampler_step: a CFG step needs at least two rows");
+    for (int r : {text_row, speaker_row, caption_row})
+        if (r < -1 || r == 0 || r > 3 || (use_cfg && r >= batch))
+            return set_error(ctx, "dit_sampler_step: CFG row %d outside 1..%d", r,
+                             use_cfg ? batch - 1 : 3);
     const IroHipDiTHead &hd = s->head;
     const int D = s->D, M = batch * S;
     if (stack_reserve(s, M, batch)) return -1;
@@ -1123,6 +1142,7 @@ size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s) {
     size_t n = 0;
     for (int b = 0; b < s->blocks; ++b) {
         if (s->ada_set[b]) n += (size_t)6 * s->D * (s->D + sizeof(float) + sizeof(int32_t));
+        if (!s->w_set[b]) continue;
         for (const auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2}) n += iro_hip_weight_bytes((*v)[b]);
     }
     return n;

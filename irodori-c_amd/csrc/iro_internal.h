@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "iro_hip.h"
 
@@ -53,6 +54,17 @@ struct IroHipContext {
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
     float *rope = nullptr;  // rotation table: per position cos[32] then sin[32]
     int rope_S = 0;         // positions held by rope
+};
+
+// The joined-key layout of one utterance's attention context: per batch b,
+// the kept context rows in order (dit.c:815-843).
+struct IroHipAttnContext {
+    IroHipContext *ctx = nullptr;
+    int B = 0, C = 0, context_batch = 0;
+    int max_valid = 0;           // largest number of kept context rows of any batch
+    int *rows = nullptr;         // [B][C]: source row of joined key S + i (device)
+    int *nvalid = nullptr;       // [B]: kept context rows (device)
+    std::vector<int> nvalid_h;   // the same, on the host
 };
 
 // A quantized weight, pre-packed for the MFMA B operand.

@@ -652,8 +652,24 @@ class DiTStack:
     def set_block(self, block, ada, wq, wk, wv, wgate, wo, w1, w3, w2):
         ctx = self.ctx
         ctx._check(ctx.lib.iro_hip_dit_stack_set_block(
-            self.h, block, *[a.vp for a in (ada, wq, wk, wv, wgate, wo, w1, w3, w2)]),
+            self.h, block, *[None if a is None else a.vp
+                             for a in (ada, wq, wk, wv, wgate, wo, w1, w3, w2)]),
             "dit_stack_set_block")
+
+    def buffers(self, B: int, S: int) -> dict:
+        """Views of the last step's activation buffers (iro_hip_dit_stack_buffers):
+        q, k, v, gate [B*S, D], hidden [B*S, H] and the modulation rows of every
+        block, mod [B, blocks * P] (block b at column b * P, P = 6D rounded up
+        to 256)."""
+        ptrs = [C.c_void_p() for _ in range(6)]
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_buffers(self.h, *[C.byref(p) for p in ptrs]),
+                        "dit_stack_buffers")
+        M, D, H = B * S, self.D, self.H
+        P = (6 * D + 255) // 256 * 256
+        shapes = [(M, D)] * 4 + [(M, H), (B, self.blocks * P)]
+        names = ["q", "k", "v", "gate", "hidden", "mod"]
+        return {n: DeviceView(self.ctx, s, np.float32, p.value)
+                for n, s, p in zip(names, shapes, ptrs)}
 
     def step(self, x: DeviceArray, cond: DeviceArray, B: int, S: int):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_step(self.h, x.vp, cond.vp, B, S),

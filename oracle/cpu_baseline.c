@@ -28,6 +28,7 @@ typedef void (*gemm_s8u8s32_fn)(int layout, int transa, int transb, int offsetc,
                                 const int32_t *co);
 typedef int (*cbwr_set_fn)(int);
 typedef int (*cbwr_get_fn)(int);
+typedef int (*cbwr_auto_fn)(void);
 typedef void (*set_threads_fn)(int);
 
 enum {
@@ -40,7 +41,28 @@ static void *mkl_handle;
 static gemm_s8u8s32_fn mkl_gemm;
 static set_threads_fn mkl_set_threads;
 static int n_threads = 1;
-static char backend_desc[256] = "oracle-openmp";
+static char backend_desc[320] = "oracle-openmp";
+
+/* MKL_CBWR_* branch codes (mkl_cbwr.h) by name. */
+static const char *cbwr_name(int code) {
+    switch (code) {
+        case 0: return "OFF";
+        case 1: return "BRANCH_OFF";
+        case 2: return "AUTO";
+        case 3: return "COMPATIBLE";
+        case 4: return "SSE2";
+        case 6: return "SSSE3";
+        case 7: return "SSE4_1";
+        case 8: return "SSE4_2";
+        case 9: return "AVX";
+        case 10: return "AVX2";
+        case 11: return "AVX512_MIC";
+        case 12: return "AVX512";
+        case 13: return "AVX512_MIC_E1";
+        case 14: return "AVX512_E1";
+        default: return code < 0 ? "unavailable" : "unknown";
+    }
+}
 
 static double now_s(void) {
     struct timespec ts;
@@ -76,9 +98,11 @@ int cpub_init(const char *mkl_path, int threads, char *desc, size_t desc_len) {
             cbwr_set_fn cs = (cbwr_set_fn)dlsym(mkl_handle, "MKL_CBWR_Set");
             cbwr_get_fn cg = (cbwr_get_fn)dlsym(mkl_handle, "MKL_CBWR_Get");
             mkl_set_threads = (set_threads_fn)dlsym(mkl_handle, "MKL_Set_Num_Threads");
-            int branch = -1;
-            if (cs) (void)cs(MKL_CBWR_AVX512_E1);
+            cbwr_auto_fn ca = (cbwr_auto_fn)dlsym(mkl_handle, "MKL_CBWR_Get_Auto_Branch");
+            int branch = -1, set_rc = -100, auto_branch = -1;
+            if (cs) set_rc = cs(MKL_CBWR_AVX512_E1);
             if (cg) branch = cg(MKL_CBWR_BRANCH);
+            if (ca) auto_branch = ca();
             if (g) {
                 mkl_gemm = g;
                 if (mkl_set_threads) mkl_set_threads(n_threads);
@@ -90,10 +114,13 @@ int cpub_init(const char *mkl_path, int threads, char *desc, size_t desc_len) {
                 if (memcmp(want, got, sizeof(got)) != 0) {
                     mkl_gemm = NULL; /* int16-saturating branch: refuse */
                     snprintf(backend_desc, sizeof backend_desc,
-                             "oracle-openmp (oneMKL refused: selfcheck failed, cbwr %d)", branch);
+                             "oracle-openmp (oneMKL refused: selfcheck failed; CBWR setting %s)",
+                             cbwr_name(branch));
                 } else {
                     snprintf(backend_desc, sizeof backend_desc,
-                             "oneMKL cblas_gemm_s8u8s32 (cbwr branch %d)", branch);
+                             "oneMKL cblas_gemm_s8u8s32; CBWR AVX512_E1 requested "
+                             "(MKL_CBWR_Set rc %d), setting in effect %s, AUTO would pick %s",
+                             set_rc, cbwr_name(branch), cbwr_name(auto_branch));
                 }
             }
         }

@@ -423,6 +423,20 @@ static inline float orc_bitsf(uint32_t u) {
     return f;
 }
 
+/* The expm1f / tanhf below follow fdlibm's s_expm1f.c and s_tanhf.c, whose
+ * notice is preserved as its licence asks:
+ *
+ * ====================================================
+ * Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+ *
+ * Developed at SunPro, a Sun Microsystems, Inc. business.
+ * Permission to use, copy, modify, and distribute this
+ * software is freely granted, provided that this notice
+ * is preserved.
+ * ====================================================
+ *
+ * (float conversion by Ian Lance Taylor, Cygnus Support.)
+ */
 /* expm1f and tanhf as glibc 2.35 computes them: the float port of fdlibm 5.3's
    s_expm1f.c (argument reduction by ln2 in two pieces, a degree-5 rational
    correction in x^2/2 with the published Q1..Q5) and s_tanhf.c (tanh through

@@ -422,6 +422,29 @@ class Reference:
         assert rc == 0 and dims[0] == x.shape[-1], (rc, dims[0])
         return x
 
+    def dit_attn_parts(self, x, cond, ada, w, ck, cv, mask, B, S, eps, use_int8=True):
+        """The operands of the attention half's gated residual inside
+        iro_dit_block (dit.c:1004-1020), computed by the functions dit_block
+        calls on the same layer: returns (gate [B, D], branch [B*S, D])."""
+        mask = np.ascontiguousarray(mask, np.uint8)
+        x = _f32(x)
+        D = x.shape[-1]
+        gate = np.empty((B, D), np.float32)
+        branch = np.empty((B * S, D), np.float32)
+        ws = [_f32(a) for a in w]
+        adas = [_f32(a) for a in ada]
+        self.lib.ref_dit_attn_parts.argtypes = ([_f32p, _f32p, C.POINTER(_f32p)] + [_f32p] * 12 +
+                                                [_u8p] + [C.c_int] * 3 +
+                                                [C.c_float, C.c_int, _f32p, _f32p])
+        self.lib.ref_dit_attn_parts.restype = C.c_int
+        rc = self.lib.ref_dit_attn_parts(
+            _p(x, _f32p), _p(_f32(cond), _f32p), (_f32p * 18)(*[_p(a, _f32p) for a in adas]),
+            *[_p(a, _f32p) for a in ws], _p(_f32(ck), _f32p), _p(_f32(cv), _f32p),
+            _p(mask, _u8p), B, S, mask.shape[-1], eps, int(bool(use_int8)), _p(gate, _f32p),
+            _p(branch, _f32p))
+        assert rc == 0, rc
+        return gate, branch
+
     def linear_f32(self, x, w, bias=None):
         """The scalar build's iro_linear (ops.c:236-254)."""
         x, w = _f32(x), _f32(w)

@@ -40,20 +40,14 @@ int ref_dit_attention_identity(const float *x, const float *q_norm, const float 
     return rc;
 }
 
-/* iro_dit_block (dit.c:1042-1047) of layer 0 of a DiT with the given adaLN
-   weights (ada: 18 arrays, the attention then the MLP IroAdaLN in dit.h:11-23
-   order) and attention / MLP weights, quantized to int8 as
-   iro_dit_int8_quantize does (dit.c:235-259) when use_int8 != 0.
-   x [B*S, MODEL_DIM] is updated in place. */
-int ref_dit_block(float *x, const float *cond, const float *const *ada, const float *wq,
-                  const float *wk, const float *wv, const float *wgate, const float *wo,
-                  const float *q_norm, const float *k_norm, const float *w1, const float *w3,
-                  const float *w2, const float *ck, const float *cv, const uint8_t *mask, int B,
-                  int S, int C, float eps, int use_int8, int *dims) {
-    IroDiT *d = calloc(1, sizeof(IroDiT));
-    IroDiTInt8 *q8 = calloc(1, sizeof(IroDiTInt8));
-    int rc = -1;
-    if (!d || !q8) goto out;
+/* Layer 0 of a DiT with the given adaLN weights (ada: 18 arrays, the
+   attention then the MLP IroAdaLN in dit.h:11-23 order) and attention / MLP
+   weights, quantized to int8 as iro_dit_int8_quantize does (dit.c:235-259)
+   into q8 when use_int8 != 0. */
+static int setup_layer0(IroDiT *d, IroDiTInt8 *q8, const float *const *ada, const float *wq,
+                        const float *wk, const float *wv, const float *wgate, const float *wo,
+                        const float *q_norm, const float *k_norm, const float *w1,
+                        const float *w3, const float *w2, float eps, int use_int8) {
     IroAdaLN att = {ada[0], ada[1], ada[2], ada[3], ada[4], ada[5], ada[6], ada[7], ada[8]};
     IroAdaLN mlp = {ada[9], ada[10], ada[11], ada[12], ada[13], ada[14], ada[15], ada[16],
                     ada[17]};
@@ -81,9 +75,26 @@ int ref_dit_block(float *x, const float *cond, const float *const *ada, const fl
             iro_int8_weight_quantize(&l->w1, w1, MLP_DIM, MODEL_DIM) ||
             iro_int8_weight_quantize(&l->w3, w3, MLP_DIM, MODEL_DIM) ||
             iro_int8_weight_quantize(&l->w2, w2, MODEL_DIM, MLP_DIM))
-            goto out;
+            return -1;
         d->int8 = q8;
     }
+    return 0;
+}
+
+/* iro_dit_block (dit.c:1042-1047) of layer 0 set up as setup_layer0 does.
+   x [B*S, MODEL_DIM] is updated in place. */
+int ref_dit_block(float *x, const float *cond, const float *const *ada, const float *wq,
+                  const float *wk, const float *wv, const float *wgate, const float *wo,
+                  const float *q_norm, const float *k_norm, const float *w1, const float *w3,
+                  const float *w2, const float *ck, const float *cv, const uint8_t *mask, int B,
+                  int S, int C, float eps, int use_int8, int *dims) {
+    IroDiT *d = calloc(1, sizeof(IroDiT));
+    IroDiTInt8 *q8 = calloc(1, sizeof(IroDiTInt8));
+    int rc = -1;
+    if (!d || !q8) goto out;
+    if (setup_layer0(d, q8, ada, wq, wk, wv, wgate, wo, q_norm, k_norm, w1, w3, w2, eps,
+                     use_int8))
+        goto out;
     rc = iro_dit_block(d, 0, x, cond, ck, cv, mask, B, S, C);
     dims[0] = MODEL_DIM;
     dims[1] = MLP_DIM;
@@ -92,6 +103,36 @@ out:
     if (q8) iro_dit_int8_free(q8);
     free(q8);
     free(d);
+    return rc;
+}
+
+/* The two operands of the attention half's gated residual inside
+   iro_dit_block (dit.c:1004-1020), computed by the functions dit_block
+   itself calls, on the same layer: dit_adaln of the attention adaLN (its
+   gate [B, MODEL_DIM]) and dit_attention with the per-batch context
+   (branch [B*S, MODEL_DIM]).  x is not modified. */
+int ref_dit_attn_parts(const float *x, const float *cond, const float *const *ada,
+                       const float *wq, const float *wk, const float *wv, const float *wgate,
+                       const float *wo, const float *q_norm, const float *k_norm,
+                       const float *w1, const float *w3, const float *w2, const float *ck,
+                       const float *cv, const uint8_t *mask, int B, int S, int C, float eps,
+                       int use_int8, float *gate, float *branch) {
+    IroDiT *d = calloc(1, sizeof(IroDiT));
+    IroDiTInt8 *q8 = calloc(1, sizeof(IroDiTInt8));
+    float *h = malloc(sizeof(float) * (size_t)B * S * MODEL_DIM);
+    int rc = -1;
+    if (!d || !q8 || !h) goto out;
+    if (setup_layer0(d, q8, ada, wq, wk, wv, wgate, wo, q_norm, k_norm, w1, w3, w2, eps,
+                     use_int8))
+        goto out;
+    if (dit_adaln(&d->attention_adaln[0], eps, x, cond, B, S, h, gate, 0)) goto out;
+    rc = dit_attention(&d->attention[0], eps, h, ck, cv, mask, B, B, S, C, branch, 0,
+                       d->int8 ? &d->int8->layer[0] : NULL);
+out:
+    if (q8) iro_dit_int8_free(q8);
+    free(q8);
+    free(d);
+    free(h);
     return rc;
 }
 

@@ -4,8 +4,10 @@ with distinct seeded weights: iro_dit_input on one latent row set, broadcast
 to the CFG rows, iro_dit_block_shared_context per layer (int8 weights, the
 default two-term W2), iro_dit_output.  The reference is compiled from its
 sources by `make -C oracle ref` (oracle/_ref/libref_strict.so).  The fixture
-stores the velocity and a SHA-256 digest of the seeded inputs that
-step_inputs() regenerates bit for bit.  Re-run after changing the case:
+stores the velocity, the velocity of the same evaluation at batch 1 (a
+plain step, sampler.c:247-249, which reads row 0 of the CFG mask) and a
+SHA-256 digest of the seeded inputs that step_inputs() regenerates bit for
+bit.  Re-run after changing the case:
 
     python tests/golden/make_step_golden.py
 """
@@ -63,10 +65,13 @@ def input_digest(x, cond, head, ada, blk, ck, cv):
 def main():
     from oracle import Reference
     x, cond, head, ada, blk, ck, cv, mask = step_inputs()
-    vel = Reference("strict").dit_step(x, cond, head, ada, blk, ck, cv, mask, B, S, EPS)
+    ref = Reference("strict")
+    vel = ref.dit_step(x, cond, head, ada, blk, ck, cv, mask, B, S, EPS)
+    vel1 = ref.dit_step(x, cond[:1], head, ada, blk, ck, cv, mask[:1], 1, S, EPS)
     path = os.path.join(HERE, "dit_step_ref.npz")
     inputs = input_digest(x, cond, head, ada, blk, ck, cv)
-    np.savez_compressed(path, velocity=vel, mask=mask, inputs_sha256=np.array(inputs))
+    np.savez_compressed(path, velocity=vel, velocity_b1=vel1, mask=mask,
+                        inputs_sha256=np.array(inputs))
     print(f"wrote {path}: velocity {vel.shape}, inputs {inputs[:16]}")
 
 

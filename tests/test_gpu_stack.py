@@ -77,3 +77,74 @@ def test_stack_graph_replays_match_direct_steps(ctx):
             ctx.sync()
     finally:
         stack.destroy()
+
+
+def _rolled(base, b):
+    """Block b's weights: the base draws with rows rotated by a block-dependent
+    offset (distinct matrices per block at the cost of one draw)."""
+    return [np.ascontiguousarray(np.roll(w, 97 * b + 13 * i, axis=0)) for i, w in enumerate(base)]
+
+
+def test_stack_full_configuration_matches_reference_sequence(ctx, oracle):
+    """The bench's configuration end to end: 12 blocks of hidden 1024, MLP
+    2816, 3 x 750 rows, the two-term W2 (mask 8): one step, every block with
+    its own weights, against the host's block sequence."""
+    from oracle import CpuBaseline
+    conv = ctx.convention
+    blocks, B, S, D, H, rm = 12, 3, 750, 1024, 2816, 8
+    shapes = [(6 * D, D), (D, D), (D, D), (D, D), (D, D), (D, D), (H, D), (H, D), (D, H)]
+    base = [gauss(1000 + i, s, 0.02) for i, s in enumerate(shapes)]
+    x0 = gauss(7, (B * S, D))
+    cond = gauss(8, (B, D), 0.1)
+    stack = iro_hip.DiTStack(ctx, blocks, D, H, rm)
+    try:
+        for b in range(blocks):
+            dev = [ctx.to_device(w) for w in _rolled(base, b)]
+            stack.set_block(b, *dev)
+            for a in dev:
+                a.free()
+        x = ctx.to_device(x0)
+        stack.step(x, ctx.to_device(cond), B, S)
+        got = x.numpy()
+    finally:
+        stack.destroy()
+    cpu = CpuBaseline(16)
+    want = np.array(x0, copy=True)
+    for b in range(blocks):
+        cpu.dit_block(conv, [oracle.weight_quantize(conv, w) for w in _rolled(base, b)], want,
+                      cond, B, S, D, H, rm)
+    bad = int((got.view(np.int32) != want.view(np.int32)).sum())
+    assert bad == 0, f"{bad} of {got.size} elements of x differ"
+
+
+def test_stacked_modulation_gemm_twelve_blocks(ctx, oracle):
+    """The 12 blocks' modulation linears (1024 -> 6 x 1024 each) run as one
+    stacked [12 x 6144, 1024] GEMM on the 3 conditioning rows (the skinny
+    kernel); block b's rows must equal the per-block int8 linear
+    (dit.c:469-486 quantize + iro_int8_linear_ex, no bias)."""
+    conv = ctx.convention
+    blocks, B, S, D, H = 12, 3, 8, 1024, 64
+    shapes = [(6 * D, D), (D, D), (D, D), (D, D), (D, D), (D, D), (H, D), (H, D), (D, H)]
+    base = [gauss(1100 + i, s, 0.02) for i, s in enumerate(shapes)]
+    cond = gauss(1120, (B, D), 0.1)
+    stack = iro_hip.DiTStack(ctx, blocks, D, H, 8)
+    try:
+        for b in range(blocks):
+            dev = [ctx.to_device(w) for w in _rolled(base, b)]
+            stack.set_block(b, *dev)
+            for a in dev:
+                a.free()
+        x = ctx.to_device(gauss(1121, (B * S, D)))
+        stack.step(x, ctx.to_device(cond), B, S)
+        mod = stack.buffers(B, S)["mod"]
+        ctx.sync()
+        q, s, z = oracle.quantize_rows(conv, cond)
+        P = mod.shape[1] // blocks
+        got_all = mod.numpy()
+        for b in range(blocks):
+            ada = _rolled(base, b)[0]
+            want = oracle.linear(conv, q, s, z, *oracle.weight_quantize(conv, ada))[0]
+            got = np.ascontiguousarray(got_all[:, b * P:b * P + 6 * D])
+            assert np.array_equal(got.view(np.int32), want.view(np.int32)), f"block {b} differs"
+    finally:
+        stack.destroy()
