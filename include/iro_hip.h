@@ -157,6 +157,21 @@ int iro_hip_dit_linear_gated(IroHipContext *ctx, const float *mix, int M,
                              const IroHipWeight *w, int residual, float *out, float *x_res,
                              const float *gate, int S);
 
+/* iro_hip_dit_linear_gated without any device allocation, for callers that
+   cannot allocate (code under HIP graph capture, tight serving loops,
+   harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+   quantized activation is staged in a fixed per-GPU scratch of 16 MiB held
+   from library load to process end instead of the context's growable
+   workspace: M rows of K codes (two planes when residual) plus their
+   scales and zero points must fit, else the call fails with an error (at
+   K = 1024 that is up to about 8000 rows, 4000 with two planes).  Every
+   call on one GPU shares that scratch, so calls that overlap on one GPU
+   (other streams, other threads, other contexts) race.  Results are
+   identical to iro_hip_dit_linear_gated. */
+int iro_hip_dit_linear_gated_noalloc(IroHipContext *ctx, const float *mix, int M,
+                                     const IroHipWeight *w, int residual, float *out,
+                                     float *x_res, const float *gate, int S);
+
 /* dit.c:939-972 then dit.c:1032-1039: SwiGLU MLP.  h [M,D] quantized once;
    fused W1/W3 GEMM (layout 1 weight, [2H,D]) whose epilogue writes
    hidden = silu(w1)*w3 [M,H]; hidden quantized with the two-term residual

@@ -297,7 +297,7 @@ int iro_hip_create(int device, int convention, IroHipContext **out) {
     } else
         snprintf(ctx->backend, sizeof(ctx->backend), "gfx950 MFMA i8");
     if (hipMalloc(&ctx->zero16, 256) != hipSuccess || launch_fill(ctx, ctx->zero16, 0, 256) ||
-        iro_hip_selfcheck(ctx) != 0) {
+        noalloc_scratch_init(ctx) != 0 || iro_hip_selfcheck(ctx) != 0) {
         iro_hip_destroy(ctx);
         return -1;
     }

@@ -14,7 +14,38 @@
 
 #include "iro_internal.h"
 
+#include <mutex>
+
+// The scratch of iro_hip_dit_linear_gated_noalloc: the quantized activation
+// (one or two planes of codes, row scales and zero points) of one call.
+// Every GPU the library runs on holds its own copy from module load to
+// process end; calls on one GPU share it (so calls that overlap on one GPU
+// race).  Host code never passes `scratch` itself to a kernel: its device
+// address on each GPU comes from hipGetSymbolAddress (noalloc_scratch_init).
+static constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace iro {
+
+// Looks up `scratch`'s device address once per device (the caller has made
+// ctx->device current) and keeps it in the context.
+int noalloc_scratch_init(IroHipContext *ctx) {
+    static std::mutex mu;
+    static std::vector<void *> per_device;
+    std::lock_guard<std::mutex> lock(mu);
+    if (per_device.size() <= (size_t)ctx->device) per_device.resize(ctx->device + 1, nullptr);
+    if (!per_device[ctx->device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(ctx, "no-alloc scratch: hipGetSymbolAddress failed: %s",
+                             hipGetErrorString(e));
+        per_device[ctx->device] = p;
+    }
+    ctx->noalloc_scratch = per_device[ctx->device];
+    ctx->noalloc_scratch_bytes = kNoAllocScratchBytes;
+    return 0;
+}
 
 namespace {
 
@@ -518,16 +549,12 @@ int qkvg_impl(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w, 
     return launch_gemm(ctx, w, a, EPI_QKVG);
 }
 
-// y = lin(quant(x)) [two-term]; x_res += gate[m / S] * y, or out = y.
-int linear_gated_impl(IroHipContext *ctx, const float *x, int M, int ldx_in,
-                      const IroHipWeight *w, int residual, float *out, int ldo, float *x_res,
-                      const float *gate, int ldg, int S) {
+// y = lin(quant(x)) [two-term] with the codes staged in b;
+// x_res += gate[m / S] * y, or out = y.
+int linear_gated_run(IroHipContext *ctx, const ActBufs &b, const float *x, int M, int ldx_in,
+                     const IroHipWeight *w, float *out, int ldo, float *x_res,
+                     const float *gate, int ldg, int S) {
     const int K = w->K;
-    Workspace ws{ctx};
-    size_t off[6];
-    act_reserve(ws, M, K, residual != 0, off);
-    if (ws.commit()) return -1;
-    const ActBufs b = act_at(ws, K, residual != 0, off);
     if (quantize_into(ctx, x, M, K, ldx_in, b)) return -1;
     GemmArgs a = gemm_args(b, M, K);
     if (x_res) {
@@ -541,6 +568,18 @@ int linear_gated_impl(IroHipContext *ctx, const float *x, int M, int ldx_in,
     a.y = out;
     a.ldy = ldo;
     return launch_gemm(ctx, w, a, EPI_LINEAR);
+}
+
+// The same with the codes in the context workspace.
+int linear_gated_impl(IroHipContext *ctx, const float *x, int M, int ldx_in,
+                      const IroHipWeight *w, int residual, float *out, int ldo, float *x_res,
+                      const float *gate, int ldg, int S) {
+    Workspace ws{ctx};
+    size_t off[6];
+    act_reserve(ws, M, w->K, residual != 0, off);
+    if (ws.commit()) return -1;
+    const ActBufs b = act_at(ws, w->K, residual != 0, off);
+    return linear_gated_run(ctx, b, x, M, ldx_in, w, out, ldo, x_res, gate, ldg, S);
 }
 
 int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
@@ -715,6 +754,37 @@ int iro_hip_dit_linear_gated(IroHipContext *ctx, const float *mix, int M, const 
         return set_error(ctx, "dit_linear_gated: invalid arguments");
     if (M == 0) return 0;
     return linear_gated_impl(ctx, mix, M, w->K, w, residual, out, w->N, x_res, gate, w->N, S);
+}
+
+int iro_hip_dit_linear_gated_noalloc(IroHipContext *ctx, const float *mix, int M,
+                                     const IroHipWeight *w, int residual, float *out,
+                                     float *x_res, const float *gate, int S) {
+    if (!ctx || !w || M < 0 || (M && (!mix || (!x_res && !out) || (x_res && (!gate || S <= 0)))))
+        return set_error(ctx, "dit_linear_gated_noalloc: invalid arguments");
+    if (!ctx->noalloc_scratch)
+        return set_error(ctx, "dit_linear_gated_noalloc: no scratch on this device");
+    if (M == 0) return 0;
+    // The codes' layout in the scratch is the workspace's (act_reserve):
+    // offsets from 0, 256-byte aligned.
+    Workspace lay{ctx};
+    size_t off[6];
+    act_reserve(lay, M, w->K, residual != 0, off);
+    if (lay.need > ctx->noalloc_scratch_bytes)
+        return set_error(ctx,
+                         "dit_linear_gated_noalloc: %d rows of %d codes%s need %zu bytes, above "
+                         "the %zu-byte scratch",
+                         M, w->K, residual ? " (two planes)" : "", lay.need,
+                         ctx->noalloc_scratch_bytes);
+    unsigned char *base = static_cast<unsigned char *>(ctx->noalloc_scratch);
+    ActBufs b;
+    b.ld = (int)round_up((size_t)w->K, 16);
+    b.q1 = base + off[0];
+    b.s1 = reinterpret_cast<float *>(base + off[1]);
+    b.z1 = reinterpret_cast<int32_t *>(base + off[2]);
+    b.q2 = residual ? base + off[3] : nullptr;
+    b.s2 = residual ? reinterpret_cast<float *>(base + off[4]) : nullptr;
+    b.z2 = residual ? reinterpret_cast<int32_t *>(base + off[5]) : nullptr;
+    return linear_gated_run(ctx, b, mix, M, w->K, w, out, w->N, x_res, gate, w->N, S);
 }
 
 int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,

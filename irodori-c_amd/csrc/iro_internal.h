@@ -54,6 +54,8 @@ struct IroHipContext {
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
     float *rope = nullptr;  // rotation table: per position cos[32] then sin[32]
     int rope_S = 0;         // positions held by rope
+    void *noalloc_scratch = nullptr;  // this device's address of the no-alloc scratch
+    size_t noalloc_scratch_bytes = 0;
 };
 
 // The joined-key layout of one utterance's attention context: per batch b,
@@ -104,6 +106,7 @@ constexpr int kNPad = 256;  // packed rows padded to a multiple of this
 constexpr int kKPad = 128;  // packed k padded to a multiple of this
 
 int set_error(IroHipContext *ctx, const char *fmt, ...);
+int noalloc_scratch_init(IroHipContext *ctx);  // iro_dit.hip
 
 #define IRO_HIP_TRY(ctx, expr)                                                        \
     do {                                                                              \

@@ -103,6 +103,7 @@ def load() -> C.CDLL:
                                           _i, _i], _i),
         "iro_hip_dit_qkvg": ([_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i], _i),
         "iro_hip_dit_linear_gated": ([_vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _i], _i),
+        "iro_hip_dit_linear_gated_noalloc": ([_vp, _vp, _i, _vp, _i, _vp, _vp, _vp, _i], _i),
         "iro_hip_dit_swiglu": ([_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i], _i),
         "iro_hip_conv1d_int8": ([_vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _vp, _i, _vp,
                                  C.POINTER(_i)], _i),
