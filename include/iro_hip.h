@@ -58,7 +58,10 @@ void *iro_hip_stream(IroHipContext *ctx);
    choice.  Negative ti selects another schedule knob with value tj:
    -1 tile order (-1 per GEMM, 0 column slabs first, 1 row tiles first),
    -2 weight ring depth of the whole-tile kernel (0 default, 4, 8),
-   -3 column slabs per whole-tile block (0 chosen per GEMM, else 1..64).
+   -3 column slabs per whole-tile block (0 chosen per GEMM, else 1..64),
+   -4 the LDS-pipelined kernel of signed-code GEMMs (0 shape chosen per GEMM,
+      -1 off, 1 192x256, 2 96x128, 3 128x256, 4 96x256, 5 64x128 rows x
+      columns per workgroup; shapes a GEMM cannot take fall back).
    Tuning knobs only: results are identical for every setting.  No
    counterpart in the reference (oneMKL picks its own blocking). */
 int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj);
@@ -364,6 +367,13 @@ void iro_hip_dit_stack_destroy(IroHipDiTStack *s);
    graph of the whole step (default on); off runs every launch directly.
    The profiler (iro_hip_profile_enable) always runs steps directly. */
 int iro_hip_dit_stack_use_graph(IroHipDiTStack *s, int on);
+/* Steps run as one persistent kernel after the modulation GEMM (default on,
+   where supported: D a multiple of 256 up to 1024, H a multiple of 256 up
+   to 3072, residual_mask 0 or 8): workgroups take quantization and GEMM
+   items of their own XCD's rows from a queue, so the hand-offs stay in one
+   L2.  Off runs one kernel per quantization and GEMM.  Results are
+   identical either way; no counterpart in the reference. */
+int iro_hip_dit_stack_use_persistent(IroHipDiTStack *s, int on);
 
 /* One DiT block forward (dit.c:984-1040 dit_block) on the device, in place on
    x [B*S, D], with this stack's int8 weights of `block`: adaLN apply, fused

@@ -42,7 +42,7 @@ const char *const kProfNames[PK_COUNT] = {
     "quant_rows",        "quant_rows_residual", "gemm_linear",  "gemm_linear_two_term",
     "gemm_qkvg",         "gemm_qkvg_two_term",  "gemm_swiglu",  "gemm_swiglu_two_term",
     "gemm_gated",        "gemm_gated_two_term", "conv_rows",    "conv_im2col",
-    "convt_gather",      "other"};
+    "convt_gather",      "persist_stack",       "other"};
 
 struct ProfState {
     struct Rec {
@@ -297,6 +297,7 @@ int iro_hip_create(int device, int convention, IroHipContext **out) {
     } else
         snprintf(ctx->backend, sizeof(ctx->backend), "gfx950 MFMA i8");
     if (hipMalloc(&ctx->zero16, 256) != hipSuccess || launch_fill(ctx, ctx->zero16, 0, 256) ||
+        hipMalloc(&ctx->dev_err, 256) != hipSuccess || launch_fill(ctx, ctx->dev_err, 0, 256) ||
         noalloc_scratch_init(ctx) != 0 || iro_hip_selfcheck(ctx) != 0) {
         iro_hip_destroy(ctx);
         return -1;
@@ -313,6 +314,7 @@ void iro_hip_destroy(IroHipContext *ctx) {
     ctx->prof = nullptr;
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->zero16) (void)hipFree(ctx->zero16);
+    if (ctx->dev_err) (void)hipFree(ctx->dev_err);
     if (ctx->rope) (void)hipFree(ctx->rope);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -331,6 +333,17 @@ void iro_hip_clear_error(IroHipContext *ctx) {
 int iro_hip_sync(IroHipContext *ctx) {
     if (!ctx) return -1;
     IRO_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    // Kernels that can fail at run time (the persistent stack's bounded
+    // waits and completion check) OR a code into the device error word.
+    int code = 0;
+    IRO_HIP_TRY(ctx, hipMemcpy(&code, ctx->dev_err, sizeof(int), hipMemcpyDeviceToHost));
+    if (code) {
+        IRO_HIP_TRY(ctx, hipMemset(ctx->dev_err, 0, sizeof(int)));
+        return set_error(ctx, "device error 0x%x: %s%s%s", code,
+                         code & 1 ? "a persistent-kernel wait timed out; " : "",
+                         code & 2 ? "a persistent-kernel queue was not completed; " : "",
+                         code & 4 ? "unexpected XCC id" : "");
+    }
     return ctx->has_err ? -1 : 0;
 }
 
@@ -351,6 +364,11 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
     if (ti == -3) {  // tj: column slabs per whole-tile block, 0 chosen per GEMM
         if (tj < 0 || tj > 64) return set_error(ctx, "set_gemm_tile: slabs per block 0..64");
         ctx->gemm_spb = tj;
+        return 0;
+    }
+    if (ti == -4) {  // tj: LDS-pipelined kernel shape, 0 per GEMM, -1 off, 1..5 forced
+        if (tj < -1 || tj > 5) return set_error(ctx, "set_gemm_tile: LDS shape -1..5");
+        ctx->gemm_lds = tj;
         return 0;
     }
     if (ti == 0 && tj == 0) {

@@ -534,11 +534,13 @@ __global__ __launch_bounds__(64) void head_norm_kernel(float *__restrict__ q,
 int qkvg_impl(IroHipContext *ctx, const float *x, int M, const IroHipWeight *w, float *q,
               float *k, float *v, float *gate, int residual) {
     const int D = w->K;
+    // codes in the fragment layout when the LDS-pipelined kernel runs the GEMM
+    const bool packed = gemm_lds_cfg(ctx, EPI_QKVG, residual != 0, M, D) != 0;
     Workspace ws{ctx};
     size_t off[6];
-    act_reserve(ws, M, D, residual != 0, off);
+    act_reserve(ws, M, D, residual != 0, off, packed);
     if (ws.commit()) return -1;
-    const ActBufs b = act_at(ws, D, residual != 0, off);
+    const ActBufs b = act_at(ws, D, residual != 0, off, packed);
     if (quantize_into(ctx, x, M, D, D, b)) return -1;
     GemmArgs a = gemm_args(b, M, D);
     a.seg[0] = q;
@@ -574,11 +576,13 @@ int linear_gated_run(IroHipContext *ctx, const ActBufs &b, const float *x, int M
 int linear_gated_impl(IroHipContext *ctx, const float *x, int M, int ldx_in,
                       const IroHipWeight *w, int residual, float *out, int ldo, float *x_res,
                       const float *gate, int ldg, int S) {
+    const bool packed =
+        gemm_lds_cfg(ctx, x_res ? EPI_GATED : EPI_LINEAR, residual != 0, M, w->K) != 0;
     Workspace ws{ctx};
     size_t off[6];
-    act_reserve(ws, M, w->K, residual != 0, off);
+    act_reserve(ws, M, w->K, residual != 0, off, packed);
     if (ws.commit()) return -1;
-    const ActBufs b = act_at(ws, w->K, residual != 0, off);
+    const ActBufs b = act_at(ws, w->K, residual != 0, off, packed);
     return linear_gated_run(ctx, b, x, M, ldx_in, w, out, ldo, x_res, gate, ldg, S);
 }
 
@@ -586,14 +590,16 @@ int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w
                 const IroHipWeight *w2, int residual_w13, int residual_w2, float *hidden,
                 float *out, float *x_res, const float *gate, int ldg, int S) {
     const int D = w13->K, H = w13->part_N[0];
+    const bool p1 = gemm_lds_cfg(ctx, EPI_SWIGLU, residual_w13 != 0, M, D) != 0;
+    const bool p2 = gemm_lds_cfg(ctx, x_res ? EPI_GATED : EPI_LINEAR, residual_w2 != 0, M, H) != 0;
     Workspace ws{ctx};
     size_t off1[6], off2[6], oh = 0;
-    act_reserve(ws, M, D, residual_w13 != 0, off1);
-    act_reserve(ws, M, H, residual_w2 != 0, off2);
+    act_reserve(ws, M, D, residual_w13 != 0, off1, p1);
+    act_reserve(ws, M, H, residual_w2 != 0, off2, p2);
     if (!hidden) oh = ws.reserve(sizeof(float) * (size_t)M * H);
     if (ws.commit()) return -1;
-    const ActBufs b1 = act_at(ws, D, residual_w13 != 0, off1);
-    const ActBufs b2 = act_at(ws, H, residual_w2 != 0, off2);
+    const ActBufs b1 = act_at(ws, D, residual_w13 != 0, off1, p1);
+    const ActBufs b2 = act_at(ws, H, residual_w2 != 0, off2, p2);
     float *hid = hidden ? hidden : ws.at<float>(oh);
     if (quantize_into(ctx, h, M, D, D, b1)) return -1;
     GemmArgs a = gemm_args(b1, M, D);
@@ -660,6 +666,10 @@ struct IroHipDiTStack {
     int gB = 0, gS = 0;
     unsigned gepoch = 0;
     int seen = 0;  // the last eager step had these arguments
+    // the persistent kernel of the step (iro_persist.hip)
+    int use_persist = 0;
+    iro::PersistPlan *persist = nullptr;
+    int persist_M = 0, persist_S = 0;  // shape the plan was prepared for (0: stale)
 };
 
 using namespace iro;
@@ -681,6 +691,28 @@ void stack_drop_graph(IroHipDiTStack *s) {
     s->gexec = nullptr;
     s->graph = nullptr;
     s->seen = 0;
+    s->persist_M = s->persist_S = 0;  // weights or buffers may have changed
+}
+
+bool stack_persistent(const IroHipDiTStack *s) {
+    return s->use_persist && persist_supported(s->D, s->H, s->residual_mask);
+}
+
+// Buffers and weight table of the persistent kernel for this shape
+// (allocates: outside graph capture).
+int stack_persist_prepare(IroHipDiTStack *s, int B, int S) {
+    const int M = B * S;
+    if (s->persist_M == M && s->persist_S == S) return 0;
+    std::vector<const IroHipWeight *> ws;
+    for (int b = 0; b < s->blocks; ++b)
+        for (const auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2}) ws.push_back((*v)[b]);
+    if (persist_prepare(s->ctx, &s->persist, M, s->D, s->H, S, s->blocks,
+                        (s->residual_mask & 8) != 0, ws.data(), s->q, s->k, s->v, s->g, s->hidden,
+                        s->mod, s->blocks * s->ada_np, s->ada_np))
+        return -1;
+    s->persist_M = M;
+    s->persist_S = S;
+    return 0;
 }
 
 int stack_reserve(IroHipDiTStack *s, int M, int B) {
@@ -720,6 +752,7 @@ int stack_launch(IroHipDiTStack *s, float *x, const float *cond, int B, int S) {
     // for attention and MLP, 6D columns per block
     if (linear_gated_impl(ctx, cond, B, D, s->ada_all, 0, s->mod, ldm, nullptr, nullptr, 0, 1))
         return -1;
+    if (stack_persistent(s)) return persist_launch(ctx, s->persist, x);
     for (int blk = 0; blk < s->blocks; ++blk) {
         const float *mod = s->mod + (size_t)blk * s->ada_np;
         if (qkvg_impl(ctx, x, M, s->qkvg[blk], s->q, s->k, s->v, s->g, rm & 1)) return -1;
@@ -766,9 +799,11 @@ int iro_hip_dit_linear_gated_noalloc(IroHipContext *ctx, const float *mix, int M
     if (M == 0) return 0;
     // The codes' layout in the scratch is the workspace's (act_reserve):
     // offsets from 0, 256-byte aligned.
+    const bool packed =
+        gemm_lds_cfg(ctx, x_res ? EPI_GATED : EPI_LINEAR, residual != 0, M, w->K) != 0;
     Workspace lay{ctx};
     size_t off[6];
-    act_reserve(lay, M, w->K, residual != 0, off);
+    act_reserve(lay, M, w->K, residual != 0, off, packed);
     if (lay.need > ctx->noalloc_scratch_bytes)
         return set_error(ctx,
                          "dit_linear_gated_noalloc: %d rows of %d codes%s need %zu bytes, above "
@@ -777,7 +812,7 @@ int iro_hip_dit_linear_gated_noalloc(IroHipContext *ctx, const float *mix, int M
                          ctx->noalloc_scratch_bytes);
     unsigned char *base = static_cast<unsigned char *>(ctx->noalloc_scratch);
     ActBufs b;
-    b.ld = (int)round_up((size_t)w->K, 16);
+    b.ld = packed ? -(w->K / 32) : (int)round_up((size_t)w->K, 16);
     b.q1 = base + off[0];
     b.s1 = reinterpret_cast<float *>(base + off[1]);
     b.z1 = reinterpret_cast<int32_t *>(base + off[2]);
@@ -1045,6 +1080,7 @@ int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B
         if (!s->ada_set[b] || !s->w_set[b])
             return set_error(ctx, "dit_stack: block %d has no weights or no modulation weight", b);
     if (stack_reserve(s, B * S, B)) return -1;
+    if (stack_persistent(s) && stack_persist_prepare(s, B, S)) return -1;
     const bool same = s->gx == x && s->gcond == cond && s->gB == B && s->gS == S &&
                       s->gepoch == ctx->ws_epoch;
     if (!s->use_graph || ctx->prof) {
@@ -1207,6 +1243,14 @@ int iro_hip_dit_stack_use_graph(IroHipDiTStack *s, int on) {
     return 0;
 }
 
+int iro_hip_dit_stack_use_persistent(IroHipDiTStack *s, int on) {
+    if (!s) return -1;
+    IRO_HIP_TRY(s->ctx, hipStreamSynchronize(s->ctx->stream));
+    s->use_persist = on != 0;
+    stack_drop_graph(s);
+    return 0;
+}
+
 size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s) {
     if (!s) return 0;
     size_t n = 0;
@@ -1238,6 +1282,7 @@ void iro_hip_dit_stack_destroy(IroHipDiTStack *s) {
     if (!s) return;
     if (s->ctx) (void)hipStreamSynchronize(s->ctx->stream);
     stack_drop_graph(s);
+    persist_free(s->persist);
     iro_hip_weight_destroy(s->ada_all);
     for (auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2})
         for (IroHipWeight *w : *v) iro_hip_weight_destroy(w);

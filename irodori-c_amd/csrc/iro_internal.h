@@ -25,6 +25,7 @@ enum ProfKind {
     PK_CONV_ROWS,
     PK_CONV_IM2COL,
     PK_CONVT_GATHER,
+    PK_PERSIST_STACK,
     PK_OTHER,
     PK_COUNT
 };
@@ -51,9 +52,11 @@ struct IroHipContext {
     int tile_order = -1;  // -1: per GEMM; 0 column-slab-major; 1 row-major
     int gemm_ring = 0;    // weight ring depth of the whole-tile kernel (0: default)
     int gemm_spb = 0;     // column slabs per whole-tile block (0: chosen per GEMM)
+    int gemm_lds = 0;     // LDS-pipelined GEMM: 0 shape chosen per GEMM, -1 off, > 0 forced shape
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
     float *rope = nullptr;  // rotation table: per position cos[32] then sin[32]
     int rope_S = 0;         // positions held by rope
+    int *dev_err = nullptr;  // device error word: kernels OR in a code, iro_hip_sync reports it
     void *noalloc_scratch = nullptr;  // this device's address of the no-alloc scratch
     size_t noalloc_scratch_bytes = 0;
 };
@@ -186,17 +189,24 @@ struct GemmArgs {
     int ldx = 0;
     int rows_per_branch = 1;
     int a_signed = 0;  // codes already stored as a ^ 0x80 (quantize_into)
+    int a_kbp = 0;     // > 0: codes in the MFMA fragment layout with a_kbp k blocks
+                       // per 32-row block (LDS-pipelined kernel only)
 };
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi);
+// The LDS-pipelined kernel's shape a GEMM of M rows and k extent K with
+// signed codes would take, or 0 when it takes another kernel.
+int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K);
 int launch_silu_selfcheck(IroHipContext *ctx, unsigned long long *out);
 int launch_fp32_selfcheck(IroHipContext *ctx, unsigned long long *out);
 
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
 // Activation staging in the context workspace: codes in rows padded to 16
-// bytes (the GEMM reads A in 16-byte chunks), row scales and zero points,
-// and the second plane when the two-term residual quantization is on.
+// bytes (the GEMM reads A in 16-byte chunks), or, for the LDS-pipelined
+// kernel, in the MFMA fragment layout (ld < 0: -ld k blocks per 32-row
+// block, rows padded to 32); row scales and zero points, and the second
+// plane when the two-term residual quantization is on.
 struct ActBufs {
     uint8_t *q1, *q2;
     float *s1, *s2;
@@ -204,19 +214,24 @@ struct ActBufs {
     int ld;
 };
 
-inline void act_reserve(Workspace &ws, int M, int K, bool two, size_t off[6]) {
-    const size_t ld = round_up((size_t)K, 16);
-    off[0] = ws.reserve(ld * M);
+inline size_t act_code_bytes(int M, int K, bool packed) {
+    return packed ? round_up((size_t)M, 32) * (size_t)K : round_up((size_t)K, 16) * M;
+}
+
+inline void act_reserve(Workspace &ws, int M, int K, bool two, size_t off[6], bool packed = false) {
+    const size_t cb = act_code_bytes(M, K, packed);
+    off[0] = ws.reserve(cb);
     off[1] = ws.reserve(sizeof(float) * M);
     off[2] = ws.reserve(sizeof(int32_t) * M);
-    off[3] = two ? ws.reserve(ld * M) : 0;
+    off[3] = two ? ws.reserve(cb) : 0;
     off[4] = two ? ws.reserve(sizeof(float) * M) : 0;
     off[5] = two ? ws.reserve(sizeof(int32_t) * M) : 0;
 }
 
-inline ActBufs act_at(const Workspace &ws, int K, bool two, const size_t off[6]) {
+inline ActBufs act_at(const Workspace &ws, int K, bool two, const size_t off[6],
+                      bool packed = false) {
     ActBufs b;
-    b.ld = (int)round_up((size_t)K, 16);
+    b.ld = packed ? -(K / 32) : (int)round_up((size_t)K, 16);
     b.q1 = ws.at<uint8_t>(off[0]);
     b.s1 = ws.at<float>(off[1]);
     b.z1 = ws.at<int32_t>(off[2]);
@@ -244,8 +259,21 @@ inline GemmArgs gemm_args(const ActBufs &b, int M, int K) {
     a.M = M;
     a.K = (int)round_up((size_t)K, 16);
     a.a_signed = 1;
+    if (b.ld < 0) {
+        a.lda = K;
+        a.a_kbp = -b.ld;
+    }
     return a;
 }
+
+// The persistent stack kernel (iro_persist.hip).
+struct PersistPlan;
+bool persist_supported(int D, int H, int residual_mask);
+int persist_prepare(IroHipContext *ctx, PersistPlan **plan, int M, int D, int H, int S, int blocks,
+                    int two_w2, const IroHipWeight *const *weights, float *q, float *k, float *v,
+                    float *g, float *hidden, const float *mod, int ldm, int ada_np);
+int persist_launch(IroHipContext *ctx, PersistPlan *plan, float *x);
+void persist_free(PersistPlan *plan);
 
 int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi);
 int launch_convt_gather(IroHipContext *ctx, const float *expanded, int T_in, int C_out,

@@ -10,104 +10,11 @@
 // variant keeps the row in registers, forms the remainder in place and
 // quantizes it again, so the input is read from HBM exactly once.
 // Roofline: HBM, 4K + K (+K) + 8 bytes per row.
-#include "iro_internal.h"
-#include "iro_round.h"
+#include "iro_quant_row.h"
 
 namespace iro {
 
 namespace {
-
-template <int CONV>
-__device__ __forceinline__ uint32_t codes4(const float4 &v, const RowQ &r, float4 *vals) {
-    float a = quant_value<CONV>(v.x, r), b = quant_value<CONV>(v.y, r);
-    float c = quant_value<CONV>(v.z, r), d = quant_value<CONV>(v.w, r);
-    if (vals) *vals = make_float4(a, b, c, d);
-    return pack_codes4(a, b, c, d);
-}
-
-// Vector path, one row held in registers as CH float4 per lane (lane L
-// holds columns 4*(64c + L) .. +3 of chunk c).  EXACT: K == 256*CH, so no
-// column is out of range.
-template <int CH, bool EXACT>
-__device__ __forceinline__ void load_row(const float *__restrict__ xr, int K, int lane,
-                                         float4 (&v)[CH]) {
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int col = (c * 64 + lane) * 4;
-        if (EXACT || col < K)
-            v[c] = *reinterpret_cast<const float4 *>(xr + col);
-        else
-            v[c] = make_float4(0.f, 0.f, 0.f, 0.f);  // zero is inside every range
-    }
-}
-
-// ops.c:321-348 (and, with RES, ops.c:427-442) on one row already in
-// registers: range, codes (xor sflip), row scale and zero point; the
-// two-term variant forms the remainder in place and quantizes it again.
-template <int CONV, int CH, bool RES, bool EXACT>
-__device__ __forceinline__ void quant_row(float4 (&v)[CH], int row, int K, int lane,
-                                          uint8_t *__restrict__ q1, int ldq,
-                                          float *__restrict__ s1, int32_t *__restrict__ z1,
-                                          float *__restrict__ res, uint8_t *__restrict__ q2,
-                                          float *__restrict__ s2, int32_t *__restrict__ z2,
-                                          uint32_t sflip) {
-    float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        lo = sel_min(lo, v[c].x); lo = sel_min(lo, v[c].y);
-        lo = sel_min(lo, v[c].z); lo = sel_min(lo, v[c].w);
-        hi = sel_max(hi, v[c].x); hi = sel_max(hi, v[c].y);
-        hi = sel_max(hi, v[c].z); hi = sel_max(hi, v[c].w);
-    }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
-    const RowQ r = row_params<CONV>(lo, hi);
-    uint8_t *qr = q1 + (size_t)row * ldq;
-    float lo2 = 0.0f, hi2 = 0.0f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int col = (c * 64 + lane) * 4;
-        float4 qv;
-        const uint32_t packed = codes4<CONV>(v[c], r, RES ? &qv : nullptr);
-        if (EXACT || col < K) *reinterpret_cast<uint32_t *>(qr + col) = packed ^ sflip;
-        if (RES) {
-            if (EXACT || col < K) {
-                v[c].x = residual_value<CONV>(v[c].x, qv.x, r);
-                v[c].y = residual_value<CONV>(v[c].y, qv.y, r);
-                v[c].z = residual_value<CONV>(v[c].z, qv.z, r);
-                v[c].w = residual_value<CONV>(v[c].w, qv.w, r);
-            }
-            lo2 = sel_min(lo2, v[c].x); lo2 = sel_min(lo2, v[c].y);
-            lo2 = sel_min(lo2, v[c].z); lo2 = sel_min(lo2, v[c].w);
-            hi2 = sel_max(hi2, v[c].x); hi2 = sel_max(hi2, v[c].y);
-            hi2 = sel_max(hi2, v[c].z); hi2 = sel_max(hi2, v[c].w);
-        }
-    }
-    if (lane == 0) {
-        s1[row] = r.s;
-        z1[row] = r.zp;
-    }
-    if (RES) {
-        lo2 = wave_min(lo2);
-        hi2 = wave_max(hi2);
-        const RowQ r2 = row_params<CONV>(lo2, hi2);
-        uint8_t *q2r = q2 + (size_t)row * ldq;
-        float *rr = res ? res + (size_t)row * K : nullptr;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int col = (c * 64 + lane) * 4;
-            const uint32_t packed = codes4<CONV>(v[c], r2, nullptr);
-            if (EXACT || col < K) {
-                *reinterpret_cast<uint32_t *>(q2r + col) = packed ^ sflip;
-                if (rr) *reinterpret_cast<float4 *>(rr + col) = v[c];
-            }
-        }
-        if (lane == 0) {
-            s2[row] = r2.s;
-            z2[row] = r2.zp;
-        }
-    }
-}
 
 // Vector path: K % 4 == 0, 16-byte aligned rows, K <= 256*CH (EXACT:
 // K == 256*CH); one wavefront per row.
@@ -151,11 +58,10 @@ __global__ __launch_bounds__(256) void quant_rows_any(const float *__restrict__ 
     lo = wave_min(lo);
     hi = wave_max(hi);
     const RowQ r = row_params<CONV>(lo, hi);
-    uint8_t *qr = q1 + (size_t)row * ldq;
     float lo2 = 0.0f, hi2 = 0.0f;
     for (int k = lane; k < K; k += 64) {
         const float v = quant_value<CONV>(xr[k], r);
-        qr[k] = (uint8_t)v ^ fb;
+        q1[code_off(row, k, ldq)] = (uint8_t)v ^ fb;
         if (RES) {
             const float rv = residual_value<CONV>(xr[k], v, r);
             lo2 = sel_min(lo2, rv);
@@ -170,10 +76,10 @@ __global__ __launch_bounds__(256) void quant_rows_any(const float *__restrict__ 
         lo2 = wave_min(lo2);
         hi2 = wave_max(hi2);
         const RowQ r2 = row_params<CONV>(lo2, hi2);
-        uint8_t *q2r = q2 + (size_t)row * ldq;
         for (int k = lane; k < K; k += 64) {
-            const float rv = residual_value<CONV>(xr[k], (float)(uint8_t)(qr[k] ^ fb), r);
-            q2r[k] = (uint8_t)quant_value<CONV>(rv, r2) ^ fb;
+            const float rv =
+                residual_value<CONV>(xr[k], (float)(uint8_t)(q1[code_off(row, k, ldq)] ^ fb), r);
+            q2[code_off(row, k, ldq)] = (uint8_t)quant_value<CONV>(rv, r2) ^ fb;
             if (res) res[(size_t)row * K + k] = rv;
         }
         if (lane == 0) {

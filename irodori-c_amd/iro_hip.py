@@ -118,6 +118,7 @@ def load() -> C.CDLL:
         "iro_hip_dit_stack_destroy": ([_vp], None),
         "iro_hip_selfcheck_silu": ([_vp, C.POINTER(C.c_ulonglong), C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_dit_stack_use_graph": ([_vp, _i], _i),
+        "iro_hip_dit_stack_use_persistent": ([_vp, _i], _i),
         "iro_hip_dit_stack_set_layer_f32": ([_vp, _i, C.POINTER(DiTLayerF32)], _i),
         "iro_hip_dit_stack_set_head": ([_vp, C.POINTER(DiTHead)], _i),
         "iro_hip_dit_sampler_step": ([_vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, C.c_float,
@@ -705,6 +706,10 @@ class DiTStack:
             self.h, state.vp, cond.vp, batch, S, actx.h, int(bool(use_cfg)),
             *[int(r) for r in rows], *[float(x) for x in scales], float(dt), velocity.vp),
             "dit_sampler_step")
+
+    def use_persistent(self, on: bool):
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_use_persistent(self.h, int(bool(on))),
+                        "dit_stack_use_persistent")
 
     def use_graph(self, on: bool):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_use_graph(self.h, int(bool(on))),
