@@ -475,6 +475,91 @@ int iro_hip_conv1x1_skip_int8(IroHipContext *ctx, const float *hidden, const flo
                               const IroHipWeight *w, const float *bias, int residual,
                               float *output);
 
+/* ---- DACVAE decoder: snake, residual unit, int8 core ------------------- */
+
+/* iro_snake_forward (dacvae.c:830-857): y = x + sin(a x)^2 / a per element
+   of the time-major [T, C] rows (alpha [C]); up to 1536 channels with the
+   hoisted reciprocal 1 / (a + 1e-9), wider rows with the quotient.  sinf
+   is glibc's, bit for bit.  y may be x.  C % 4 == 0, 16-byte aligned rows.
+   Bit-exact against the strict build; the fast build's vectorised libmvec
+   sinf is not restated (its results are compared within a tolerance). */
+int iro_hip_snake(IroHipContext *ctx, const float *x, int T, int C, const float *alpha,
+                  float *y);
+/* snake_bias_forward (dacvae.c:910-931): v = x + bias, y = snake(v); the
+   hoisted reciprocal only in place (y == x) up to 1536 channels. */
+int iro_hip_snake_bias(IroHipContext *ctx, const float *x, int T, int C, const float *bias,
+                       const float *alpha, float *y);
+/* Digests (the iro_hip_selfcheck_silu form) of the device sinf and cosf
+   over all 2^32 float inputs, to be compared with glibc's (no counterpart
+   in the reference; a test hook). */
+int iro_hip_selfcheck_sincosf(IroHipContext *ctx, unsigned long long *sin_digest,
+                              unsigned long long *cos_digest);
+
+/* run_residual_int8 (dacvae.c:934-1018) with the int8 group mask 15:
+   hidden = Conv7(snake(input, alpha0)) (dilation d, padding 3d, no bias,
+   second activation plane when residual_conv7), snake_bias in place with
+   conv0_bias and alpha1, output = input + conv1(hidden) + conv1_bias
+   (second plane when residual_conv1).  conv0 from iro_hip_weight_create of
+   the [C, 7, C] export ([C, 7C]), conv1 [C, C].  input and output [T, C],
+   distinct.  The reference's residual flags are the policy of
+   dacvae.c:27-73: (IRO_CODEC_INT8_RESIDUAL & group) and bit `stage` of
+   IRO_CODEC_INT8_RESIDUAL_STAGES. */
+int iro_hip_dacvae_residual_int8(IroHipContext *ctx, const float *input, int T, int C,
+                                 const IroHipWeight *conv0, const float *alpha0,
+                                 const float *conv0_bias, const float *alpha1, int dilation,
+                                 const IroHipWeight *conv1, const float *conv1_bias,
+                                 int residual_conv7, int residual_conv1, float *output);
+
+#define IRO_HIP_DACVAE_STAGES 4
+#define IRO_HIP_DACVAE_RESIDUALS 3
+
+/* The decoder's fp32 parameters (IroDACVAEDecoder, dacvae.h:36-76) as
+   device pointers in the export layouts, borrowed: they must outlive the
+   IroHipDACVAE made from them. */
+typedef struct {
+    const float *alpha0, *conv0_weight, *conv0_bias; /* [C], [C, 7, C], [C] */
+    const float *alpha1, *conv1_weight, *conv1_bias; /* [C], [C, 1, C], [C] */
+    int dilation;                                    /* 1, 3, 9 (dacvae.c:187) */
+} IroHipDACVAEResidualF32;
+typedef struct {
+    const float *alpha;     /* [c_in], the snake before the upsample */
+    const float *up_weight; /* [c_in, kernel, c_out] */
+    const float *up_bias;   /* [c_out] */
+    int c_in, c_out, kernel, stride, padding, output_padding;
+    IroHipDACVAEResidualF32 residual[IRO_HIP_DACVAE_RESIDUALS];
+} IroHipDACVAEStageF32;
+typedef struct {
+    const float *initial_weight; /* [channels, 7, latent_channels] */
+    const float *initial_bias;   /* [channels] */
+    int latent_channels, channels; /* 1024, 1536 */
+    IroHipDACVAEStageF32 stage[IRO_HIP_DACVAE_STAGES];
+} IroHipDACVAEDecoderF32;
+typedef struct IroHipDACVAE IroHipDACVAE;
+
+/* iro_dacvae_int8_quantize (dacvae.c:228-262): the initial conv as
+   [channels, 7 latent], each upsample transposed to [kernel c_out, c_in],
+   each residual unit's conv0 [C, 7C] and conv1 [C, C], quantized and packed
+   on the device.  Refuses stages whose channels do not chain. */
+int iro_hip_dacvae_create(IroHipContext *ctx, const IroHipDACVAEDecoderF32 *params,
+                          IroHipDACVAE **out);
+/* IroDACVAEInt8.bytes: iro_int8_weight_bytes summed over the 26 weights. */
+size_t iro_hip_dacvae_int8_bytes(const IroHipDACVAE *d);
+void iro_hip_dacvae_destroy(IroHipDACVAE *d);
+/* Frames after the four upsamples (iro_convtranspose1d_output_length
+   chained, dacvae.c:350-358), or -1. */
+int iro_hip_dacvae_output_frames(const IroHipDACVAE *d, int frames);
+/* The int8 core of iro_dacvae_decode (dacvae.c:1221-1277) with all four
+   groups in int8 (IRO_CODEC_INT8_MASK 15): state [frames, latent] (the
+   quantizer_out result) -> initial conv (second plane when residual_mask
+   & 1) -> per stage snake + upsample (& 2) and three residual units (& 4,
+   & 8, each only in the stages of residual_stages) -> out
+   [output_frames, last c_out].  The fp32 quantizer_out before it and the
+   final snake + 96->1 tap + tanh after it stay with the caller, as the
+   reference keeps them in fp32.  The defaults are residual_mask 12,
+   residual_stages 8 (dacvae.c:51-69). */
+int iro_hip_dacvae_decode_int8(IroHipDACVAE *d, const float *state, int frames,
+                               int residual_mask, int residual_stages, float *out);
+
 /* ---- per-kernel event profiler ----------------------------------------- */
 
 /* While enabled, every kernel launch on the context is bracketed by HIP

@@ -24,14 +24,16 @@ int set_error(IroHipContext *ctx, const char *fmt, ...) {
 }
 
 int Workspace::commit() {
-    if (need <= ctx->ws_bytes) return 0;
+    void *&buf = outer ? ctx->ws_outer : ctx->ws;
+    size_t &have = outer ? ctx->ws_outer_bytes : ctx->ws_bytes;
+    if (need <= have) return 0;
     IRO_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->ws) IRO_HIP_TRY(ctx, hipFree(ctx->ws));
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
+    if (buf) IRO_HIP_TRY(ctx, hipFree(buf));
+    buf = nullptr;
+    have = 0;
     size_t grow = need + need / 4;
-    IRO_HIP_TRY(ctx, hipMalloc(&ctx->ws, grow));
-    ctx->ws_bytes = grow;
+    IRO_HIP_TRY(ctx, hipMalloc(&buf, grow));
+    have = grow;
     ++ctx->ws_epoch;
     return 0;
 }
@@ -42,7 +44,7 @@ const char *const kProfNames[PK_COUNT] = {
     "quant_rows",        "quant_rows_residual", "gemm_linear",  "gemm_linear_two_term",
     "gemm_qkvg",         "gemm_qkvg_two_term",  "gemm_swiglu",  "gemm_swiglu_two_term",
     "gemm_gated",        "gemm_gated_two_term", "conv_rows",    "conv_im2col",
-    "convt_gather",      "persist_stack",       "other"};
+    "convt_gather",      "persist_stack",       "snake",        "other"};
 
 struct ProfState {
     struct Rec {
@@ -313,6 +315,7 @@ void iro_hip_destroy(IroHipContext *ctx) {
     prof_free(ctx->prof);
     ctx->prof = nullptr;
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->ws_outer) (void)hipFree(ctx->ws_outer);
     if (ctx->zero16) (void)hipFree(ctx->zero16);
     if (ctx->dev_err) (void)hipFree(ctx->dev_err);
     if (ctx->rope) (void)hipFree(ctx->rope);

@@ -26,6 +26,7 @@ enum ProfKind {
     PK_CONV_IM2COL,
     PK_CONVT_GATHER,
     PK_PERSIST_STACK,
+    PK_SNAKE,
     PK_OTHER,
     PK_COUNT
 };
@@ -45,6 +46,11 @@ struct IroHipContext {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     unsigned ws_epoch = 0;  // bumped whenever ws is reallocated
+    // a second workspace for calls composed of other calls (the codec
+    // residual unit and decoder): their intermediates live here while the
+    // inner calls use ws
+    void *ws_outer = nullptr;
+    size_t ws_outer_bytes = 0;
     char backend[256] = {0};
     int cus = 0;        // compute units of the device
     void *zero16 = nullptr;  // 256 zero bytes: the source of padding k pieces
@@ -130,6 +136,7 @@ void prof_end(IroHipContext *ctx, ProfKind kind, double ops, double bytes);
 // stream) when a call needs more.  Offsets are 256-byte aligned.
 struct Workspace {
     IroHipContext *ctx;
+    int outer = 0;  // 1: the context's outer workspace
     size_t need = 0;
     size_t reserve(size_t bytes) {
         size_t off = need;
@@ -139,7 +146,7 @@ struct Workspace {
     int commit();  // ensures ctx->ws holds `need` bytes
     template <class T>
     T *at(size_t off) const {
-        return reinterpret_cast<T *>(static_cast<char *>(ctx->ws) + off);
+        return reinterpret_cast<T *>(static_cast<char *>(outer ? ctx->ws_outer : ctx->ws) + off);
     }
 };
 

@@ -1,0 +1,105 @@
+// iro_sincosf.h -- glibc's sinf and cosf, bit for bit, on gfx950.
+//
+// glibc 2.35 on x86-64 resolves sinf/cosf to the FMA build of ARM
+// optimized-routines' sincosf method, which the reference's scalar code
+// calls (the snake activations of dacvae.c:810-925, the timestep embedding
+// of dit.c:486-499):
+//   |x| < pi/4   an odd (sin) or even (cos) polynomial in double;
+//   |x| < 120    n = round(x * 2/pi) through a 2^24-scaled product and an
+//                integer shift, r = fma(-n, pi/2, x), then the polynomial of
+//                quadrant n with its sign (the cosine coefficients negated for
+//                n & 2);
+//   larger |x|   a 32 x 96-bit product of the mantissa with 4/pi (a 192-bit
+//                table, 8 new bits per word) gives the quadrant and a 2.62
+//                fixed-point remainder, scaled by pi * 2^-62.
+// Every "a + b * c" of the polynomials and of the fast reduction is one fma
+// in that build; double operations on the device round as on the host, so
+// the results are libm's (iro_hip_selfcheck_sincosf hashes all 2^32 inputs
+// for comparison with the same hash of glibc's results).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace iro {
+namespace {
+
+struct SinCosTab {
+    double sign[4], hpi_inv, hpi, c0, c1, c2, c3, c4, s1, s2, s3;
+};
+
+__constant__ SinCosTab kSinCosTab[2] = {
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, 0x1p0,
+     -0x1.ffffffd0c621cp-2, 0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10, 0x1.99343027bf8c3p-16,
+     -0x1.555545995a603p-3, 0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, -0x1p0,
+     0x1.ffffffd0c621cp-2, -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10, -0x1.99343027bf8c3p-16,
+     -0x1.555545995a603p-3, 0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13}};
+
+// 4/pi in 192 bits; word i holds bits 8i .. 8i+31 of the expansion.
+__constant__ uint32_t kInvPio4[24] = {
+    0xa2,       0xa2f9,     0xa2f983,   0xa2f9836e, 0xf9836e4e, 0x836e4e44,
+    0x6e4e4415, 0x4e441529, 0x441529fc, 0x1529fc27, 0x29fc2757, 0xfc2757d1,
+    0x2757d1f5, 0x57d1f534, 0xd1f534dd, 0xf534ddc0, 0x34ddc0db, 0xddc0db62,
+    0xc0db6295, 0xdb629599, 0x6295993c, 0x95993c43, 0x993c4390, 0x3c439041};
+
+__device__ __forceinline__ float sincos_poly(double x, double x2, const SinCosTab &p, int n) {
+    if ((n & 1) == 0) {
+        const double x3 = x * x2;
+        const double s1 = __builtin_fma(x2, p.s3, p.s2);
+        const double x7 = x3 * x2;
+        const double s = __builtin_fma(x3, p.s1, x);
+        return (float)__builtin_fma(x7, s1, s);
+    }
+    const double x4 = x2 * x2;
+    const double c2 = __builtin_fma(x2, p.c4, p.c3);
+    const double c1 = __builtin_fma(x2, p.c1, p.c0);
+    const double x6 = x4 * x2;
+    const double c = __builtin_fma(x4, p.c2, c1);
+    return (float)__builtin_fma(x6, c2, c);
+}
+
+// cosine = 0: sinf(y); 1: cosf(y).
+__device__ __forceinline__ float sincosf_glibc(float y, int cosine) {
+    const uint32_t yi = __float_as_uint(y);
+    const uint32_t top = (yi >> 20) & 0x7ff;
+    double x = y;
+    if (top < 0x3f4) {  // |y| < pi/4 (top 12 bits of the float pi/4)
+        if (top < 0x398) return cosine ? 1.0f : y;  // |y| < 2^-12
+        return sincos_poly(x, x * x, kSinCosTab[0], cosine);
+    }
+    int n;
+    int t;  // table: negated cosine coefficients for quadrants 2, 3
+    double sgn;
+    if (top < 0x42f) {  // |y| < 120
+        const double r = x * kSinCosTab[0].hpi_inv;
+        n = ((int32_t)r + 0x800000) >> 24;
+        x = __builtin_fma(-(double)n, kSinCosTab[0].hpi, x);
+        sgn = kSinCosTab[0].sign[n & 3];
+        t = (n & 2) ? 1 : 0;
+    } else if (top < 0x7f8) {  // finite
+        const uint32_t *arr = &kInvPio4[(yi >> 26) & 15];
+        const int shift = (yi >> 23) & 7;
+        uint32_t xi = ((yi & 0xffffff) | 0x800000) << shift;
+        uint64_t res0 = (uint32_t)(xi * arr[0]);
+        const uint64_t res1 = (uint64_t)xi * arr[4];
+        const uint64_t res2 = (uint64_t)xi * arr[8];
+        res0 = (res2 >> 32) | (res0 << 32);
+        res0 += res1;
+        const uint64_t nn = (res0 + (1ull << 61)) >> 62;
+        res0 -= nn << 62;
+        x = (double)(int64_t)res0 * 0x1.921FB54442D18p-62;
+        n = (int)nn;
+        const int sign = (int)(yi >> 31);
+        sgn = kSinCosTab[0].sign[(n + sign) & 3];
+        t = ((n + sign) & 2) ? 1 : 0;
+    } else {
+        return (y - y) / (y - y);
+    }
+    return sincos_poly(x * sgn, x * x, kSinCosTab[t], n ^ cosine);
+}
+
+__device__ __forceinline__ float sinf_glibc(float y) { return sincosf_glibc(y, 0); }
+__device__ __forceinline__ float cosf_glibc(float y) { return sincosf_glibc(y, 1); }
+
+}  // namespace
+}  // namespace iro

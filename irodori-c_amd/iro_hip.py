@@ -36,6 +36,28 @@ class DiTHead(C.Structure):
 _lib = None
 
 
+class DACVAEResidualF32(C.Structure):
+    # iro_hip.h IroHipDACVAEResidualF32 (dacvae.h:36-41)
+    _fields_ = [("alpha0", C.c_void_p), ("conv0_weight", C.c_void_p), ("conv0_bias", C.c_void_p),
+                ("alpha1", C.c_void_p), ("conv1_weight", C.c_void_p), ("conv1_bias", C.c_void_p),
+                ("dilation", C.c_int)]
+
+
+class DACVAEStageF32(C.Structure):
+    # iro_hip.h IroHipDACVAEStageF32 (dacvae.h:43-47)
+    _fields_ = [("alpha", C.c_void_p), ("up_weight", C.c_void_p), ("up_bias", C.c_void_p),
+                ("c_in", C.c_int), ("c_out", C.c_int), ("kernel", C.c_int), ("stride", C.c_int),
+                ("padding", C.c_int), ("output_padding", C.c_int),
+                ("residual", DACVAEResidualF32 * 3)]
+
+
+class DACVAEDecoderF32(C.Structure):
+    # iro_hip.h IroHipDACVAEDecoderF32 (dacvae.h:69-76, the int8-path part)
+    _fields_ = [("initial_weight", C.c_void_p), ("initial_bias", C.c_void_p),
+                ("latent_channels", C.c_int), ("channels", C.c_int),
+                ("stage", DACVAEStageF32 * 4)]
+
+
 def declared_symbols() -> list[str]:
     """Every function name the C headers in include/ declare."""
     names = []
@@ -145,6 +167,17 @@ def load() -> C.CDLL:
                                   C.POINTER(C.c_double), C.POINTER(C.c_double),
                                   C.POINTER(C.c_double)], _i),
         "iro_hip_selfcheck": ([_vp], _i),
+        "iro_hip_snake": ([_vp, _vp, _i, _i, _vp, _vp], _i),
+        "iro_hip_snake_bias": ([_vp, _vp, _i, _i, _vp, _vp, _vp], _i),
+        "iro_hip_selfcheck_sincosf": ([_vp, C.POINTER(C.c_ulonglong),
+                                       C.POINTER(C.c_ulonglong)], _i),
+        "iro_hip_dacvae_residual_int8": ([_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _i,
+                                          _i, _vp], _i),
+        "iro_hip_dacvae_create": ([_vp, C.POINTER(DACVAEDecoderF32), C.POINTER(_vp)], _i),
+        "iro_hip_dacvae_int8_bytes": ([_vp], C.c_size_t),
+        "iro_hip_dacvae_destroy": ([_vp], None),
+        "iro_hip_dacvae_output_frames": ([_vp, _i], _i),
+        "iro_hip_dacvae_decode_int8": ([_vp, _vp, _i, _i, _i, _vp], _i),
         "iro_hip_backend_name": ([_vp], C.c_char_p),
         # ops.h drop-in
         "iro_int8_weight_quantize": ([_vp, _vp, _i, _i], _i),
@@ -618,6 +651,31 @@ class Context:
             int(bool(residual)), out.vp), "conv1x1_skip_int8")
 
 
+    # -- codec ---------------------------------------------------------------------------
+    def snake(self, x, T, Cc, alpha, y):
+        """iro_snake_forward (dacvae.c:830-857); y may be x."""
+        self._check(self.lib.iro_hip_snake(self.h, x.vp, T, Cc, alpha.vp, y.vp), "snake")
+
+    def snake_bias(self, x, T, Cc, bias, alpha, y):
+        """snake_bias_forward (dacvae.c:910-931); y may be x."""
+        self._check(self.lib.iro_hip_snake_bias(self.h, x.vp, T, Cc, bias.vp, alpha.vp, y.vp),
+                    "snake_bias")
+
+    def selfcheck_sincosf(self):
+        """(sinf digest, cosf digest) over every float input."""
+        a, b = C.c_ulonglong(0), C.c_ulonglong(0)
+        self._check(self.lib.iro_hip_selfcheck_sincosf(self.h, C.byref(a), C.byref(b)),
+                    "selfcheck_sincosf")
+        return int(a.value), int(b.value)
+
+    def dacvae_residual(self, x, T, Cc, conv0, alpha0, conv0_bias, alpha1, dilation, conv1,
+                        conv1_bias, residual_conv7, residual_conv1, out):
+        """run_residual_int8 (dacvae.c:934-1018)."""
+        self._check(self.lib.iro_hip_dacvae_residual_int8(
+            self.h, x.vp, T, Cc, conv0.h, alpha0.vp, conv0_bias.vp, alpha1.vp, dilation, conv1.h,
+            conv1_bias.vp, int(bool(residual_conv7)), int(bool(residual_conv1)), out.vp),
+            "dacvae_residual_int8")
+
     # -- profiler ----------------------------------------------------------------------
     def profile(self, on: bool):
         self._check(self.lib.iro_hip_profile_enable(self.h, int(bool(on))), "profile_enable")
@@ -721,6 +779,52 @@ class DiTStack:
     def destroy(self):
         if self.h:
             self.ctx.lib.iro_hip_dit_stack_destroy(self.h)
+            self.h = None
+
+
+class DACVAE:
+    """The decoder's int8 weights and core (iro_hip_dacvae_*).  params: the
+    fp32 device arrays, dict(initial_w, initial_b, stages=[dict(alpha, up_w,
+    up_b, c_in, c_out, kernel, stride, padding, output_padding,
+    residual=[dict(alpha0, w0, b0, alpha1, w1, b1, dil)] * 3)] * 4); they are
+    borrowed and must outlive this object."""
+
+    def __init__(self, ctx: Context, params: dict):
+        self.ctx = ctx
+        self._keep = params
+        p = DACVAEDecoderF32()
+        p.initial_weight = params["initial_w"].vp
+        p.initial_bias = params["initial_b"].vp
+        p.latent_channels = params["latent_channels"]
+        p.channels = params["channels"]
+        for i, st in enumerate(params["stages"]):
+            d = p.stage[i]
+            d.alpha, d.up_weight, d.up_bias = st["alpha"].vp, st["up_w"].vp, st["up_b"].vp
+            for f in ("c_in", "c_out", "kernel", "stride", "padding", "output_padding"):
+                setattr(d, f, st[f])
+            for r, u in enumerate(st["residual"]):
+                e = d.residual[r]
+                e.alpha0, e.conv0_weight, e.conv0_bias = u["alpha0"].vp, u["w0"].vp, u["b0"].vp
+                e.alpha1, e.conv1_weight, e.conv1_bias = u["alpha1"].vp, u["w1"].vp, u["b1"].vp
+                e.dilation = u["dil"]
+        h = C.c_void_p()
+        ctx._check(ctx.lib.iro_hip_dacvae_create(ctx.h, C.byref(p), C.byref(h)), "dacvae_create")
+        self.h = h
+
+    def nbytes(self) -> int:
+        return int(self.ctx.lib.iro_hip_dacvae_int8_bytes(self.h))
+
+    def output_frames(self, frames: int) -> int:
+        return int(self.ctx.lib.iro_hip_dacvae_output_frames(self.h, frames))
+
+    def decode_int8(self, state, frames, out, residual_mask=12, residual_stages=8):
+        self.ctx._check(self.ctx.lib.iro_hip_dacvae_decode_int8(
+            self.h, state.vp, frames, residual_mask, residual_stages, out.vp),
+            "dacvae_decode_int8")
+
+    def destroy(self):
+        if self.h:
+            self.ctx.lib.iro_hip_dacvae_destroy(self.h)
             self.h = None
 
 

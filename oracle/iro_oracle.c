@@ -553,6 +553,163 @@ unsigned long long orc_tanhf_digest(int threads) {
     return h;
 }
 
+/* sinf and cosf as glibc 2.35 computes them on x86-64 (the FMA ifunc
+   variant libm's sinf/cosf resolve to on this host): ARM optimized-routines'
+   sincosf method.  |x| < pi/4: an odd (sin) or even (cos) polynomial in
+   double; |x| < 120: x - n*pi/2 with n from x * 2/pi scaled by 2^24
+   (fnmadd), then the polynomial of the quadrant with its sign; larger |x|:
+   a 32 x 96-bit product with 4/pi (192-bit table, 8 new bits per word)
+   gives the quadrant and a 2.62 fixed-point remainder.  In the FMA build
+   each "a + b * c" of the polynomials and the reduction is one fma.  The
+   constants are the published ones (sincosf_data.c); the restatement is
+   checked against libm on every float input
+   (tests/test_oracle_pins.py::test_sinf_cosf_restatement_equals_libm_on_every_float). */
+typedef struct {
+    double sign[4], hpi_inv, hpi, c0, c1, c2, c3, c4, s1, s2, s3;
+} orc_sincos_t;
+static const orc_sincos_t orc_sincos_tab[2] = {
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, 0x1p0,
+     -0x1.ffffffd0c621cp-2, 0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10,
+     0x1.99343027bf8c3p-16, -0x1.555545995a603p-3, 0x1.1107605230bc4p-7,
+     -0x1.994eb3774cf24p-13},
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, -0x1p0,
+     0x1.ffffffd0c621cp-2, -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10,
+     -0x1.99343027bf8c3p-16, -0x1.555545995a603p-3, 0x1.1107605230bc4p-7,
+     -0x1.994eb3774cf24p-13}};
+static const uint32_t orc_inv_pio4[24] = {
+    0xa2,       0xa2f9,     0xa2f983,   0xa2f9836e, 0xf9836e4e, 0x836e4e44,
+    0x6e4e4415, 0x4e441529, 0x441529fc, 0x1529fc27, 0x29fc2757, 0xfc2757d1,
+    0x2757d1f5, 0x57d1f534, 0xd1f534dd, 0xf534ddc0, 0x34ddc0db, 0xddc0db62,
+    0xc0db6295, 0xdb629599, 0x6295993c, 0x95993c43, 0x993c4390, 0x3c439041};
+
+static inline uint32_t orc_abstop12(float x) { return (orc_fbits(x) >> 20) & 0x7ff; }
+
+static inline float orc_sincos_poly(double x, double x2, const orc_sincos_t *p, int n) {
+    if ((n & 1) == 0) {
+        const double x3 = x * x2;
+        const double s1 = fma(x2, p->s3, p->s2);
+        const double x7 = x3 * x2;
+        const double s = fma(x3, p->s1, x);
+        return (float)fma(x7, s1, s);
+    }
+    const double x4 = x2 * x2;
+    const double c2 = fma(x2, p->c4, p->c3);
+    const double c1 = fma(x2, p->c1, p->c0);
+    const double x6 = x4 * x2;
+    const double c = fma(x4, p->c2, c1);
+    return (float)fma(x6, c2, c);
+}
+
+static inline double orc_reduce_fast(double x, const orc_sincos_t *p, int *np) {
+    const double r = x * p->hpi_inv;
+    const int n = ((int32_t)r + 0x800000) >> 24;
+    *np = n;
+    return fma(-(double)n, p->hpi, x);
+}
+
+static inline double orc_reduce_large(uint32_t xi, int *np) {
+    const uint32_t *arr = &orc_inv_pio4[(xi >> 26) & 15];
+    const int shift = (xi >> 23) & 7;
+    xi = (xi & 0xffffff) | 0x800000;
+    xi <<= shift;
+    uint64_t res0 = (uint32_t)(xi * arr[0]);
+    const uint64_t res1 = (uint64_t)xi * arr[4];
+    const uint64_t res2 = (uint64_t)xi * arr[8];
+    res0 = (res2 >> 32) | (res0 << 32);
+    res0 += res1;
+    const uint64_t n = (res0 + (1ULL << 61)) >> 62;
+    res0 -= n << 62;
+    const double x = (double)(int64_t)res0;
+    *np = (int)n;
+    return x * 0x1.921FB54442D18p-62;
+}
+
+/* cosine = 0: sinf; 1: cosf. */
+static float orc_sincosf(float y, int cosine) {
+    double x = y;
+    int n;
+    const orc_sincos_t *p = &orc_sincos_tab[0];
+    if (orc_abstop12(y) < orc_abstop12(0x1.921FB6p-1f)) {
+        const double x2 = x * x;
+        if (orc_abstop12(y) < orc_abstop12(0x1p-12f)) return cosine ? 1.0f : y;
+        return orc_sincos_poly(x, x2, p, cosine);
+    }
+    if (orc_abstop12(y) < orc_abstop12(120.0f)) {
+        x = orc_reduce_fast(x, p, &n);
+        const double s = p->sign[n & 3];
+        if (n & 2) p = &orc_sincos_tab[1];
+        return orc_sincos_poly(x * s, x * x, p, n ^ cosine);
+    }
+    if (orc_abstop12(y) < orc_abstop12(INFINITY)) {
+        const uint32_t xi = orc_fbits(y);
+        const int sign = xi >> 31;
+        x = orc_reduce_large(xi, &n);
+        const double s = p->sign[(n + sign) & 3];
+        if ((n + sign) & 2) p = &orc_sincos_tab[1];
+        return orc_sincos_poly(x * s, x * x, p, n ^ cosine);
+    }
+    return (y - y) / (y - y);
+}
+
+float orc_sinf(float x) { return orc_sincosf(x, 0); }
+float orc_cosf(float x) { return orc_sincosf(x, 1); }
+
+/* Inputs whose restated sinf (which = 0) or cosf (1) differs from libm's
+   (NaN == NaN), over all 2^32 floats. */
+long long orc_sincosf_mismatches(int which, int threads) {
+    long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static) num_threads(threads)
+    for (long long i = 0; i < (1LL << 32); i++) {
+        const float x = orc_bitsf((uint32_t)i);
+        const float a = which ? orc_cosf(x) : orc_sinf(x);
+        const float b = which ? cosf(x) : sinf(x);
+        if (orc_fbits(a) != orc_fbits(b) && !(a != a && b != b)) bad++;
+    }
+    return bad;
+}
+
+/* Digest of the restated sinf (which = 0) or cosf (1) over all 2^32 inputs,
+   in the form of orc_tanhf_digest. */
+unsigned long long orc_sincosf_digest(int which, int threads) {
+    unsigned long long h = 0;
+#pragma omp parallel for reduction(+ : h) schedule(static) num_threads(threads)
+    for (long long i = 0; i < (1LL << 32); i++) {
+        const float x = orc_bitsf((uint32_t)i);
+        const float t = which ? orc_cosf(x) : orc_sinf(x);
+        const uint32_t ut = t != t ? 0x7FC00000u : orc_fbits(t);
+        h += ((unsigned long long)(uint32_t)i * 0x9E3779B97F4A7C15ull) ^
+             ((unsigned long long)ut * 0xC2B2AE3D27D4EB4Full);
+    }
+    return h;
+}
+
+/* The snake activations of the decoder (dacvae.c:803-931) on time-major
+   [T, C] rows: v = x (+ bias[c] when bias is not NULL), y = v + sin(a v)^2
+   / a with sinf = orc_sinf.  inv_form: the hoisted reciprocal
+   inv = 1 / (a + 1e-9), y = v + (s * s) * inv (iro_snake_forward up to 1536
+   channels, snake_bias_forward in place up to 1536 channels); otherwise the
+   quotient y = v + (s * s) / (a + 1e-9).  conv ORC_GCC_FASTMATH contracts the
+   reciprocal form's final add into fma(s * s, inv, v); the fast build's
+   libmvec sinf is not restated, so that convention is parity unpinned here.
+   y may be x. */
+void orc_snake(int conv, const float *x, int T, int C, const float *bias, const float *alpha,
+               int inv_form, float *y) {
+    for (long long t = 0; t < T; t++)
+        for (int c = 0; c < C; c++) {
+            const size_t i = (size_t)t * C + c;
+            const float v = bias ? x[i] + bias[c] : x[i];
+            const float a = alpha[c];
+            const float s = orc_sinf(a * v);
+            const float ss = s * s;
+            if (inv_form) {
+                const float inv = 1.0f / (a + 1e-9f);
+                y[i] = conv == ORC_GCC_FASTMATH ? fmaf(ss, inv, v) : v + ss * inv;
+            } else {
+                y[i] = v + ss / (a + 1e-9f);
+            }
+        }
+}
+
 /* dit.c:543-558 adaln_branch for branches 0..2 of one adaLN, then the gate's
    tanhf (dit.c:588): act = silu(cond slice) as x / (1 + expf(-x));
    low[r] = sum_d act[d] down[r][d] in index order (+ 0, the scalar linear's

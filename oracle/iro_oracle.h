@@ -99,6 +99,12 @@ void orc_rmsnorm(const float *x, int M, int D, const float *w, float eps, float 
 float orc_expm1f(float x);
 float orc_tanhf(float x);
 long long orc_tanhf_mismatches(int threads);
+float orc_sinf(float x);
+float orc_cosf(float x);
+long long orc_sincosf_mismatches(int which, int threads);
+unsigned long long orc_sincosf_digest(int which, int threads);
+void orc_snake(int conv, const float *x, int T, int C, const float *bias, const float *alpha,
+               int inv_form, float *y);
 unsigned long long orc_tanhf_digest(int threads);
 void orc_adaln_params(const float *cond, int B, int D, int R, const float *const *down,
                       const float *const *up, const float *const *bias, float *out);

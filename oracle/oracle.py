@@ -100,6 +100,15 @@ class Oracle:
         L.orc_conv1x1_skip_int8.argtypes = [C.c_int, _f32p, _f32p, C.c_int, _i8p, _f32p, _i32p,
                                             C.c_int, C.c_int, _f32p, C.c_int, _f32p, C.c_int]
         L.orc_conv1x1_skip_int8.restype = C.c_int
+        L.orc_sinf.argtypes = [C.c_float]
+        L.orc_sinf.restype = C.c_float
+        L.orc_cosf.argtypes = [C.c_float]
+        L.orc_cosf.restype = C.c_float
+        L.orc_sincosf_mismatches.argtypes = [C.c_int, C.c_int]
+        L.orc_sincosf_mismatches.restype = C.c_longlong
+        L.orc_sincosf_digest.argtypes = [C.c_int, C.c_int]
+        L.orc_sincosf_digest.restype = C.c_ulonglong
+        L.orc_snake.argtypes = [C.c_int, _f32p, C.c_int, C.c_int, _f32p, _f32p, C.c_int, _f32p]
         self.threads = min(8, os.cpu_count() or 1)
 
     def weight_quantize(self, conv, w):
@@ -357,6 +366,67 @@ class Oracle:
         return y
 
 
+    def sincosf_mismatches(self, which):
+        """Inputs (of all 2^32) where the restated sinf (0) / cosf (1) differs from libm."""
+        return self.lib.orc_sincosf_mismatches(which, self.threads)
+
+    def sincosf_digest(self, which):
+        """The device self-check's hash of sinf (0) / cosf (1) over all 2^32 inputs."""
+        return int(self.lib.orc_sincosf_digest(which, self.threads))
+
+    def snake(self, conv, x, alpha, bias=None, inv_form=None):
+        """dacvae.c:830-931 on [T, C]; inv_form defaults to iro_snake_forward's
+        choice (C <= 1536).  With bias it is snake_bias_forward, whose
+        reciprocal form needs in-place (pass inv_form=True for that case)."""
+        x = _f32(x)
+        T, Cc = x.shape
+        if inv_form is None:
+            inv_form = Cc <= 1536 and bias is None
+        y = np.empty_like(x)
+        self.lib.orc_snake(conv, _p(x, _f32p), T, Cc, _p(None if bias is None else _f32(bias),
+                                                          _f32p),
+                           _p(_f32(alpha), _f32p), int(bool(inv_form)), _p(y, _f32p))
+        return y
+
+    def residual_unit(self, conv, x, u, two7, two1):
+        """run_residual_int8 (dacvae.c:934-1018) composed from the restated
+        pieces: u = dict(alpha0, w0 [C,7,C], b0, alpha1, w1 [C,1,C], b1, dil)."""
+        x = _f32(x)
+        T, Cc = x.shape
+        q0, s0, c0 = self.weight_quantize(conv, np.asarray(u["w0"]).reshape(Cc, 7 * Cc))
+        q1, s1, c1 = self.weight_quantize(conv, np.asarray(u["w1"]).reshape(Cc, Cc))
+        act = self.snake(conv, x, u["alpha0"])
+        d = u["dil"]
+        hidden, _, _, _ = self.conv1d(conv, act, q0, s0, c0, 7, 1, d, 3 * d, None, two7)
+        hidden = self.snake(conv, hidden, u["alpha1"], bias=u["b0"], inv_form=Cc <= 1536)
+        return self.conv1x1_skip(conv, hidden, x, q1, s1, c1, u["b1"], two1)
+
+    def decode_core(self, conv, state, p, residual_mask=12, residual_stages=8):
+        """The int8 core of iro_dacvae_decode (dacvae.c:1221-1277) composed
+        from the restated pieces; p = dict(initial_w [1536,7,1024], initial_b,
+        stages=[dict(alpha, up_w [c_in,k,c_out], up_b, c_out, kernel, stride,
+        padding, output_padding, residual=[u, u, u])])."""
+        state = _f32(state)
+        lat = state.shape[1]
+        iw = np.asarray(p["initial_w"])
+        q, s_, c_ = self.weight_quantize(conv, iw.reshape(iw.shape[0], 7 * lat))
+        x, _, _, _ = self.conv1d(conv, state, q, s_, c_, 7, 1, 1, 3, p["initial_b"],
+                                 bool(residual_mask & 1))
+        for si, st in enumerate(p["stages"]):
+            c_in = x.shape[1]
+            k, c_out = st["kernel"], st["c_out"]
+            uq, us, uc = self.weight_quantize_transposed(conv, np.asarray(st["up_w"]).reshape(
+                c_in, k * c_out), k * c_out, c_in)
+            act = self.snake(conv, x, st["alpha"])
+            x = self.convtranspose1d(conv, act, uq, us, uc, c_out, k, st["stride"], st["padding"],
+                                     st["output_padding"], st["up_b"], bool(residual_mask & 2))
+            on = bool(residual_stages >> si & 1)
+            for u in st["residual"]:
+                x = self.residual_unit(conv, x, u, bool(residual_mask & 4) and on,
+                                       bool(residual_mask & 8) and on)
+        return x
+
+
 class _Weight(C.Structure):
     # ops.h:23-28 IroInt8Weight
     _fields_ = [("data", _i8p), ("scale", _f32p), ("colsum", _i32p), ("N", C.c_int),
@@ -401,6 +471,14 @@ class Reference:
                                                  C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                                  _f32p]
         L.ref_dit_attention_identity.restype = C.c_int
+        L.ref_snake.argtypes = [_f32p, _f32p, C.c_int, C.c_int, _f32p]
+        L.ref_snake_bias.argtypes = [_f32p, _f32p, C.c_int, C.c_int, _f32p, _f32p]
+        L.ref_dacvae_residual_int8.argtypes = [_f32p, C.c_int, C.c_int, _f32p, _f32p, _f32p,
+                                               _f32p, _f32p, _f32p, C.c_int, C.c_int, _f32p]
+        L.ref_dacvae_residual_int8.restype = C.c_int
+        L.ref_dacvae_decode_trace.argtypes = [C.POINTER(_f32p), _f32p, C.c_int, _f32p, _f32p,
+                                              _f32p]
+        L.ref_dacvae_decode_trace.restype = C.c_int
 
     def dit_block(self, x, cond, ada, w, ck, cv, mask, B, S, eps, use_int8=True):
         """iro_dit_block (dit.c:1042-1047) of one layer: ada = 18 adaLN arrays
@@ -693,6 +771,53 @@ class Reference:
             _p(np.ascontiguousarray(colsum, np.int32), _i32p), _p(_f32(bias), _f32p), _p(y, _f32p))
         assert rc == 0
         return y
+
+
+    def snake(self, x, alpha, inplace=False):
+        """iro_snake_forward (dacvae.c:830-857), out of place or in place."""
+        x = np.array(x, np.float32, copy=True, order="C")
+        y = x if inplace else np.empty_like(x)
+        self.lib.ref_snake(_p(x, _f32p), _p(y, _f32p), x.shape[0], x.shape[1],
+                           _p(_f32(alpha), _f32p))
+        return y
+
+    def snake_bias(self, x, bias, alpha, inplace=True):
+        """snake_bias_forward (dacvae.c:910-931)."""
+        x = np.array(x, np.float32, copy=True, order="C")
+        y = x if inplace else np.empty_like(x)
+        self.lib.ref_snake_bias(_p(x, _f32p), _p(y, _f32p), x.shape[0], x.shape[1],
+                                _p(_f32(bias), _f32p), _p(_f32(alpha), _f32p))
+        return y
+
+    def residual_unit(self, x, u, stage):
+        """run_residual_int8 (dacvae.c:934-1018) of a unit in decoder `stage`
+        under the default policy (second plane in stage 3 only)."""
+        x = _f32(x)
+        T, Cc = x.shape
+        y = np.empty_like(x)
+        rc = self.lib.ref_dacvae_residual_int8(
+            _p(x, _f32p), T, Cc, _p(_f32(u["alpha0"]), _f32p), _p(_f32(u["w0"]), _f32p),
+            _p(_f32(u["b0"]), _f32p), _p(_f32(u["alpha1"]), _f32p), _p(_f32(u["w1"]), _f32p),
+            _p(_f32(u["b1"]), _f32p), u["dil"], stage, _p(y, _f32p))
+        assert rc == 0
+        return y
+
+    def decode_trace(self, params, latent):
+        """iro_dacvae_decode (dacvae.c:1213-1300) with int8 weights: returns the
+        quantizer_out state, the state after stage 3 and the waveform.
+        params: the 91 fp32 arrays in ref_dacvae_decode_trace's order."""
+        keep = [_f32(a) for a in params]
+        assert len(keep) == 91
+        arr = (_f32p * 91)(*[_p(a, _f32p) for a in keep])
+        latent = _f32(latent)
+        frames = latent.shape[0]
+        state = np.empty((frames, 1024), np.float32)
+        core = np.empty((frames * 1920, 96), np.float32)
+        wave = np.empty(frames * 1920, np.float32)
+        rc = self.lib.ref_dacvae_decode_trace(arr, _p(latent, _f32p), frames, _p(state, _f32p),
+                                              _p(core, _f32p), _p(wave, _f32p))
+        assert rc == frames * 1920, rc
+        return state, core, wave
 
 
 class _CpubWeight(C.Structure):

@@ -75,3 +75,120 @@ int ref_dit_adaln_zero_rank(float eps, const float *x, const float *cond,
     *dim = IRO_DIT_MODEL_DIM;
     return rc;
 }
+
+/* The snake activations (dacvae.c:830-931): iro_snake_forward is public,
+   snake_bias_forward file-static. */
+void ref_snake(const float *input, float *output, int T, int C, const float *alpha) {
+    iro_snake_forward(input, output, T, C, alpha);
+}
+
+void ref_snake_bias(const float *input, float *output, int T, int C, const float *bias,
+                    const float *alpha) {
+    snake_bias_forward(input, output, T, C, bias, alpha);
+}
+
+/* run_residual_int8 (dacvae.c:934-1018) on one residual unit built from fp32
+   export-layout weights (conv0 [C, 7, C], conv1 [C, 1, C]), quantized as
+   iro_dacvae_int8_quantize does (dacvae.c:247-255).  `stage` is the decoder
+   stage the unit belongs to: with the default policy (dacvae.c:51-69) the
+   second activation plane runs only in stage 3. */
+int ref_dacvae_residual_int8(const float *input, int T, int C, const float *alpha0,
+                             const float *w0, const float *b0, const float *alpha1,
+                             const float *w1, const float *b1, int dilation, int stage,
+                             float *output) {
+    IroDACVAEResidual unit;
+    memset(&unit, 0, sizeof(unit));
+    unit.alpha0 = alpha0;
+    unit.alpha1 = alpha1;
+    IroConv1d c0 = {w0, b0, C, C, 7, 1, dilation, 3 * dilation};
+    IroConv1d c1 = {w1, b1, C, C, 1, 1, 1, 0};
+    unit.conv0 = c0;
+    unit.conv1 = c1;
+    IroDACVAEInt8Residual q;
+    memset(&q, 0, sizeof(q));
+    if (iro_int8_weight_quantize(&q.conv0, w0, C, 7 * C) != 0 ||
+        iro_int8_weight_quantize(&q.conv1, w1, C, C) != 0) {
+        iro_int8_weight_free(&q.conv0);
+        iro_int8_weight_free(&q.conv1);
+        return -1;
+    }
+    float *out = run_residual_int8(&unit, &q, input, T, C, NULL, stage, 0);
+    iro_int8_weight_free(&q.conv0);
+    iro_int8_weight_free(&q.conv1);
+    if (!out) return -1;
+    memcpy(output, out, sizeof(float) * (size_t)T * C);
+    free(out);
+    return 0;
+}
+
+/* iro_dacvae_decode (dacvae.c:1213-1300) with the int8 weights of
+   iro_dacvae_int8_quantize, its trace observer keeping the quantizer_out
+   state [frames, 1024] and the state after decoder stage 3 [T, 96].
+   params holds 91 device-free host pointers in this order:
+   quantizer_out weight [1024, 1, 32], bias; initial weight [1536, 7, 1024],
+   bias; per stage: alpha, upsample weight [c_in, 2 rate, c_out], bias, then
+   per residual unit alpha0, conv0 weight, bias, alpha1, conv1 weight, bias;
+   final alpha [96], final weight [1, 7, 96], bias [1]. */
+typedef struct {
+    float *state, *core;
+    int state_frames, core_frames;
+} RefDecodeTrace;
+
+static int ref_decode_observe(void *user, const char *name, const float *data, int frames,
+                              int channels) {
+    RefDecodeTrace *t = user;
+    if (!strcmp(name, "codec_quantizer_out") && t->state) {
+        memcpy(t->state, data, sizeof(float) * (size_t)frames * channels);
+        t->state_frames = frames;
+    } else if (!strcmp(name, "codec_decoder_stage3") && t->core) {
+        memcpy(t->core, data, sizeof(float) * (size_t)frames * channels);
+        t->core_frames = frames;
+    }
+    return 0;
+}
+
+int ref_dacvae_decode_trace(const float *const *params, const float *latent, int latent_frames,
+                            float *state, float *core, float *waveform) {
+    IroDACVAEDecoder dec;
+    memset(&dec, 0, sizeof(dec));
+    int i = 0;
+    IroConv1d qo = {params[i], params[i + 1], CODEBOOK_DIM, LATENT_DIM, 1, 1, 1, 0};
+    i += 2;
+    IroConv1d ini = {params[i], params[i + 1], LATENT_DIM, DECODER_DIM, 7, 1, 1, 3};
+    i += 2;
+    dec.quantizer_out = qo;
+    dec.initial = ini;
+    const int cin[IRO_DACVAE_STAGES] = {1536, 768, 384, 192};
+    const int cout[IRO_DACVAE_STAGES] = {768, 384, 192, 96};
+    const int rates[IRO_DACVAE_STAGES] = {12, 10, 8, 2};
+    const int dil[IRO_DACVAE_RESIDUALS] = {1, 3, 9};
+    for (int s = 0; s < IRO_DACVAE_STAGES; s++) {
+        IroDACVAEStage *st = &dec.stage[s];
+        st->alpha = params[i++];
+        IroConvTranspose1d up = {params[i], params[i + 1], cin[s], cout[s], 2 * rates[s],
+                                 rates[s], (rates[s] + 1) / 2, rates[s] & 1};
+        i += 2;
+        st->upsample = up;
+        for (int r = 0; r < IRO_DACVAE_RESIDUALS; r++) {
+            IroDACVAEResidual *u = &st->residual[r];
+            u->alpha0 = params[i++];
+            IroConv1d c0 = {params[i], params[i + 1], cout[s], cout[s], 7, 1, dil[r], 3 * dil[r]};
+            i += 2;
+            u->alpha1 = params[i++];
+            IroConv1d c1 = {params[i], params[i + 1], cout[s], cout[s], 1, 1, 1, 0};
+            i += 2;
+            u->conv0 = c0;
+            u->conv1 = c1;
+        }
+    }
+    dec.final_alpha = params[i++];
+    IroConv1d fin = {params[i], params[i + 1], FINAL_CHANNELS, 1, 7, 1, 1, 3};
+    dec.final = fin;
+    IroDACVAEInt8 q;
+    if (iro_dacvae_int8_quantize(&q, &dec) != 0) return -1;
+    dec.int8 = &q;
+    RefDecodeTrace t = {state, core, 0, 0};
+    const int rc = iro_dacvae_decode(&dec, latent, latent_frames, waveform, ref_decode_observe, &t);
+    iro_dacvae_int8_free(&q);
+    return rc ? rc : t.core_frames;
+}
