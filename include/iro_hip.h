@@ -367,13 +367,23 @@ void iro_hip_dit_stack_destroy(IroHipDiTStack *s);
    graph of the whole step (default on); off runs every launch directly.
    The profiler (iro_hip_profile_enable) always runs steps directly. */
 int iro_hip_dit_stack_use_graph(IroHipDiTStack *s, int on);
-/* Steps run as one persistent kernel after the modulation GEMM (default on,
-   where supported: D a multiple of 256 up to 1024, H a multiple of 256 up
-   to 3072, residual_mask 0 or 8): workgroups take quantization and GEMM
-   items of their own XCD's rows from a queue, so the hand-offs stay in one
-   L2.  Off runs one kernel per quantization and GEMM.  Results are
-   identical either way; no counterpart in the reference. */
+/* Steps run as one persistent kernel after the modulation GEMM (default
+   off; where supported: D a multiple of 256 up to 1024, H a multiple of 256
+   up to 3072, residual_mask 0 or 8, int8 mask 15): workgroups take
+   quantization and GEMM items of their own XCD's rows from a queue, so the
+   hand-offs stay in one L2.  Off runs one kernel per quantization and GEMM.
+   Results are identical either way; no counterpart in the reference. */
 int iro_hip_dit_stack_use_persistent(IroHipDiTStack *s, int on);
+/* IRO_INT8_MASK (dit.c:273-291): the projection groups that run in int8
+   (1 Q/K/V/gate, 2 Wo, 4 W1/W3, 8 W2; default 15).  A group whose bit is
+   clear runs through iro_hip_linear_f32 (the reference's iro_linear) on a
+   device copy of its fp32 weights that set_block keeps, with the SiLU gate
+   and gated residual as separate fp32 passes (ops.c:781-784,
+   dit.c:1013-1039); the int8 weights are built regardless, as
+   iro_dit_int8_quantize builds all of them, so iro_hip_dit_stack_bytes is
+   unchanged.  Must be set before the first set_block. */
+int iro_hip_dit_stack_set_int8_mask(IroHipDiTStack *s, int mask);
+int iro_hip_dit_stack_get_int8_mask(const IroHipDiTStack *s);
 
 /* One DiT block forward (dit.c:984-1040 dit_block) on the device, in place on
    x [B*S, D], with this stack's int8 weights of `block`: adaLN apply, fused
@@ -430,12 +440,35 @@ int iro_hip_dit_stack_set_head(IroHipDiTStack *s, const IroHipDiTHead *head);
    the reference's scalar build, so the step is too; only cond crosses PCIe
    per step.  batch may be below actx's batch: a plain step (use_cfg 0,
    batch 1, sampler.c:247-249) reads mask row 0 of the CFG context, as the
-   reference does.  Every argument is checked before the first launch. */
+   reference does.  Every argument is checked before the first launch.
+   Steps with the same state, cond, batch, S, actx and velocity as the
+   previous one (and use_graph on) replay a HIP graph of the network
+   forward (input projection to velocity), captured on the second such
+   step; the CFG / Euler update, whose scalars change per step, is launched
+   after it. */
 int iro_hip_dit_sampler_step(IroHipDiTStack *s, float *state, const float *cond, int batch,
                              int S, const IroHipAttnContext *actx, int use_cfg, int text_row,
                              int speaker_row, int caption_row, float scale_text,
                              float scale_speaker, float scale_caption, float dt,
                              float *velocity);
+
+/* iro_dit_condition (dit.c:488-530) on the device: the timestep embedding
+   of t [B] (cos then sin of t * 1000 expf(-log(10000) i / half), half =
+   tdim / 2, with glibc's expf, cosf and sinf), then linear w0 [D, tdim],
+   SiLU, linear w1 [D, D], SiLU, linear w2 [cond_dim, D], no biases, into
+   cond [B, cond_dim].  Bit-identical to the strict build; the fast build
+   vectorises the embedding with libmvec, which is not restated. */
+int iro_hip_dit_condition(IroHipContext *ctx, const float *t, int B, const float *w0,
+                          const float *w1, const float *w2, int tdim, int D, int cond_dim,
+                          float *cond);
+/* ops.c:776-784 in place on n device floats: x = x / (1 + expf(-x)), times
+   gate[i] when gate is not NULL (iro_silu_inplace / iro_silu_mul_inplace,
+   glibc's expf, the strict build's rounding). */
+int iro_hip_silu(IroHipContext *ctx, float *x, const float *gate, long long n);
+/* dit.c:1013-1020: x[m][d] += gate[(m / S) * ldg + d] * branch[m][d] for M
+   rows of D (two roundings; one fma under IRO_HIP_GCC_FASTMATH). */
+int iro_hip_gated_residual(IroHipContext *ctx, float *x, const float *gate, int ldg,
+                           const float *branch, int M, int D, int S);
 
 /* ---- DACVAE int8 Conv1d (dacvae.c:543-688, no snake) ------------------- */
 
@@ -578,6 +611,11 @@ int iro_hip_profile_read(IroHipContext *ctx, int kind, const char **name, long l
 
 /* Runs the ops.c:375-398 known answer through the MFMA GEMM: 0 exact. */
 int iro_hip_selfcheck(IroHipContext *ctx);
+/* Test hook (the counterpart of the reference refusing an inexact backend
+   at init, generate.c:527-536): while on, the known answer's input is
+   altered after its expected sums are computed, so iro_hip_selfcheck and
+   iro_hip_create must refuse.  Process-wide. */
+int iro_hip_selfcheck_inject_fault(int on);
 /* Exhaustive check of the SiLU gate's device pieces over all 2^32 float
    inputs (no counterpart in the reference; a test hook): exp_digest = sum
    mod 2^64 of (bits(x) * 0x9E3779B97F4A7C15) ^ (bits(expf(x)) *

@@ -1,6 +1,7 @@
 // iro_capi.hip -- the C ABI of include/iro_hip.h: contexts, device
 // weights, and the entry points that chain the quantize / GEMM / im2col
 // kernels on the context's stream.
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -816,6 +817,15 @@ int iro_hip_conv1x1_skip_int8(IroHipContext *ctx, const float *hidden, const flo
 
 // ---- backend queries -------------------------------------------------------------------
 
+// Test hook: while set, the known answer's first activation code is altered
+// after its expected sums are computed, so the check must refuse.
+static std::atomic<int> g_selfcheck_fault{0};
+
+int iro_hip_selfcheck_inject_fault(int on) {
+    g_selfcheck_fault.store(on != 0);
+    return 0;
+}
+
 int iro_hip_selfcheck(IroHipContext *ctx) {
     if (!ctx) return -1;
     const int M = 3, N = 5, K = 64;
@@ -823,6 +833,7 @@ int iro_hip_selfcheck(IroHipContext *ctx) {
     int8_t b[N * K];
     int32_t want[M * N], got[M * N];
     kat_arrays(a, b, want);
+    if (g_selfcheck_fault.load()) a[0] ^= 0x01;
     // As ops.c:388-391: unit scales and a zero colsum; only `work` is read.
     float wscale[N] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f}, sx[M] = {1.0f, 1.0f, 1.0f};
     int32_t colsum[N] = {0}, zx[M] = {0};

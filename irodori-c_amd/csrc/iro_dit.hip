@@ -586,6 +586,23 @@ int linear_gated_impl(IroHipContext *ctx, const float *x, int M, int ldx_in,
     return linear_gated_run(ctx, b, x, M, ldx_in, w, out, ldo, x_res, gate, ldg, S);
 }
 
+// hidden [M, H] = silu(W1 h) * W3 h from one int8 GEMM (dit.c:939-956).
+int swiglu_w13(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
+               int residual_w13, float *hidden) {
+    const int D = w13->K, H = w13->part_N[0];
+    const bool p1 = gemm_lds_cfg(ctx, EPI_SWIGLU, residual_w13 != 0, M, D) != 0;
+    Workspace ws{ctx};
+    size_t off1[6];
+    act_reserve(ws, M, D, residual_w13 != 0, off1, p1);
+    if (ws.commit()) return -1;
+    const ActBufs b1 = act_at(ws, D, residual_w13 != 0, off1, p1);
+    if (quantize_into(ctx, h, M, D, D, b1)) return -1;
+    GemmArgs a = gemm_args(b1, M, D);
+    a.hidden = hidden;
+    a.ldh = H;
+    return launch_gemm(ctx, w13, a, EPI_SWIGLU);
+}
+
 int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
                 const IroHipWeight *w2, int residual_w13, int residual_w2, float *hidden,
                 float *out, float *x_res, const float *gate, int ldg, int S) {
@@ -624,6 +641,24 @@ int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w
 }  // namespace
 }  // namespace iro
 
+// A captured sequence of launches and the arguments it was captured with:
+// replayed while the arguments (pointers, sizes, the workspace epoch) stay
+// the same; the first call with new arguments runs eagerly (sizing every
+// buffer), the second captures.
+struct GraphCache {
+    std::vector<long long> key;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int seen = 0;
+    void drop() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+        seen = 0;
+    }
+};
+
 // The int8 weights of one DiT linear stack, device resident and pre-packed
 // once (the reference builds them once in iro_engine_init,
 // generate.c:527-579), plus the per-step activation buffers.
@@ -643,6 +678,17 @@ struct IroHipDiTStack {
     IroHipContext *ctx = nullptr;
     int blocks = 0, D = 0, H = 0;
     int residual_mask = 8;
+    // IRO_INT8_MASK (dit.c:273-291): groups whose bit is clear (1 QKVG, 2 Wo,
+    // 4 W1/W3, 8 W2) run through the fp32 linear on device copies of their
+    // fp32 weights, kept by set_block; the int8 weights are built anyway, as
+    // the reference's iro_dit_int8_quantize builds all of them.
+    int int8_mask = 15;
+    struct F32Weights {
+        float *wq = nullptr, *wk = nullptr, *wv = nullptr, *wg = nullptr, *wo = nullptr,
+              *w1 = nullptr, *w3 = nullptr, *w2 = nullptr;
+    };
+    std::vector<F32Weights> f32w;
+    int any_set = 0;  // some block's weights were set (the mask is then fixed)
     IroHipWeight *ada_all = nullptr;
     int ada_np = 0;
     std::vector<char> ada_set;  // block has its modulation weight (the stack step reads it)
@@ -653,6 +699,7 @@ struct IroHipDiTStack {
     float *mod = nullptr;
     float *h = nullptr, *mix = nullptr;  // block forward: normed input, attention output
     float *proj = nullptr, *params = nullptr;  // sampler step: hidden rows, adaLN parameters
+    float *branch = nullptr, *hidden3 = nullptr;  // fp32 groups: a branch [M, D], W3 rows [M, H]
     std::vector<IroHipDiTLayerF32> f32;        // sampler step: per-layer fp32 parameters
     std::vector<char> f32_set;
     IroHipDiTHead head{};
@@ -666,6 +713,9 @@ struct IroHipDiTStack {
     int gB = 0, gS = 0;
     unsigned gepoch = 0;
     int seen = 0;  // the last eager step had these arguments
+    // graph of the last sampler step's network forward (its CFG / Euler
+    // update, whose scalars change every step, is launched after it)
+    GraphCache sgraph;
     // the persistent kernel of the step (iro_persist.hip)
     int use_persist = 0;
     iro::PersistPlan *persist = nullptr;
@@ -678,7 +728,7 @@ namespace {
 
 void stack_free_acts(IroHipDiTStack *s) {
     for (float **p : {&s->q, &s->k, &s->v, &s->g, &s->hidden, &s->mod, &s->h, &s->mix,
-                      &s->proj, &s->params}) {
+                      &s->proj, &s->params, &s->branch, &s->hidden3}) {
         if (*p) (void)hipFree(*p);
         *p = nullptr;
     }
@@ -692,10 +742,17 @@ void stack_drop_graph(IroHipDiTStack *s) {
     s->graph = nullptr;
     s->seen = 0;
     s->persist_M = s->persist_S = 0;  // weights or buffers may have changed
+    s->sgraph.drop();
+}
+
+void f32_weights_free(IroHipDiTStack::F32Weights &f) {
+    for (float *p : {f.wq, f.wk, f.wv, f.wg, f.wo, f.w1, f.w3, f.w2})
+        if (p) (void)hipFree(p);
+    f = IroHipDiTStack::F32Weights{};
 }
 
 bool stack_persistent(const IroHipDiTStack *s) {
-    return s->use_persist && persist_supported(s->D, s->H, s->residual_mask);
+    return s->use_persist && s->int8_mask == 15 && persist_supported(s->D, s->H, s->residual_mask);
 }
 
 // Buffers and weight table of the persistent kernel for this shape
@@ -733,6 +790,9 @@ int stack_reserve(IroHipDiTStack *s, int M, int B) {
     if (e == hipSuccess) e = hipMalloc(&s->hidden, sizeof(float) * (size_t)M * s->H);
     if (e == hipSuccess)
         e = hipMalloc(&s->mod, sizeof(float) * (size_t)B * s->blocks * s->ada_np);
+    if (e == hipSuccess && s->int8_mask != 15) e = hipMalloc(&s->branch, md);
+    if (e == hipSuccess && s->int8_mask != 15)
+        e = hipMalloc(&s->hidden3, sizeof(float) * (size_t)M * s->H);
     if (e != hipSuccess) {
         stack_free_acts(s);
         return set_error(ctx, "dit_stack: hipMalloc failed: %s", hipGetErrorString(e));
@@ -742,11 +802,107 @@ int stack_reserve(IroHipDiTStack *s, int M, int B) {
     return 0;
 }
 
+// Runs `launch` through the graph cache gc: replays the graph captured with
+// the same key (the arguments plus the workspace epoch), runs eagerly the
+// first time a key is seen and captures on the second.
+template <class F>
+int graph_step(IroHipContext *ctx, GraphCache &gc, bool use, std::vector<long long> key,
+               F &&launch) {
+    key.push_back((long long)ctx->ws_epoch);
+    if (!use || ctx->prof) {
+        gc.drop();
+        return launch();
+    }
+    if (gc.exec && key == gc.key) {
+        IRO_HIP_TRY(ctx, hipGraphLaunch(gc.exec, ctx->stream));
+        return 0;
+    }
+    if (key != gc.key || !gc.seen) {
+        gc.drop();
+        if (launch()) return -1;
+        key.back() = (long long)ctx->ws_epoch;  // the eager run sized the workspace
+        gc.key = key;
+        gc.seen = 1;
+        return 0;
+    }
+    IRO_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    const int rc = launch();
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (rc || e != hipSuccess || !graph || (long long)ctx->ws_epoch != key.back()) {
+        if (graph) (void)hipGraphDestroy(graph);
+        gc.drop();
+        return set_error(ctx, "graph capture failed (%s)",
+                         e != hipSuccess ? hipGetErrorString(e) : "a launch failed");
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        gc.drop();
+        return set_error(ctx, "graph instantiate failed: %s", hipGetErrorString(ei));
+    }
+    gc.graph = graph;
+    gc.exec = exec;
+    IRO_HIP_TRY(ctx, hipGraphLaunch(gc.exec, ctx->stream));
+    return 0;
+}
+
+// The four projection sites of block blk, int8 or, for a group whose mask
+// bit is clear, the fp32 linear (dit.c:780-798, 876-884, 939-972).
+// dit.c:780-798: Q, K, V and the attention gate from `in` [M, D].
+int site_qkvg(IroHipDiTStack *s, int blk, const float *in, int M) {
+    IroHipContext *ctx = s->ctx;
+    const int D = s->D;
+    if (s->int8_mask & 1)
+        return qkvg_impl(ctx, in, M, s->qkvg[blk], s->q, s->k, s->v, s->g, s->residual_mask & 1);
+    const IroHipDiTStack::F32Weights &f = s->f32w[blk];
+    return iro_hip_linear_f32(ctx, in, M, D, f.wq, D, nullptr, s->q) ||
+           iro_hip_linear_f32(ctx, in, M, D, f.wk, D, nullptr, s->k) ||
+           iro_hip_linear_f32(ctx, in, M, D, f.wv, D, nullptr, s->v) ||
+           iro_hip_linear_f32(ctx, in, M, D, f.wg, D, nullptr, s->g);
+}
+
+// dit.c:876-884 and 1013-1020: x += gate[m / S] * Wo(mix).
+int site_wo(IroHipDiTStack *s, int blk, const float *mix, int M, float *x, const float *gate,
+            int ldg, int S) {
+    IroHipContext *ctx = s->ctx;
+    const int D = s->D;
+    if (s->int8_mask & 2)
+        return linear_gated_impl(ctx, mix, M, D, s->wo[blk], s->residual_mask & 2, nullptr, 0, x,
+                                 gate, ldg, S);
+    return iro_hip_linear_f32(ctx, mix, M, D, s->f32w[blk].wo, D, nullptr, s->branch) ||
+           launch_gated_residual(ctx, x, gate, ldg, s->branch, M, D, S);
+}
+
+// dit.c:939-972 and 1032-1039: x += gate[m / S] * W2(silu(W1 h) * W3 h).
+int site_mlp(IroHipDiTStack *s, int blk, const float *h, int M, float *x, const float *gate,
+             int ldg, int S) {
+    IroHipContext *ctx = s->ctx;
+    const int D = s->D, H = s->H, rm = s->residual_mask;
+    const bool i13 = (s->int8_mask & 4) != 0, i2 = (s->int8_mask & 8) != 0;
+    if (i13 && i2)
+        return swiglu_impl(ctx, h, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, s->hidden, nullptr,
+                           x, gate, ldg, S);
+    const IroHipDiTStack::F32Weights &f = s->f32w[blk];
+    if (i13) {
+        if (swiglu_w13(ctx, h, M, s->w13[blk], rm & 4, s->hidden)) return -1;
+    } else if (iro_hip_linear_f32(ctx, h, M, D, f.w1, H, nullptr, s->hidden) ||
+               iro_hip_linear_f32(ctx, h, M, D, f.w3, H, nullptr, s->hidden3) ||
+               launch_silu(ctx, s->hidden, s->hidden3, (long long)M * H)) {
+        return -1;
+    }
+    if (i2)
+        return linear_gated_impl(ctx, s->hidden, M, H, s->w2[blk], rm & 8, nullptr, 0, x, gate,
+                                 ldg, S);
+    return iro_hip_linear_f32(ctx, s->hidden, M, H, f.w2, D, nullptr, s->branch) ||
+           launch_gated_residual(ctx, x, gate, ldg, s->branch, M, D, S);
+}
+
 // The launches of one step (sampler.c:243-301 runs dit_block per layer).
 int stack_launch(IroHipDiTStack *s, float *x, const float *cond, int B, int S) {
     IroHipContext *ctx = s->ctx;
     const int M = B * S, D = s->D;
-    const int rm = s->residual_mask;
     const int ldm = s->blocks * s->ada_np;
     // modulation rows of every block [B, blocks * ada_np]: shift/scale/gate
     // for attention and MLP, 6D columns per block
@@ -755,12 +911,8 @@ int stack_launch(IroHipDiTStack *s, float *x, const float *cond, int B, int S) {
     if (stack_persistent(s)) return persist_launch(ctx, s->persist, x);
     for (int blk = 0; blk < s->blocks; ++blk) {
         const float *mod = s->mod + (size_t)blk * s->ada_np;
-        if (qkvg_impl(ctx, x, M, s->qkvg[blk], s->q, s->k, s->v, s->g, rm & 1)) return -1;
-        if (linear_gated_impl(ctx, s->v, M, D, s->wo[blk], rm & 2, nullptr, 0, x, mod + 2 * D,
-                              ldm, S))
-            return -1;
-        if (swiglu_impl(ctx, x, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, s->hidden, nullptr, x,
-                        mod + 5 * D, ldm, S))
+        if (site_qkvg(s, blk, x, M) || site_wo(s, blk, s->v, M, x, mod + 2 * D, ldm, S) ||
+            site_mlp(s, blk, x, M, x, mod + 5 * D, ldm, S))
             return -1;
     }
     return 0;
@@ -1025,6 +1177,7 @@ int iro_hip_dit_stack_create(IroHipContext *ctx, int blocks, int D, int H, int r
     s->wo.assign(blocks, nullptr);
     s->w13.assign(blocks, nullptr);
     s->w2.assign(blocks, nullptr);
+    s->f32w.assign(blocks, IroHipDiTStack::F32Weights{});
     *out = s;
     return 0;
 }
@@ -1055,8 +1208,36 @@ int iro_hip_dit_stack_set_block(IroHipDiTStack *s, int block, const float *ada, 
         for (IroHipWeight *w : {na, nq, no, n13, n2}) iro_hip_weight_destroy(w);
         return -1;
     }
+    // fp32 copies of the groups the int8 mask sends to the fp32 linear
+    IroHipDiTStack::F32Weights f;
+    const int mask = s->int8_mask;
+    const struct {
+        float **dst;
+        const float *src;
+        size_t n;
+        int bit;
+    } keep[8] = {{&f.wq, wq, (size_t)D * D, 1},  {&f.wk, wk, (size_t)D * D, 1},
+                 {&f.wv, wv, (size_t)D * D, 1},  {&f.wg, wgate, (size_t)D * D, 1},
+                 {&f.wo, wo, (size_t)D * D, 2},  {&f.w1, w1, (size_t)H * D, 4},
+                 {&f.w3, w3, (size_t)H * D, 4},  {&f.w2, w2, (size_t)D * H, 8}};
+    hipError_t e = hipSuccess;
+    for (const auto &k : keep) {
+        if (mask & k.bit || e != hipSuccess) continue;
+        e = hipMalloc(k.dst, sizeof(float) * k.n);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(*k.dst, k.src, sizeof(float) * k.n, hipMemcpyDeviceToDevice,
+                               ctx->stream);
+    }
+    if (e != hipSuccess) {
+        f32_weights_free(f);
+        for (IroHipWeight *w : {na, nq, no, n13, n2}) iro_hip_weight_destroy(w);
+        return set_error(ctx, "dit_stack: fp32 weight copy failed: %s", hipGetErrorString(e));
+    }
     if (na) iro_hip_weight_destroy(na);  // drains the stream: its rows are copied
     for (auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2}) iro_hip_weight_destroy((*v)[block]);
+    f32_weights_free(s->f32w[block]);
+    s->f32w[block] = f;
+    s->any_set = 1;
     s->qkvg[block] = nq;
     s->wo[block] = no;
     s->w13[block] = n13;
@@ -1136,27 +1317,23 @@ int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int 
         return set_error(s ? s->ctx : nullptr, "dit_block_forward: invalid arguments");
     IroHipContext *ctx = s->ctx;
     if (!s->w_set[block]) return set_error(ctx, "dit_block_forward: block %d has no weights", block);
-    const int M = B * S, D = s->D, rm = s->residual_mask;
+    const int M = B * S, D = s->D;
     if (stack_reserve(s, M, B)) return -1;
     const size_t BD = (size_t)B * D;
     // dit.c:1003-1006: h = RMSNorm-modulate(x) with the attention shift/scale.
     if (iro_hip_dit_adaln_apply(ctx, x, B, S, D, ada_attn, ada_attn + BD, eps, s->h)) return -1;
     // dit.c:785-792: one quantization of h, Q/K/V/gate from the fused weight.
-    if (qkvg_impl(ctx, s->h, M, s->qkvg[block], s->q, s->k, s->v, s->g, rm & 1)) return -1;
+    if (site_qkvg(s, block, s->h, M)) return -1;
     // dit.c:803, 808-870, 872: norm + RoPE, attention core, sigmoid gate.
     if (iro_hip_dit_qk_norm_rope(ctx, s->q, q_norm, s->k, k_norm, B, S, D, eps)) return -1;
     if (iro_hip_dit_attention(ctx, actx, s->q, s->k, s->v, s->g, B, S, D, context_k, context_v,
                               s->mix))
         return -1;
     // dit.c:878-881, 1012-1020: Wo, then x += gate * branch.
-    if (linear_gated_impl(ctx, s->mix, M, D, s->wo[block], rm & 2, nullptr, 0, x,
-                          ada_attn + 2 * BD, D, S))
-        return -1;
+    if (site_wo(s, block, s->mix, M, x, ada_attn + 2 * BD, D, S)) return -1;
     // dit.c:1022-1039: the MLP half.
     if (iro_hip_dit_adaln_apply(ctx, x, B, S, D, ada_mlp, ada_mlp + BD, eps, s->h)) return -1;
-    if (swiglu_impl(ctx, s->h, M, s->w13[block], s->w2[block], rm & 4, rm & 8, s->hidden, nullptr,
-                    x, ada_mlp + 2 * BD, D, S))
-        return -1;
+    if (site_mlp(s, block, s->h, M, x, ada_mlp + 2 * BD, D, S)) return -1;
     return ctx->has_err ? -1 : 0;
 }
 
@@ -1169,6 +1346,7 @@ int iro_hip_dit_stack_set_layer_f32(IroHipDiTStack *s, int layer, const IroHipDi
         return set_error(s->ctx, "dit_stack_set_layer_f32: NULL norm or context array");
     s->f32[layer] = *p;
     s->f32_set[layer] = 1;
+    s->sgraph.drop();  // a captured step holds the previous pointers
     return 0;
 }
 
@@ -1178,6 +1356,7 @@ int iro_hip_dit_stack_set_head(IroHipDiTStack *s, const IroHipDiTHead *head) {
         return set_error(s ? s->ctx : nullptr, "dit_stack_set_head: invalid arguments");
     s->head = *head;
     s->head_set = 1;
+    s->sgraph.drop();
     return 0;
 }
 
@@ -1212,23 +1391,30 @@ int iro_hip_dit_sampler_step(IroHipDiTStack *s, float *state, const float *cond,
     const IroHipDiTHead &hd = s->head;
     const int D = s->D, M = batch * S;
     if (stack_reserve(s, M, batch)) return -1;
-    if (iro_hip_linear_f32(ctx, state, S, hd.latent, hd.in_w, D, hd.in_b, s->proj)) return -1;
-    const size_t rows = sizeof(float) * (size_t)S * D;
-    for (int b = 1; b < batch; ++b)
-        IRO_HIP_TRY(ctx, hipMemcpyAsync(s->proj + (size_t)b * S * D, s->proj, rows,
-                                        hipMemcpyDeviceToDevice, ctx->stream));
-    const size_t BD = (size_t)batch * D;
-    for (int l = 0; l < s->blocks; ++l) {
-        const IroHipDiTLayerF32 &p = s->f32[l];
-        if (iro_hip_dit_adaln_params(ctx, cond, batch, D, hd.rank, p.adaln, 2, s->params))
-            return -1;
-        if (iro_hip_dit_stack_block_forward(s, l, s->proj, batch, S, s->params,
-                                            s->params + 3 * BD, p.q_norm, p.k_norm, hd.eps, actx,
-                                            p.context_k, p.context_v))
-            return -1;
-    }
-    if (iro_hip_rmsnorm_f32(ctx, s->proj, M, D, hd.out_norm, hd.eps, s->h)) return -1;
-    if (iro_hip_linear_f32(ctx, s->h, M, D, hd.out_w, hd.latent, hd.out_b, velocity)) return -1;
+    auto forward = [&]() -> int {
+        if (iro_hip_linear_f32(ctx, state, S, hd.latent, hd.in_w, D, hd.in_b, s->proj)) return -1;
+        const size_t rows = sizeof(float) * (size_t)S * D;
+        for (int b = 1; b < batch; ++b)
+            IRO_HIP_TRY(ctx, hipMemcpyAsync(s->proj + (size_t)b * S * D, s->proj, rows,
+                                            hipMemcpyDeviceToDevice, ctx->stream));
+        const size_t BD = (size_t)batch * D;
+        for (int l = 0; l < s->blocks; ++l) {
+            const IroHipDiTLayerF32 &p = s->f32[l];
+            if (iro_hip_dit_adaln_params(ctx, cond, batch, D, hd.rank, p.adaln, 2, s->params))
+                return -1;
+            if (iro_hip_dit_stack_block_forward(s, l, s->proj, batch, S, s->params,
+                                                s->params + 3 * BD, p.q_norm, p.k_norm, hd.eps,
+                                                actx, p.context_k, p.context_v))
+                return -1;
+        }
+        if (iro_hip_rmsnorm_f32(ctx, s->proj, M, D, hd.out_norm, hd.eps, s->h)) return -1;
+        return iro_hip_linear_f32(ctx, s->h, M, D, hd.out_w, hd.latent, hd.out_b, velocity);
+    };
+    const std::vector<long long> key = {(long long)(uintptr_t)state, (long long)(uintptr_t)cond,
+                                        batch, S, (long long)(uintptr_t)actx,
+                                        (long long)(uintptr_t)velocity};
+    if (graph_step(ctx, s->sgraph, s->use_graph != 0, key, forward) || ctx->has_err) return -1;
+    // sampler.c:281-297, outside the graph: its scalars change every step.
     if (iro_hip_euler_update(ctx, state, velocity, S * hd.latent, batch, use_cfg, text_row,
                              speaker_row, caption_row, scale_text, scale_speaker, scale_caption,
                              dt))
@@ -1250,6 +1436,17 @@ int iro_hip_dit_stack_use_persistent(IroHipDiTStack *s, int on) {
     stack_drop_graph(s);
     return 0;
 }
+
+int iro_hip_dit_stack_set_int8_mask(IroHipDiTStack *s, int mask) {
+    if (!s) return -1;
+    if (mask < 0 || mask > 15) return set_error(s->ctx, "dit_stack: int8 mask %d outside 0..15", mask);
+    if (s->any_set && mask != s->int8_mask)
+        return set_error(s->ctx, "dit_stack: set the int8 mask before the blocks' weights");
+    s->int8_mask = mask;
+    return 0;
+}
+
+int iro_hip_dit_stack_get_int8_mask(const IroHipDiTStack *s) { return s ? s->int8_mask : -1; }
 
 size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s) {
     if (!s) return 0;
@@ -1286,6 +1483,7 @@ void iro_hip_dit_stack_destroy(IroHipDiTStack *s) {
     iro_hip_weight_destroy(s->ada_all);
     for (auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2})
         for (IroHipWeight *w : *v) iro_hip_weight_destroy(w);
+    for (auto &f : s->f32w) f32_weights_free(f);
     stack_free_acts(s);
     delete s;
 }

@@ -160,6 +160,10 @@ int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long l
 int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const int32_t *colsum,
                 const int32_t *rowsum, IroHipWeight *w);
 int launch_fill(IroHipContext *ctx, void *dst, int value, size_t bytes);
+// iro_engine.hip: x = silu(x) [* g] (ops.c:776-784) and x += gate[m / S] * branch.
+int launch_silu(IroHipContext *ctx, float *x, const float *g, long long n);
+int launch_gated_residual(IroHipContext *ctx, float *x, const float *gate, int ldg,
+                          const float *branch, int M, int D, int S);
 
 // A zeroed layout-0 weight of N x K, and a copy of a whole layout-0 weight
 // into its rows row0 .. row0 + src->Np (row0 a multiple of 32): several

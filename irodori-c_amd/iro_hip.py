@@ -168,6 +168,12 @@ def load() -> C.CDLL:
                                   C.POINTER(C.c_double)], _i),
         "iro_hip_selfcheck": ([_vp], _i),
         "iro_hip_snake": ([_vp, _vp, _i, _i, _vp, _vp], _i),
+        "iro_hip_silu": ([_vp, _vp, _vp, C.c_longlong], _i),
+        "iro_hip_gated_residual": ([_vp, _vp, _vp, _i, _vp, _i, _i, _i], _i),
+        "iro_hip_dit_condition": ([_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
+        "iro_hip_dit_stack_set_int8_mask": ([_vp, _i], _i),
+        "iro_hip_dit_stack_get_int8_mask": ([_vp], _i),
+        "iro_hip_selfcheck_inject_fault": ([_i], _i),
         "iro_hip_snake_bias": ([_vp, _vp, _i, _i, _vp, _vp, _vp], _i),
         "iro_hip_selfcheck_sincosf": ([_vp, C.POINTER(C.c_ulonglong),
                                        C.POINTER(C.c_ulonglong)], _i),
@@ -651,6 +657,22 @@ class Context:
             int(bool(residual)), out.vp), "conv1x1_skip_int8")
 
 
+    # -- fp32 pieces around the int8 linears -------------------------------------------
+    def silu(self, x, n, gate=None):
+        """ops.c:776-784 in place: x = silu(x) [* gate]."""
+        self._check(self.lib.iro_hip_silu(self.h, x.vp, None if gate is None else gate.vp, n),
+                    "silu")
+
+    def gated_residual(self, x, gate, ldg, branch, M, D, S):
+        """dit.c:1013-1020: x += gate[m / S] * branch."""
+        self._check(self.lib.iro_hip_gated_residual(self.h, x.vp, gate.vp, ldg, branch.vp, M, D,
+                                                    S), "gated_residual")
+
+    def dit_condition(self, t, B, w0, w1, w2, tdim, D, cond_dim, cond):
+        """iro_dit_condition (dit.c:488-530) into cond [B, cond_dim]."""
+        self._check(self.lib.iro_hip_dit_condition(self.h, t.vp, B, w0.vp, w1.vp, w2.vp, tdim, D,
+                                                   cond_dim, cond.vp), "dit_condition")
+
     # -- codec ---------------------------------------------------------------------------
     def snake(self, x, T, Cc, alpha, y):
         """iro_snake_forward (dacvae.c:830-857); y may be x."""
@@ -764,6 +786,11 @@ class DiTStack:
             self.h, state.vp, cond.vp, batch, S, actx.h, int(bool(use_cfg)),
             *[int(r) for r in rows], *[float(x) for x in scales], float(dt), velocity.vp),
             "dit_sampler_step")
+
+    def set_int8_mask(self, mask: int):
+        """IRO_INT8_MASK (dit.c:273-291); before the first set_block."""
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_set_int8_mask(self.h, mask),
+                        "dit_stack_set_int8_mask")
 
     def use_persistent(self, on: bool):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_use_persistent(self.h, int(bool(on))),

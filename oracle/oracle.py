@@ -366,6 +366,32 @@ class Oracle:
         return y
 
 
+    def dit_condition(self, w0, w1, w2, t):
+        """iro_dit_condition (dit.c:488-530) composed from the restated pieces:
+        the timestep embedding with the restated expf, cosf and sinf in the
+        reference's op order, then linear / SiLU / linear / SiLU / linear
+        (the scalar linear, no biases)."""
+        L = self.lib
+        w0, w1, w2 = _f32(w0), _f32(w1), _f32(w2)
+        t = _f32(t).reshape(-1)
+        B, tdim = t.shape[0], w0.shape[1]
+        half = tdim // 2
+        log_theta = np.float32(float.fromhex("0x1.26bb1cp+3"))  # logf(10000.0f)
+        emb = np.empty((B, tdim), np.float32)
+        for i in range(half):
+            e = (np.float32(-log_theta) * np.float32(i)) / np.float32(half)
+            freq = np.float32(1000.0) * np.float32(L.orc_expf_restated(float(e)))
+            for b in range(B):
+                arg = np.float32(t[b] * freq)
+                emb[b, i] = L.orc_cosf(float(arg))
+                emb[b, half + i] = L.orc_sinf(float(arg))
+        ones = np.ones(1, np.float32)
+        h0 = self.linear_f32(emb, w0)
+        h0 = self.silu_mul(h0, np.broadcast_to(ones, h0.shape))
+        h1 = self.linear_f32(h0, w1)
+        h1 = self.silu_mul(h1, np.broadcast_to(ones, h1.shape))
+        return self.linear_f32(h1, w2)
+
     def sincosf_mismatches(self, which):
         """Inputs (of all 2^32) where the restated sinf (0) / cosf (1) differs from libm."""
         return self.lib.orc_sincosf_mismatches(which, self.threads)
@@ -772,6 +798,20 @@ class Reference:
         assert rc == 0
         return y
 
+
+    def dit_condition(self, w0, w1, w2, t):
+        """iro_dit_condition (dit.c:501-530) of this build."""
+        t = _f32(t).reshape(-1)
+        dims = (C.c_int * 3)()
+        self.lib.ref_dit_condition.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_int, _f32p,
+                                               C.POINTER(C.c_int)]
+        self.lib.ref_dit_condition.restype = C.c_int
+        cond = np.empty((t.shape[0], np.asarray(w2).shape[0]), np.float32)
+        rc = self.lib.ref_dit_condition(_p(_f32(w0), _f32p), _p(_f32(w1), _f32p),
+                                        _p(_f32(w2), _f32p), _p(t, _f32p), t.shape[0],
+                                        _p(cond, _f32p), dims)
+        assert rc == 0 and dims[2] == cond.shape[1], (rc, list(dims))
+        return cond
 
     def snake(self, x, alpha, inplace=False):
         """iro_snake_forward (dacvae.c:830-857), out of place or in place."""

@@ -232,3 +232,21 @@ int ref_dit_context_kv(int kind, const float *in, const float *wk, const float *
     *in_dim = SPEAKER_DIM;
     return iro_dit_speaker_kv(&a, eps, in, B, T, k, v);
 }
+
+/* iro_dit_condition (dit.c:501-530) with only the conditioner weights set:
+   w0 [MODEL_DIM, TIMESTEP_DIM], w1 [MODEL_DIM, MODEL_DIM], w2 [COND_DIM,
+   MODEL_DIM]; cond [B, COND_DIM].  dims: TIMESTEP_DIM, MODEL_DIM, COND_DIM. */
+int ref_dit_condition(const float *w0, const float *w1, const float *w2, const float *t, int B,
+                      float *cond, int *dims) {
+    IroDiT *d = calloc(1, sizeof(IroDiT));
+    if (!d) return -1;
+    d->cond_w0 = w0;
+    d->cond_w1 = w1;
+    d->cond_w2 = w2;
+    const int rc = iro_dit_condition(d, t, B, cond);
+    free(d);
+    dims[0] = TIMESTEP_DIM;
+    dims[1] = MODEL_DIM;
+    dims[2] = COND_DIM;
+    return rc;
+}

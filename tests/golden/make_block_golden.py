@@ -7,8 +7,13 @@ Every weight is seeded, the adaLN low-rank ones included; the fixture stores
 the block's output x, the six adaLN parameter rows per batch that the
 oracle's restatement of dit.c:543-588 gives (checked against the same
 reference build in tests/test_oracle_pins.py), and a SHA-256 digest of the
-seeded inputs that block_inputs() regenerates bit for bit.  Re-run after
-changing the case:
+seeded inputs that block_inputs() regenerates bit for bit.
+
+It also writes tests/golden/dit_block_mask_ref.npz: the same block under the
+reference's diagnostic group mask IRO_INT8_MASK (dit.c:273-291, read once
+per process, so each mask runs in a child process with the variable set),
+for MASKS: all groups fp32, and two mixes that put every group through both
+of its paths.  Re-run after changing the case:
 
     python tests/golden/make_block_golden.py
 """
@@ -26,6 +31,7 @@ sys.path.insert(0, os.path.join(REPO, "irodori-c_amd"))
 from iro_synth import gauss  # noqa: E402
 
 D, H, R = 1280, 3680, 192   # MODEL_DIM, MLP_DIM, ADALN_RANK of dit.c:12-20
+MASKS = (0, 5, 10)
 B, S, C = 2, 24, 9
 EPS = 1e-6
 
@@ -57,9 +63,31 @@ def block_inputs():
     return x, cond, ada, w, ck, cv, mask
 
 
+def block_under_mask(out_path):
+    """Child process: the block with the IRO_INT8_MASK of the environment."""
+    from oracle import Reference
+    x, cond, ada, w, ck, cv, mask = block_inputs()
+    y = Reference("strict").dit_block(x, cond, ada, w, ck, cv, mask, B, S, EPS, use_int8=True)
+    np.save(out_path, y)
+
+
 def main():
+    import subprocess
+    import tempfile
     from oracle import Oracle, Reference
     x, cond, ada, w, ck, cv, mask = block_inputs()
+    outs = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        for m in MASKS:
+            path = os.path.join(tmp, f"mask{m}.npy")
+            env = dict(os.environ, IRO_INT8_MASK=str(m))
+            subprocess.run([sys.executable, os.path.abspath(__file__), "--mask-child", path],
+                           env=env, check=True)
+            outs[f"x_out_mask{m}"] = np.load(path)
+    mpath = os.path.join(HERE, "dit_block_mask_ref.npz")
+    np.savez_compressed(mpath, masks=np.array(MASKS), inputs_sha256=np.array(
+        input_digest(x, cond, ada, w, ck, cv)), **outs)
+    print(f"wrote {mpath}: masks {MASKS}")
     ref = Reference("strict")
     y = ref.dit_block(x, cond, ada, w, ck, cv, mask, B, S, EPS, use_int8=True)
     o = Oracle()
@@ -72,4 +100,7 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) == 3 and sys.argv[1] == "--mask-child":
+        block_under_mask(sys.argv[2])
+    else:
+        main()
