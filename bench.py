@@ -1112,6 +1112,51 @@ def main():
     log(f"stack: {ms_step:.3f} ms/step wall, {ev_ms / args.steps:.3f} ms/step events, "
         f"x finite: {finite}")
 
+    # The reference sampler's schedule (sampler.c:247-250): CFG steps run the
+    # B branches, plain steps (t below the CFG window) one branch of S rows.
+    # Each shape keeps its own captured graph.
+    x1_init = ctx.to_device(x0[:S])
+    x1 = ctx.to_device(x0[:S])
+    c1 = ctx.to_device(cond[:1])
+
+    def step1():
+        ctx.copy(x1, x1_init)
+        stack.step(x1, c1, 1, S)
+
+    for _ in range(args.warmup):
+        step1()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step1()
+    ctx.sync()
+    ms_b1 = (time.perf_counter() - t0) * 1e3 / args.steps
+    ops_b1 = stack_ops(args.blocks, 1, S, D, H, rm)
+    reps = max(1, args.steps // 4)
+    for _ in range(4):
+        step()
+    for _ in range(4):
+        step1()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for _ in range(4):
+            step()
+        for _ in range(4):
+            step1()
+    ctx.sync()
+    ms_sched = (time.perf_counter() - t0) * 1e3 / reps
+    schedule = {
+        "m_cfg_rows": M, "m_cfg_ms_per_step": round(ms_step, 4),
+        "m_plain_rows": S, "m_plain_ms_per_step": round(ms_b1, 4),
+        "m_plain_tops": round(ops_b1 / ms_b1 / 1e9, 2),
+        "eight_step_ms": round(ms_sched, 4),
+        "eight_step_tops": round((4 * ops + 4 * ops_b1) / ms_sched / 1e9, 2),
+        "note": ("4 CFG steps at M=B*S then 4 plain steps at M=S, as the reference "
+                 "sampler's default CFG window gives (sampler.c:247-250); graph replay"),
+    }
+    log(f"schedule: plain M={S} {ms_b1:.3f} ms/step, 8 steps {ms_sched:.3f} ms")
+
     # Per-kernel durations on the stack's stream (HIP events), after the
     # timed region.
     ctx.profile(True)
@@ -1155,6 +1200,7 @@ def main():
             "resident_int8_bytes": stack_bytes, "parallelism": "single GPU",
         },
         "roofline": roof,
+        "schedule": schedule,
         "kernels": kernels,
         "kernels_source": ("per-kernel HIP events around each launch of directly launched "
                            "(not graph-replayed) steps after the timed region"),

@@ -646,7 +646,8 @@ int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w
 // the same; the first call with new arguments runs eagerly (sizing every
 // buffer), the second captures.
 struct GraphCache {
-    std::vector<long long> key;
+    std::vector<long long> args;
+    unsigned epoch = 0;  // the workspace epoch the launches were recorded at
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int seen = 0;
@@ -656,6 +657,25 @@ struct GraphCache {
         exec = nullptr;
         graph = nullptr;
         seen = 0;
+        args.clear();
+    }
+};
+
+// A few graph caches for alternating argument sets (a sampler's CFG steps
+// at batch 3 and its plain steps at batch 1): the slot holding the same
+// arguments, else a free one, else the oldest.
+struct GraphSet {
+    GraphCache slot[4];
+    int next = 0;
+    GraphCache &pick(const std::vector<long long> &args) {
+        for (GraphCache &g : slot)
+            if (g.seen && g.args == args) return g;
+        for (GraphCache &g : slot)
+            if (!g.seen) return g;
+        return slot[next++ & 3];
+    }
+    void drop() {
+        for (GraphCache &g : slot) g.drop();
     }
 };
 
@@ -704,18 +724,11 @@ struct IroHipDiTStack {
     std::vector<char> f32_set;
     IroHipDiTHead head{};
     int head_set = 0;
-    // graph of the last step's launches
+    // graphs of the linear-stack step, and of the sampler step's network
+    // forward (its CFG / Euler update, whose scalars change every step, is
+    // launched after it), per argument set
     int use_graph = 1;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t gexec = nullptr;
-    float *gx = nullptr;
-    const float *gcond = nullptr;
-    int gB = 0, gS = 0;
-    unsigned gepoch = 0;
-    int seen = 0;  // the last eager step had these arguments
-    // graph of the last sampler step's network forward (its CFG / Euler
-    // update, whose scalars change every step, is launched after it)
-    GraphCache sgraph;
+    GraphSet graphs, sgraphs;
     // the persistent kernel of the step (iro_persist.hip)
     int use_persist = 0;
     iro::PersistPlan *persist = nullptr;
@@ -736,13 +749,9 @@ void stack_free_acts(IroHipDiTStack *s) {
 }
 
 void stack_drop_graph(IroHipDiTStack *s) {
-    if (s->gexec) (void)hipGraphExecDestroy(s->gexec);
-    if (s->graph) (void)hipGraphDestroy(s->graph);
-    s->gexec = nullptr;
-    s->graph = nullptr;
-    s->seen = 0;
+    s->graphs.drop();
+    s->sgraphs.drop();
     s->persist_M = s->persist_S = 0;  // weights or buffers may have changed
-    s->sgraph.drop();
 }
 
 void f32_weights_free(IroHipDiTStack::F32Weights &f) {
@@ -760,6 +769,7 @@ bool stack_persistent(const IroHipDiTStack *s) {
 int stack_persist_prepare(IroHipDiTStack *s, int B, int S) {
     const int M = B * S;
     if (s->persist_M == M && s->persist_S == S) return 0;
+    s->graphs.drop();  // captured steps hold the previous plan's buffers
     std::vector<const IroHipWeight *> ws;
     for (int b = 0; b < s->blocks; ++b)
         for (const auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2}) ws.push_back((*v)[b]);
@@ -806,22 +816,22 @@ int stack_reserve(IroHipDiTStack *s, int M, int B) {
 // the same key (the arguments plus the workspace epoch), runs eagerly the
 // first time a key is seen and captures on the second.
 template <class F>
-int graph_step(IroHipContext *ctx, GraphCache &gc, bool use, std::vector<long long> key,
+int graph_step(IroHipContext *ctx, GraphSet &set, bool use, const std::vector<long long> &args,
                F &&launch) {
-    key.push_back((long long)ctx->ws_epoch);
     if (!use || ctx->prof) {
-        gc.drop();
+        set.drop();
         return launch();
     }
-    if (gc.exec && key == gc.key) {
+    GraphCache &gc = set.pick(args);
+    if (gc.exec && gc.args == args && gc.epoch == ctx->ws_epoch) {
         IRO_HIP_TRY(ctx, hipGraphLaunch(gc.exec, ctx->stream));
         return 0;
     }
-    if (key != gc.key || !gc.seen) {
+    if (gc.args != args || !gc.seen || gc.epoch != ctx->ws_epoch) {
         gc.drop();
         if (launch()) return -1;
-        key.back() = (long long)ctx->ws_epoch;  // the eager run sized the workspace
-        gc.key = key;
+        gc.args = args;
+        gc.epoch = ctx->ws_epoch;  // after the eager run sized the workspace
         gc.seen = 1;
         return 0;
     }
@@ -829,7 +839,7 @@ int graph_step(IroHipContext *ctx, GraphCache &gc, bool use, std::vector<long lo
     const int rc = launch();
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
-    if (rc || e != hipSuccess || !graph || (long long)ctx->ws_epoch != key.back()) {
+    if (rc || e != hipSuccess || !graph || ctx->ws_epoch != gc.epoch) {
         if (graph) (void)hipGraphDestroy(graph);
         gc.drop();
         return set_error(ctx, "graph capture failed (%s)",
@@ -1262,49 +1272,13 @@ int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B
             return set_error(ctx, "dit_stack: block %d has no weights or no modulation weight", b);
     if (stack_reserve(s, B * S, B)) return -1;
     if (stack_persistent(s) && stack_persist_prepare(s, B, S)) return -1;
-    const bool same = s->gx == x && s->gcond == cond && s->gB == B && s->gS == S &&
-                      s->gepoch == ctx->ws_epoch;
-    if (!s->use_graph || ctx->prof) {
-        stack_drop_graph(s);
-        return stack_launch(s, x, cond, B, S) || ctx->has_err ? -1 : 0;
-    }
-    if (same && s->gexec) {
-        IRO_HIP_TRY(ctx, hipGraphLaunch(s->gexec, ctx->stream));
-        return ctx->has_err ? -1 : 0;
-    }
-    if (!same || !s->seen) {
-        // First step with these buffers: run it directly (this sizes the
-        // workspace), capture on the next one.
-        stack_drop_graph(s);
-        if (stack_launch(s, x, cond, B, S) || ctx->has_err) return -1;
-        s->gx = x;
-        s->gcond = cond;
-        s->gB = B;
-        s->gS = S;
-        s->gepoch = ctx->ws_epoch;
-        s->seen = 1;
-        return 0;
-    }
-    IRO_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    const int rc = stack_launch(s, x, cond, B, S);
-    hipGraph_t graph = nullptr;
-    const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
-    if (rc || e != hipSuccess || !graph || s->gepoch != ctx->ws_epoch) {
-        if (graph) (void)hipGraphDestroy(graph);
-        stack_drop_graph(s);
-        return set_error(ctx, "dit_stack: graph capture failed (%s)",
-                         e != hipSuccess ? hipGetErrorString(e) : "a launch failed");
-    }
-    hipGraphExec_t exec = nullptr;
-    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    if (ei != hipSuccess) {
-        (void)hipGraphDestroy(graph);
-        return set_error(ctx, "dit_stack: graph instantiate failed: %s", hipGetErrorString(ei));
-    }
-    s->graph = graph;
-    s->gexec = exec;
-    IRO_HIP_TRY(ctx, hipGraphLaunch(s->gexec, ctx->stream));
-    return ctx->has_err ? -1 : 0;
+    const std::vector<long long> args = {(long long)(uintptr_t)x, (long long)(uintptr_t)cond, B,
+                                         S};
+    return graph_step(ctx, s->graphs, s->use_graph != 0, args,
+                      [&]() { return stack_launch(s, x, cond, B, S); }) ||
+                   ctx->has_err
+               ? -1
+               : 0;
 }
 
 int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int B, int S,
@@ -1346,7 +1320,7 @@ int iro_hip_dit_stack_set_layer_f32(IroHipDiTStack *s, int layer, const IroHipDi
         return set_error(s->ctx, "dit_stack_set_layer_f32: NULL norm or context array");
     s->f32[layer] = *p;
     s->f32_set[layer] = 1;
-    s->sgraph.drop();  // a captured step holds the previous pointers
+    s->sgraphs.drop();  // a captured step holds the previous pointers
     return 0;
 }
 
@@ -1356,7 +1330,7 @@ int iro_hip_dit_stack_set_head(IroHipDiTStack *s, const IroHipDiTHead *head) {
         return set_error(s ? s->ctx : nullptr, "dit_stack_set_head: invalid arguments");
     s->head = *head;
     s->head_set = 1;
-    s->sgraph.drop();
+    s->sgraphs.drop();
     return 0;
 }
 
@@ -1413,7 +1387,7 @@ int iro_hip_dit_sampler_step(IroHipDiTStack *s, float *state, const float *cond,
     const std::vector<long long> key = {(long long)(uintptr_t)state, (long long)(uintptr_t)cond,
                                         batch, S, (long long)(uintptr_t)actx,
                                         (long long)(uintptr_t)velocity};
-    if (graph_step(ctx, s->sgraph, s->use_graph != 0, key, forward) || ctx->has_err) return -1;
+    if (graph_step(ctx, s->sgraphs, s->use_graph != 0, key, forward) || ctx->has_err) return -1;
     // sampler.c:281-297, outside the graph: its scalars change every step.
     if (iro_hip_euler_update(ctx, state, velocity, S * hd.latent, batch, use_cfg, text_row,
                              speaker_row, caption_row, scale_text, scale_speaker, scale_caption,
