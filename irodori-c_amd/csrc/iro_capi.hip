@@ -375,6 +375,12 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
         ctx->gemm_lds = tj;
         return 0;
     }
+    if (ti == -5) {  // tj: rows per whole-tile block, 0 per GEMM, 64 or 128
+        if (tj != 0 && tj != 64 && tj != 128)
+            return set_error(ctx, "set_gemm_tile: whole-tile rows 0, 64 or 128");
+        ctx->gemm_wt_rows = tj;
+        return 0;
+    }
     if (ti == 0 && tj == 0) {
         ctx->gemm_tile = 0;
         return 0;

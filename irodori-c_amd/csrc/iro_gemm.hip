@@ -325,10 +325,11 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel_o2(KParams p) {
 // k past K is copied from a zero page.  The accumulators start at
 // 128 * rowsum[n] (the signed-operand correction), so they end as the
 // reference's raw u8 x s8 sums.
-template <int CONV, int EPI, int TJ, int R>
-__global__ __launch_bounds__(256, (EPI == EPI_QKVG || EPI == EPI_SWIGLU) ? 2 : 1) void gemm_wt_kernel(KParams p) {
-    constexpr int TI = 2, BM = 64, KMAX = 1024;
-    constexpr int P = R / 2;  // activation pieces per thread per ring turn (a piece spans 2 k blocks)
+template <int CONV, int EPI, int TJ, int R, int TI>
+__global__ __launch_bounds__(256, (TI == 2 && (EPI == EPI_QKVG || EPI == EPI_SWIGLU)) ? 2 : 1) void gemm_wt_kernel(KParams p) {
+    static_assert(TI == 2 || TI == 4, "64- or 128-row tiles");
+    constexpr int BM = 32 * TI, KMAX = 1024;
+    constexpr int P = R * TI / 4;  // activation pieces per thread per ring turn
     // Sweeping several slabs pays for the projections with the largest N
     // (QKVG, W1/W3); the others run one slab per block, which keeps their
     // epilogues' registers out of a loop.
@@ -355,21 +356,21 @@ __global__ __launch_bounds__(256, (EPI == EPI_QKVG || EPI == EPI_SWIGLU) ? 2 : 1
     const int nkb = (p.K + 31) / 32;             // k blocks holding activation data
     const int nkr = (nkb + R - 1) / R * R;       // whole ring turns (<= KMAX / 32)
     const int nturn = nkr / R;
-    // Piece q = tid + 256 i of the tile: fragment f = q / 64 = (k block,
-    // row block) = (f / 2, f % 2), lane q % 64.  For this thread the row is
-    // fixed and k advances by 64 per piece, so pieces t*P .. t*P+P-1 hold
-    // ring turn t's k blocks.  Turns past the last one load the zero page
-    // into a sink, which keeps the count of loads behind every turn's pieces
-    // the same.
-    int arow_i = m0 + (wave & 1) * 32 + (lane & 31);
+    // Piece q = tid + 256 i of the tile: fragment f = q / 64 = wave + 4 i =
+    // (k block, row block) = (f / TI, f % TI), lane q % 64.  For this thread
+    // the row block is wave % TI and k advances by 128 / TI per piece, so
+    // pieces t*P .. t*P+P-1 hold ring turn t's k blocks.  Turns past the
+    // last one load the zero page into a sink, which keeps the count of
+    // loads behind every turn's pieces the same.
+    int arow_i = m0 + (wave % TI) * 32 + (lane & 31);
     arow_i = arow_i < p.M ? arow_i : p.M - 1;
     const uint8_t *arow = p.a1 + (size_t)arow_i * p.lda;
-    const int k0 = (wave >> 1) * 32 + (lane >> 5) * 16;
+    const int k0 = (wave / TI) * 32 + (lane >> 5) * 16;
     auto copy_turn = [&](int t) {
 #pragma unroll
         for (int q = 0; q < P; ++q) {
             const int i = t * P + q;
-            const int k = k0 + 64 * i;
+            const int k = k0 + (128 / TI) * i;
             const bool real = t < nturn;
             const uint8_t *src = real && k < p.K ? arow + k : p.zero16;
             uint8_t *dst = real ? lds_a + (size_t)(tid - lane + 256 * i) * 16 : lds_sink;
@@ -588,13 +589,20 @@ void launch_tile(const KParams &kp, TileCfg t, unsigned grid, hipStream_t st) {
 enum Mode { MODE_TILE = 0, MODE_SKINNY = 1, MODE_WHOLE = 2 };
 
 template <int CONV, int EPI>
-void launch_wt(const KParams &kp, int tj, int ring, unsigned grid, hipStream_t st) {
-    if (tj == 1)
-        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 1, 8>), dim3(grid), dim3(256), 0, st, kp);
+void launch_wt(const KParams &kp, int ti, int tj, int ring, unsigned grid, hipStream_t st) {
+    if (ti == 4) {
+        if (tj == 1)
+            hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 1, 8, 4>), dim3(grid), dim3(256), 0, st,
+                               kp);
+        else
+            hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 4, 4>), dim3(grid), dim3(256), 0, st,
+                               kp);
+    } else if (tj == 1)
+        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 1, 8, 2>), dim3(grid), dim3(256), 0, st, kp);
     else if (ring == 8)
-        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 8>), dim3(grid), dim3(256), 0, st, kp);
+        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 8, 2>), dim3(grid), dim3(256), 0, st, kp);
     else
-        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 4>), dim3(grid), dim3(256), 0, st, kp);
+        hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 4, 2>), dim3(grid), dim3(256), 0, st, kp);
 }
 
 template <int CONV, int EPI>
@@ -608,7 +616,7 @@ void launch_e(const KParams &kp, bool two, Mode mode, TileCfg t, int ring, unsig
             hipLaunchKernelGGL((gemm_skinny_kernel<CONV, EPI, false>), dim3(grid), dim3(256), 0,
                                st, kp);
     } else if (mode == MODE_WHOLE) {
-        launch_wt<CONV, EPI>(kp, t.tj, ring, grid, st);
+        launch_wt<CONV, EPI>(kp, t.ti, t.tj, ring, grid, st);
     } else if (two) {
         launch_tile<CONV, EPI, true>(kp, t, grid, st);
     } else {
@@ -644,8 +652,12 @@ TileCfg choose_tile(int M, int Np, int cus, bool two, Epi epi, int forced) {
         return t;
     }
     const long long tiles22 = (long long)((M + 63) / 64) * (Np / 256);
-    if (two) return TileCfg{2, 2};
     if (epi == EPI_SWIGLU) return TileCfg{2, 2};
+    // Few rows (a plain sampler step, M = 750): 64 x 256 tiles would leave
+    // most CUs idle; 32-row tiles double the count (measured at M = 750:
+    // W2 two-term 22.6 us against 32.1, Wo 12.4 against 13.8).
+    if (tiles22 * 2 < cus) return TileCfg{1, 2};
+    if (two) return TileCfg{2, 2};
     return tiles22 >= cus ? TileCfg{2, 2} : TileCfg{2, 1};
 }
 
@@ -710,7 +722,14 @@ int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K) {
     // 23.2 us against 25.8 us for the register-streamed whole-tile kernel;
     // the W1/W3, Wo and W2 shapes ran slower through it).
     if (ctx->gemm_lds == 0 && epi != EPI_QKVG) return 0;
-    const int cfg = ctx->gemm_lds > 0 ? ctx->gemm_lds : LDS_192x256_CFG;
+    int cfg = ctx->gemm_lds > 0 ? ctx->gemm_lds : LDS_192x256_CFG;
+    // Few rows: 96 x 128 tiles keep every CU busy (measured at M = 750,
+    // N = 4096: 15.4 us against 22.0 for 192 x 256).
+    if (ctx->gemm_lds == 0) {
+        const int cus = ctx->cus > 0 ? ctx->cus : 256;
+        // the QKVG output is 4K wide: K / 64 column tiles of 256
+        if ((long long)((M + 191) / 192) * (K / 64) * 2 < cus) cfg = LDS_96x128_CFG;
+    }
     return lds_cfg_ok(cfg, two, epi) ? cfg : 0;
 }
 
@@ -806,7 +825,12 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
         if (two && t.ti * t.tj > 4) t.tj = 1;  // as launch_tile runs it
         // Signed single-plane codes with K <= 1024 fit a whole 64-row tile
         // in LDS: the barrier-free whole-tile kernel.
-        if (a.a_signed && !two && a.K <= 1024 && t.ti == 2) mode = MODE_WHOLE;
+        if (a.a_signed && !two && a.K <= 1024 && t.ti == 2) {
+            mode = MODE_WHOLE;
+            // 128-row tiles (one block per CU, the tile in 128 KiB of LDS)
+            // halve the weight stream per output against 64-row ones.
+            if (ctx->gemm_wt_rows == 128) t.ti = 4;
+        }
         kp.tiles_n = w->Np / (128 * t.tj);
         kp.tiles_m = (a.M + 32 * t.ti - 1) / (32 * t.ti);
         const int tiles = kp.tiles_n * kp.tiles_m;
@@ -826,6 +850,12 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
             // 29.5 us with two slabs at M = 2250, N = 4096, K = 1024).
             int spb = (epi == EPI_QKVG || epi == EPI_SWIGLU) ? ctx->gemm_spb : 1;
             if (spb <= 0 && epi == EPI_QKVG) spb = 1;
+            if (spb <= 0 && t.ti == 4) {
+                // one resident block per CU: the fewest slabs per block
+                // that give every item a CU
+                const int cus = ctx->cus > 0 ? ctx->cus : 256;
+                spb = (int)(((long long)kp.tiles_m * kp.tiles_n + cus - 1) / cus);
+            }
             if (spb <= 0) {
                 const int cus = ctx->cus > 0 ? ctx->cus : 256;
                 spb = 1;

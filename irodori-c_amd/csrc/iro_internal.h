@@ -59,6 +59,7 @@ struct IroHipContext {
     int gemm_ring = 0;    // weight ring depth of the whole-tile kernel (0: default)
     int gemm_spb = 0;     // column slabs per whole-tile block (0: chosen per GEMM)
     int gemm_lds = 0;     // LDS-pipelined GEMM: 0 shape chosen per GEMM, -1 off, > 0 forced shape
+    int gemm_wt_rows = 0; // rows per whole-tile block: 0 chosen per GEMM, 64 or 128
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
     float *rope = nullptr;  // rotation table: per position cos[32] then sin[32]
     int rope_S = 0;         // positions held by rope
