@@ -625,6 +625,11 @@ int iro_hip_selfcheck_inject_fault(int on);
    from the IEEE division (0 expected).  Takes well under a second. */
 int iro_hip_selfcheck_silu(IroHipContext *ctx, unsigned long long *exp_digest,
                            unsigned long long *div_mismatches);
+/* Exhaustive check of the code packing every activation quantizer uses
+   (no counterpart in the reference; a test hook): the number of float
+   inputs v whose packed u8 code differs from the reference's
+   clamp(nearbyintf(v), 0, 255) (NaN: 0).  0 expected. */
+int iro_hip_selfcheck_codes(IroHipContext *ctx, unsigned long long *mismatches);
 /* Exhaustive digests (same form) of the device's sqrtf(x) and 1 / x over all
    2^32 float inputs, to be compared with the host's IEEE results: the
    correctly rounded operations the adaLN apply relies on (no counterpart in

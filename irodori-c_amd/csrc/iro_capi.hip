@@ -375,6 +375,10 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
         ctx->gemm_lds = tj;
         return 0;
     }
+    if (ti == -6) {  // tj: 1 kernel-7 im2col in one pass (default), 0 the two-pass form
+        ctx->conv_fused = tj != 0;
+        return 0;
+    }
     if (ti == -5) {  // tj: rows per whole-tile block, 0 per GEMM, 64 or 128
         if (tj != 0 && tj != 64 && tj != 128)
             return set_error(ctx, "set_gemm_tile: whole-tile rows 0, 64 or 128");
@@ -731,10 +735,19 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
     uint8_t *c1 = ws.at<uint8_t>(oc1), *c2 = residual ? ws.at<uint8_t>(oc2) : nullptr;
     float *s1 = ws.at<float>(os1), *s2 = residual ? ws.at<float>(os2) : nullptr;
     int32_t *z1 = ws.at<int32_t>(oz1), *z2 = residual ? ws.at<int32_t>(oz2) : nullptr;
-    if (launch_conv_rows(ctx, input, T, C, lo, hi)) return -1;
-    if (launch_conv_im2col(ctx, input, T, C, T_out, kernel, stride, dilation, padding, lo, hi, c1,
-                           c2, ldc, s1, z1, s2, z2))
+    // The one-pass kernel can store the signed operand form the
+    // LDS-pipelined GEMM reads.
+    const bool fused = conv_im2col7_ok(C, kernel, ldc) && ctx->conv_fused;
+    const bool sgn = fused && gemm_lds_cfg(ctx, EPI_LINEAR, residual != 0, T_out, ldc) != 0;
+    if (fused) {
+        if (launch_conv_im2col7(ctx, input, T, C, T_out, stride, dilation, padding, c1, c2, ldc,
+                                s1, z1, s2, z2, sgn))
+            return -1;
+    } else if (launch_conv_rows(ctx, input, T, C, lo, hi) ||
+               launch_conv_im2col(ctx, input, T, C, T_out, kernel, stride, dilation, padding, lo,
+                                  hi, c1, c2, ldc, s1, z1, s2, z2)) {
         return -1;
+    }
     GemmArgs a;
     a.a1 = c1;
     a.a2 = c2;
@@ -745,6 +758,7 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
     a.zx2 = z2;
     a.M = T_out;
     a.K = ldc;
+    a.a_signed = sgn;
     a.bias = bias;
     a.y = output;
     a.ldy = w->N;
@@ -884,6 +898,20 @@ int iro_hip_selfcheck_fp32(IroHipContext *ctx, unsigned long long *sqrt_digest,
     if (rc) return -1;
     *sqrt_digest = h[0];
     *recip_digest = h[1];
+    return 0;
+}
+
+int iro_hip_selfcheck_codes(IroHipContext *ctx, unsigned long long *mismatches) {
+    if (!ctx || !mismatches) return -1;
+    void *buf = nullptr;
+    if (iro_hip_alloc(ctx, 8, &buf)) return -1;
+    unsigned long long h = 0;
+    int rc = iro_hip_upload(ctx, buf, &h, sizeof(h));
+    if (!rc) rc = launch_codes_selfcheck(ctx, static_cast<unsigned long long *>(buf));
+    if (!rc) rc = iro_hip_download(ctx, &h, buf, sizeof(h));
+    iro_hip_free(ctx, buf);
+    if (rc) return -1;
+    *mismatches = h;
     return 0;
 }
 

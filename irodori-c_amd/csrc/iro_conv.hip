@@ -62,6 +62,13 @@ __device__ __forceinline__ uint32_t plane2_code(float x, float v, const RowQ &r,
     return (uint32_t)v2;
 }
 
+// The same before rounding, for pack_codes4.
+template <int CONV>
+__device__ __forceinline__ float plane2_pre(float x, float v, const RowQ &r, float inv2) {
+    const float rem = residual_value<CONV>(x, v, r);
+    return CONV == 1 ? __builtin_fmaf(rem, inv2, 128.0f) : rem * inv2 + 128.0f;
+}
+
 template <int CONV, bool RES>
 __global__ __launch_bounds__(256) void conv_im2col_kernel(
     const float *__restrict__ x, int T, int C, int T_out, int kernel, int stride, int dilation,
@@ -132,6 +139,108 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(
             }
         }
     }
+    if (lane == 0) {
+        s1[r] = q.s;
+        z1[r] = q.zp;
+        if (RES) {
+            s2[r] = sc2;
+            z2[r] = 128;
+        }
+    }
+}
+
+// Kernel-7 convolutions with C <= 1024 (every Conv7 of the decoder) in one
+// pass: the wavefront of output step r loads its seven tap rows into
+// registers (CHN float4 per lane per tap, all loads in flight at once),
+// reduces the window's lo/hi itself -- min(0, window) and max(0, window)
+// equal the reference's min over the taps' row ranges (dacvae.c:607-627),
+// whatever the order, since both only select -- and codes the rows from
+// registers.  Taps outside [0, T) load nothing and hold the zero point.
+// flip: XOR applied to every stored code word (0x80808080 stores the
+// signed operand form a - 128 the LDS-pipelined GEMM reads, 0 keeps u8).
+// Workgroup w runs on XCD w % 8; XCD x takes the contiguous run of row
+// blocks x*per .. x*per + per - 1, so the tap rows neighbouring blocks
+// share are read through one L2.
+constexpr int kIm2colRows = 4;  // output steps (wavefronts) per workgroup
+
+template <int CONV, bool RES, int CHN>
+__global__ __launch_bounds__(64 * kIm2colRows) void conv_im2col7_kernel(
+    const float *__restrict__ x, int T, int C, int T_out, int stride, int dilation, int padding,
+    uint8_t *__restrict__ cols1, uint8_t *__restrict__ cols2, int ldc, float *__restrict__ s1,
+    int32_t *__restrict__ z1, float *__restrict__ s2, int32_t *__restrict__ z2, uint32_t flip,
+    int per) {
+    constexpr int KT = 7;
+    const int blk = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    const int r = blk * kIm2colRows + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= T_out) return;
+    float4 v[KT][CHN];
+    bool inside[KT];
+#pragma unroll
+    for (int tap = 0; tap < KT; ++tap) {
+        const int it = r * stride - padding + tap * dilation;
+        inside[tap] = it >= 0 && it < T;
+        const float *xr = x + (size_t)(inside[tap] ? it : 0) * C;
+#pragma unroll
+        for (int j = 0; j < CHN; ++j) {
+            const int c = j * 256 + lane * 4;
+            v[tap][j] = inside[tap] && c < C ? *reinterpret_cast<const float4 *>(xr + c)
+                                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int tap = 0; tap < KT; ++tap)
+#pragma unroll
+        for (int j = 0; j < CHN; ++j) {
+            const float4 e = v[tap][j];
+            lo = sel_min(lo, e.x); lo = sel_min(lo, e.y); lo = sel_min(lo, e.z); lo = sel_min(lo, e.w);
+            hi = sel_max(hi, e.x); hi = sel_max(hi, e.y); hi = sel_max(hi, e.z); hi = sel_max(hi, e.w);
+        }
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    const RowQ q = row_params<CONV>(lo, hi);
+    float sc2 = 0.0f, inv2 = 0.0f;
+    if (RES) {
+        if (CONV == 1) {
+            const float d = hi - lo;
+            sc2 = q.s * c_inv255();
+            inv2 = d * c_inv255() > 0.0f ? c_255_inv255_b() / d : 255.0f;
+        } else {
+            sc2 = q.s / 255.0f;
+            inv2 = 255.0f / q.s;
+        }
+    }
+    const uint32_t zp4 = (0x01010101u * (uint32_t)q.zp) ^ flip;
+    const uint32_t h4 = 0x80808080u ^ flip;
+    uint8_t *d1 = cols1 + (size_t)r * ldc;
+    uint8_t *d2 = RES ? cols2 + (size_t)r * ldc : nullptr;
+#pragma unroll
+    for (int tap = 0; tap < KT; ++tap)
+#pragma unroll
+        for (int j = 0; j < CHN; ++j) {
+            const int c = j * 256 + lane * 4;
+            if (c >= C) continue;
+            const size_t o = (size_t)tap * C + c;
+            if (!inside[tap]) {
+                *reinterpret_cast<uint32_t *>(d1 + o) = zp4;
+                if (RES) *reinterpret_cast<uint32_t *>(d2 + o) = h4;
+                continue;
+            }
+            const float4 e = v[tap][j];
+            const uint32_t w1 = pack_codes4(quant_pre<CONV>(e.x, q), quant_pre<CONV>(e.y, q),
+                                            quant_pre<CONV>(e.z, q), quant_pre<CONV>(e.w, q));
+            *reinterpret_cast<uint32_t *>(d1 + o) = w1 ^ flip;
+            if (RES) {
+                const float4 c4 = unpack_codes4(w1);
+                *reinterpret_cast<uint32_t *>(d2 + o) =
+                    pack_codes4(plane2_pre<CONV>(e.x, c4.x, q, inv2),
+                                plane2_pre<CONV>(e.y, c4.y, q, inv2),
+                                plane2_pre<CONV>(e.z, c4.z, q, inv2),
+                                plane2_pre<CONV>(e.w, c4.w, q, inv2)) ^
+                    flip;
+            }
+        }
     if (lane == 0) {
         s1[r] = q.s;
         z1[r] = q.zp;
@@ -213,6 +322,43 @@ int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo
                        hi);
     IRO_HIP_CHECK_LAUNCH(ctx);
     prof_end(ctx, PK_CONV_ROWS, 0, 4.0 * T * C + 8.0 * T);
+    return 0;
+}
+
+bool conv_im2col7_ok(int C, int kernel, int ldc) {
+    return kernel == 7 && C % 4 == 0 && C <= 1024 && ldc % 4 == 0;
+}
+
+int launch_conv_im2col7(IroHipContext *ctx, const float *x, int T, int C, int T_out, int stride,
+                        int dilation, int padding, uint8_t *cols1, uint8_t *cols2, int ldc,
+                        float *s1, int32_t *z1, float *s2, int32_t *z2, bool signed_codes) {
+    const uint32_t flip = signed_codes ? 0x80808080u : 0u;
+    const int per = ((T_out + kIm2colRows - 1) / kIm2colRows + 7) / 8;  // row blocks per XCD
+    const dim3 grid(8 * per), block(64 * kIm2colRows);
+    const bool res = cols2 != nullptr;
+    const int chn = (C + 255) / 256;
+    prof_begin(ctx);
+#define IRO_IM2COL7(CV, RS, CH)                                                                 \
+    hipLaunchKernelGGL((conv_im2col7_kernel<CV, RS, CH>), grid, block, 0, ctx->stream, x, T, C, \
+                       T_out, stride, dilation, padding, cols1, cols2, ldc, s1, z1, s2, z2, flip, per)
+#define IRO_IM2COL7_C(CV, RS)          \
+    switch (chn) {                     \
+        case 1: IRO_IM2COL7(CV, RS, 1); break; \
+        case 2: IRO_IM2COL7(CV, RS, 2); break; \
+        case 3: IRO_IM2COL7(CV, RS, 3); break; \
+        default: IRO_IM2COL7(CV, RS, 4); break; \
+    }
+    if (ctx->convention == IRO_HIP_GCC_FASTMATH) {
+        if (res) { IRO_IM2COL7_C(1, true); } else { IRO_IM2COL7_C(1, false); }
+    } else {
+        if (res) { IRO_IM2COL7_C(0, true); } else { IRO_IM2COL7_C(0, false); }
+    }
+#undef IRO_IM2COL7_C
+#undef IRO_IM2COL7
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    // Algorithmic HBM bytes: the input once, the code plane(s) out.
+    prof_end(ctx, PK_CONV_IM2COL, 0,
+             4.0 * T * C + (res ? 2.0 : 1.0) * ((double)T_out * 7 * C + 8.0 * T_out));
     return 0;
 }
 

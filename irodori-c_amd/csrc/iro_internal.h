@@ -60,6 +60,7 @@ struct IroHipContext {
     int gemm_spb = 0;     // column slabs per whole-tile block (0: chosen per GEMM)
     int gemm_lds = 0;     // LDS-pipelined GEMM: 0 shape chosen per GEMM, -1 off, > 0 forced shape
     int gemm_wt_rows = 0; // rows per whole-tile block: 0 chosen per GEMM, 64 or 128
+    int conv_fused = 1;   // kernel-7 convolutions: window ranges and codes in one pass
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
     float *rope = nullptr;  // rotation table: per position cos[32] then sin[32]
     int rope_S = 0;         // positions held by rope
@@ -161,6 +162,7 @@ int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long l
 int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const int32_t *colsum,
                 const int32_t *rowsum, IroHipWeight *w);
 int launch_fill(IroHipContext *ctx, void *dst, int value, size_t bytes);
+int launch_codes_selfcheck(IroHipContext *ctx, unsigned long long *out);
 // iro_engine.hip: x = silu(x) [* g] (ops.c:776-784) and x += gate[m / S] * branch.
 int launch_silu(IroHipContext *ctx, float *x, const float *g, long long n);
 int launch_gated_residual(IroHipContext *ctx, float *x, const float *gate, int ldg,
@@ -288,6 +290,11 @@ int persist_launch(IroHipContext *ctx, PersistPlan *plan, float *x);
 void persist_free(PersistPlan *plan);
 
 int launch_conv_rows(IroHipContext *ctx, const float *x, int T, int C, float *lo, float *hi);
+// Kernel 7, C % 4 == 0, C <= 1024: window ranges and codes in one pass.
+bool conv_im2col7_ok(int C, int kernel, int ldc);
+int launch_conv_im2col7(IroHipContext *ctx, const float *x, int T, int C, int T_out, int stride,
+                        int dilation, int padding, uint8_t *cols1, uint8_t *cols2, int ldc,
+                        float *s1, int32_t *z1, float *s2, int32_t *z2, bool signed_codes);
 int launch_convt_gather(IroHipContext *ctx, const float *expanded, int T_in, int C_out,
                         int kernel, int stride, int padding, int T_out, const float *bias,
                         float *y);

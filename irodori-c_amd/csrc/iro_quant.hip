@@ -287,6 +287,39 @@ int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const i
     return 0;
 }
 
+namespace {
+// Inputs v in [base, base + 2^28) whose packed code differs from the
+// reference's clamp(rint(v), 0, 255) (NaN: code 0), counted into *out.
+__global__ __launch_bounds__(256) void codes_selfcheck_kernel(unsigned long long *out,
+                                                              unsigned base) {
+    __shared__ unsigned part[4];
+    const unsigned u = base + blockIdx.x * 256u + threadIdx.x;
+    const float v = __uint_as_float(u);
+    float r = __builtin_rintf(v);
+    r = r < 0.0f ? 0.0f : r;
+    r = r > 255.0f ? 255.0f : r;
+    const unsigned want = v != v ? 0u : (unsigned)r;
+    const unsigned got = pack_codes4(v, 0.0f, 0.0f, 0.0f) & 0xffu;
+    const unsigned long long m = __ballot(got != want);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = (unsigned)__popcll(m);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned n = part[0] + part[1] + part[2] + part[3];
+        if (n) atomicAdd(out, (unsigned long long)n);
+    }
+}
+}  // namespace
+
+// All 2^32 inputs in 16 launches; *out must start zeroed.
+int launch_codes_selfcheck(IroHipContext *ctx, unsigned long long *out) {
+    for (unsigned long long base = 0; base < (1ull << 32); base += (1ull << 28)) {
+        hipLaunchKernelGGL(codes_selfcheck_kernel, dim3(1u << 20), dim3(256), 0, ctx->stream, out,
+                           (unsigned)base);
+        IRO_HIP_CHECK_LAUNCH(ctx);
+    }
+    return 0;
+}
+
 int launch_fill(IroHipContext *ctx, void *dst, int value, size_t bytes) {
     if (!bytes) return 0;
     size_t blocks = (bytes + 256 * 16 - 1) / (256 * 16);

@@ -24,10 +24,10 @@ __device__ __forceinline__ size_t code_off(int row, int col, int ldq) {
 
 template <int CONV>
 __device__ __forceinline__ uint32_t codes4(const float4 &v, const RowQ &r, float4 *vals) {
-    float a = quant_value<CONV>(v.x, r), b = quant_value<CONV>(v.y, r);
-    float c = quant_value<CONV>(v.z, r), d = quant_value<CONV>(v.w, r);
-    if (vals) *vals = make_float4(a, b, c, d);
-    return pack_codes4(a, b, c, d);
+    const uint32_t w = pack_codes4(quant_pre<CONV>(v.x, r), quant_pre<CONV>(v.y, r),
+                                   quant_pre<CONV>(v.z, r), quant_pre<CONV>(v.w, r));
+    if (vals) *vals = unpack_codes4(w);
+    return w;
 }
 
 // Vector path, one row held in registers as CH float4 per lane (lane L

@@ -70,12 +70,27 @@ __device__ __forceinline__ float quant_value(float x, const RowQ &r) {
     return __builtin_fminf(__builtin_fmaxf(v, 0.0f), 255.0f);
 }
 
-// Four codes (values in [0, 255], integral) packed little-endian into a u32.
+// The value the reference rounds: x*inv + zp (fma in the fast build).
+template <int CONV>
+__device__ __forceinline__ float quant_pre(float x, const RowQ &r) {
+    return CONV == 1 ? __builtin_fmaf(x, r.inv, r.zpf) : x * r.inv + r.zpf;
+}
+
+// Four codes packed little-endian into a u32.  v_cvt_pk_u8_f32 rounds to
+// nearest even and saturates to [0, 255], NaN to 0 -- clamp(rint(v), 0,
+// 255) for every float v, as iro_hip_selfcheck_codes checks on the device
+// -- so it takes either the codes or the unrounded quant_pre values.
 __device__ __forceinline__ uint32_t pack_codes4(float a, float b, float c, float d) {
     uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(a, 0, 0u);
     w = __builtin_amdgcn_cvt_pk_u8_f32(b, 1, w);
     w = __builtin_amdgcn_cvt_pk_u8_f32(c, 2, w);
     return __builtin_amdgcn_cvt_pk_u8_f32(d, 3, w);
+}
+
+// The four codes of a packed word as floats (v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ float4 unpack_codes4(uint32_t w) {
+    return make_float4((float)(w & 0xffu), (float)((w >> 8) & 0xffu), (float)((w >> 16) & 0xffu),
+                       (float)(w >> 24));
 }
 
 // ops.c:437-439 residual: r = x - s1*(q1 - zp1).

@@ -174,6 +174,7 @@ def load() -> C.CDLL:
         "iro_hip_dit_stack_set_int8_mask": ([_vp, _i], _i),
         "iro_hip_dit_stack_get_int8_mask": ([_vp], _i),
         "iro_hip_selfcheck_inject_fault": ([_i], _i),
+        "iro_hip_selfcheck_codes": ([_vp, C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_snake_bias": ([_vp, _vp, _i, _i, _vp, _vp, _vp], _i),
         "iro_hip_selfcheck_sincosf": ([_vp, C.POINTER(C.c_ulonglong),
                                        C.POINTER(C.c_ulonglong)], _i),
@@ -445,6 +446,12 @@ class Context:
         self._check(self.lib.iro_hip_selfcheck_fp32(self.h, C.byref(d), C.byref(r)),
                     "selfcheck_fp32")
         return int(d.value), int(r.value)
+
+    def selfcheck_codes(self) -> int:
+        """Float inputs whose packed code differs from clamp(rint(v), 0, 255)."""
+        m = C.c_ulonglong(0)
+        self._check(self.lib.iro_hip_selfcheck_codes(self.h, C.byref(m)), "selfcheck_codes")
+        return int(m.value)
 
     def selfcheck_silu(self):
         """(expf digest over every float input, fast-division mismatches)."""

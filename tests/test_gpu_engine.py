@@ -211,3 +211,10 @@ def test_silu_and_gated_residual_match_oracle(ctx, oracle):
     ctx.gated_residual(xd, ctx.to_device(gate), D, ctx.to_device(br), B * S, D, S)
     assert_bits_equal(xd.numpy(), oracle.gated_residual(ctx.convention, x, gate, br, B, S),
                       "gated residual")
+
+
+def test_code_packing_equals_reference_rounding_on_every_float(ctx_strict):
+    # Every activation quantizer packs its unrounded values with
+    # v_cvt_pk_u8_f32; that must equal the reference's clamp(nearbyintf(v),
+    # 0, 255) conversion (ops.c:341-345) for every float v.
+    assert ctx_strict.selfcheck_codes() == 0
