@@ -384,6 +384,14 @@ int iro_hip_dit_stack_use_persistent(IroHipDiTStack *s, int on);
    unchanged.  Must be set before the first set_block. */
 int iro_hip_dit_stack_set_int8_mask(IroHipDiTStack *s, int mask);
 int iro_hip_dit_stack_get_int8_mask(const IroHipDiTStack *s);
+/* Concurrent row runs of iro_hip_dit_stack_step (no counterpart in the
+   reference; a scheduling choice): with runs > 1 the step forks after the
+   modulation GEMM into one stream per CFG branch (B > 1) or per slice of
+   whole 32-row blocks of S (B = 1, up to `runs` slices), each taking its
+   rows through every block, and joins them before returning.  Rows are
+   independent through the linear stack, so the results are identical; the
+   runs' kernels overlap on the GPU.  0 or 1: one stream (default). */
+int iro_hip_dit_stack_set_runs(IroHipDiTStack *s, int runs);
 
 /* One DiT block forward (dit.c:984-1040 dit_block) on the device, in place on
    x [B*S, D], with this stack's int8 weights of `block`: adaLN apply, fused

@@ -25,6 +25,12 @@ int set_error(IroHipContext *ctx, const char *fmt, ...) {
 }
 
 int Workspace::commit() {
+    if (!outer && ctx->ws_override) {
+        if (need > ctx->ws_override_bytes)
+            return set_error(ctx, "workspace: a chain needs %zu bytes, its region holds %zu", need,
+                             ctx->ws_override_bytes);
+        return 0;
+    }
     void *&buf = outer ? ctx->ws_outer : ctx->ws;
     size_t &have = outer ? ctx->ws_outer_bytes : ctx->ws_bytes;
     if (need <= have) return 0;

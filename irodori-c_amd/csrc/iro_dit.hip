@@ -661,6 +661,8 @@ struct GraphCache {
     }
 };
 
+constexpr int kMaxChains = 4;  // concurrent row runs of a linear-stack step
+
 // A few graph caches for alternating argument sets (a sampler's CFG steps
 // at batch 3 and its plain steps at batch 1): the slot holding the same
 // arguments, else a free one, else the oldest.
@@ -729,6 +731,14 @@ struct IroHipDiTStack {
     // launched after it), per argument set
     int use_graph = 1;
     GraphSet graphs, sgraphs;
+    // concurrent row runs of the linear-stack step (0: off)
+    int chains = 0;
+    hipStream_t side[kMaxChains] = {};
+    hipEvent_t join[kMaxChains] = {};
+    hipEvent_t fork = nullptr;
+    int nstreams = 0;
+    void *chain_ws[kMaxChains] = {};
+    size_t chain_ws_bytes = 0;
     // the persistent kernel of the step (iro_persist.hip)
     int use_persist = 0;
     iro::PersistPlan *persist = nullptr;
@@ -858,55 +868,134 @@ int graph_step(IroHipContext *ctx, GraphSet &set, bool use, const std::vector<lo
     return 0;
 }
 
+// The activation buffers a run of rows writes: the stack's, from row r0.
+struct SiteBufs {
+    float *q, *k, *v, *g, *hidden, *branch, *hidden3;
+};
+
+SiteBufs site_bufs(const IroHipDiTStack *s, int r0) {
+    const size_t d = (size_t)r0 * s->D, h = (size_t)r0 * s->H;
+    return SiteBufs{s->q + d, s->k + d, s->v + d, s->g + d, s->hidden + h,
+                    s->branch ? s->branch + d : nullptr, s->hidden3 ? s->hidden3 + h : nullptr};
+}
+
 // The four projection sites of block blk, int8 or, for a group whose mask
 // bit is clear, the fp32 linear (dit.c:780-798, 876-884, 939-972).
 // dit.c:780-798: Q, K, V and the attention gate from `in` [M, D].
-int site_qkvg(IroHipDiTStack *s, int blk, const float *in, int M) {
+int site_qkvg(IroHipDiTStack *s, const SiteBufs &o, int blk, const float *in, int M) {
     IroHipContext *ctx = s->ctx;
     const int D = s->D;
     if (s->int8_mask & 1)
-        return qkvg_impl(ctx, in, M, s->qkvg[blk], s->q, s->k, s->v, s->g, s->residual_mask & 1);
+        return qkvg_impl(ctx, in, M, s->qkvg[blk], o.q, o.k, o.v, o.g, s->residual_mask & 1);
     const IroHipDiTStack::F32Weights &f = s->f32w[blk];
-    return iro_hip_linear_f32(ctx, in, M, D, f.wq, D, nullptr, s->q) ||
-           iro_hip_linear_f32(ctx, in, M, D, f.wk, D, nullptr, s->k) ||
-           iro_hip_linear_f32(ctx, in, M, D, f.wv, D, nullptr, s->v) ||
-           iro_hip_linear_f32(ctx, in, M, D, f.wg, D, nullptr, s->g);
+    return iro_hip_linear_f32(ctx, in, M, D, f.wq, D, nullptr, o.q) ||
+           iro_hip_linear_f32(ctx, in, M, D, f.wk, D, nullptr, o.k) ||
+           iro_hip_linear_f32(ctx, in, M, D, f.wv, D, nullptr, o.v) ||
+           iro_hip_linear_f32(ctx, in, M, D, f.wg, D, nullptr, o.g);
 }
 
 // dit.c:876-884 and 1013-1020: x += gate[m / S] * Wo(mix).
-int site_wo(IroHipDiTStack *s, int blk, const float *mix, int M, float *x, const float *gate,
-            int ldg, int S) {
+int site_wo(IroHipDiTStack *s, const SiteBufs &o, int blk, const float *mix, int M, float *x,
+            const float *gate, int ldg, int S) {
     IroHipContext *ctx = s->ctx;
     const int D = s->D;
     if (s->int8_mask & 2)
         return linear_gated_impl(ctx, mix, M, D, s->wo[blk], s->residual_mask & 2, nullptr, 0, x,
                                  gate, ldg, S);
-    return iro_hip_linear_f32(ctx, mix, M, D, s->f32w[blk].wo, D, nullptr, s->branch) ||
-           launch_gated_residual(ctx, x, gate, ldg, s->branch, M, D, S);
+    return iro_hip_linear_f32(ctx, mix, M, D, s->f32w[blk].wo, D, nullptr, o.branch) ||
+           launch_gated_residual(ctx, x, gate, ldg, o.branch, M, D, S);
 }
 
 // dit.c:939-972 and 1032-1039: x += gate[m / S] * W2(silu(W1 h) * W3 h).
-int site_mlp(IroHipDiTStack *s, int blk, const float *h, int M, float *x, const float *gate,
-             int ldg, int S) {
+int site_mlp(IroHipDiTStack *s, const SiteBufs &o, int blk, const float *h, int M, float *x,
+             const float *gate, int ldg, int S) {
     IroHipContext *ctx = s->ctx;
     const int D = s->D, H = s->H, rm = s->residual_mask;
     const bool i13 = (s->int8_mask & 4) != 0, i2 = (s->int8_mask & 8) != 0;
     if (i13 && i2)
-        return swiglu_impl(ctx, h, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, s->hidden, nullptr,
+        return swiglu_impl(ctx, h, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, o.hidden, nullptr,
                            x, gate, ldg, S);
     const IroHipDiTStack::F32Weights &f = s->f32w[blk];
     if (i13) {
-        if (swiglu_w13(ctx, h, M, s->w13[blk], rm & 4, s->hidden)) return -1;
-    } else if (iro_hip_linear_f32(ctx, h, M, D, f.w1, H, nullptr, s->hidden) ||
-               iro_hip_linear_f32(ctx, h, M, D, f.w3, H, nullptr, s->hidden3) ||
-               launch_silu(ctx, s->hidden, s->hidden3, (long long)M * H)) {
+        if (swiglu_w13(ctx, h, M, s->w13[blk], rm & 4, o.hidden)) return -1;
+    } else if (iro_hip_linear_f32(ctx, h, M, D, f.w1, H, nullptr, o.hidden) ||
+               iro_hip_linear_f32(ctx, h, M, D, f.w3, H, nullptr, o.hidden3) ||
+               launch_silu(ctx, o.hidden, o.hidden3, (long long)M * H)) {
         return -1;
     }
     if (i2)
-        return linear_gated_impl(ctx, s->hidden, M, H, s->w2[blk], rm & 8, nullptr, 0, x, gate,
+        return linear_gated_impl(ctx, o.hidden, M, H, s->w2[blk], rm & 8, nullptr, 0, x, gate,
                                  ldg, S);
-    return iro_hip_linear_f32(ctx, s->hidden, M, H, f.w2, D, nullptr, s->branch) ||
-           launch_gated_residual(ctx, x, gate, ldg, s->branch, M, D, S);
+    return iro_hip_linear_f32(ctx, o.hidden, M, H, f.w2, D, nullptr, o.branch) ||
+           launch_gated_residual(ctx, x, gate, ldg, o.branch, M, D, S);
+}
+
+// Row runs that go through a step's blocks concurrently, each on its own
+// stream: one per CFG branch when B > 1 (rows of one branch share their
+// modulation rows), else S split into runs of whole 32-row blocks.  The
+// runs' kernels overlap, which fills the GPU where one run's kernels leave
+// it idle (their tails, their few tiles at one branch's 750 rows).
+int stack_runs(const IroHipDiTStack *s, int B, int S, int *r0, int *rows) {
+    int n = s->chains;
+    if (n <= 1) return 1;
+    if (B > 1) {
+        if (B > kMaxChains) return 1;
+        for (int b = 0; b < B; ++b) {
+            r0[b] = b * S;
+            rows[b] = S;
+        }
+        return B;
+    }
+    const int blocks = (S + 31) / 32;
+    if (n > blocks) n = blocks;
+    if (n <= 1) return 1;
+    int start = 0;
+    for (int c = 0; c < n; ++c) {
+        const int nb = blocks / n + (c < blocks % n ? 1 : 0);
+        r0[c] = start;
+        rows[c] = (c == n - 1) ? S - start : nb * 32;
+        start += rows[c];
+    }
+    return n;
+}
+
+// Streams, events and one inner-workspace region per run, sized for the
+// largest run's codes (allocates: outside graph capture).
+int stack_chain_prepare(IroHipDiTStack *s, int nrun, const int *rows) {
+    IroHipContext *ctx = s->ctx;
+    const int D = s->D, H = s->H, rm = s->residual_mask;
+    size_t need = 0;
+    for (int c = 0; c < nrun; ++c) {
+        const int Mc = rows[c];
+        size_t off[6], off2[6];
+        Workspace a{ctx}, b{ctx}, w{ctx};
+        act_reserve(a, Mc, D, rm & 1, off, gemm_lds_cfg(ctx, EPI_QKVG, rm & 1, Mc, D) != 0);
+        act_reserve(b, Mc, D, rm & 2, off, gemm_lds_cfg(ctx, EPI_GATED, rm & 2, Mc, D) != 0);
+        act_reserve(w, Mc, D, rm & 4, off, gemm_lds_cfg(ctx, EPI_SWIGLU, rm & 4, Mc, D) != 0);
+        act_reserve(w, Mc, H, rm & 8, off2, gemm_lds_cfg(ctx, EPI_GATED, rm & 8, Mc, H) != 0);
+        need = std::max(need, std::max(a.need, std::max(b.need, w.need)));
+    }
+    if (s->nstreams < nrun) {
+        for (int c = s->nstreams; c < nrun; ++c) {
+            IRO_HIP_TRY(ctx, hipStreamCreateWithFlags(&s->side[c], hipStreamNonBlocking));
+            IRO_HIP_TRY(ctx, hipEventCreateWithFlags(&s->join[c], hipEventDisableTiming));
+            s->nstreams = c + 1;
+        }
+    }
+    if (!s->fork) IRO_HIP_TRY(ctx, hipEventCreateWithFlags(&s->fork, hipEventDisableTiming));
+    if (need > s->chain_ws_bytes) {
+        IRO_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        for (void *&p : s->chain_ws)
+            if (p) {
+                (void)hipFree(p);
+                p = nullptr;
+            }
+        s->chain_ws_bytes = 0;
+        for (int c = 0; c < kMaxChains; ++c) IRO_HIP_TRY(ctx, hipMalloc(&s->chain_ws[c], need));
+        s->chain_ws_bytes = need;
+        s->graphs.drop();  // captured steps hold the previous regions
+    }
+    return 0;
 }
 
 // The launches of one step (sampler.c:243-301 runs dit_block per layer).
@@ -919,13 +1008,45 @@ int stack_launch(IroHipDiTStack *s, float *x, const float *cond, int B, int S) {
     if (linear_gated_impl(ctx, cond, B, D, s->ada_all, 0, s->mod, ldm, nullptr, nullptr, 0, 1))
         return -1;
     if (stack_persistent(s)) return persist_launch(ctx, s->persist, x);
-    for (int blk = 0; blk < s->blocks; ++blk) {
-        const float *mod = s->mod + (size_t)blk * s->ada_np;
-        if (site_qkvg(s, blk, x, M) || site_wo(s, blk, s->v, M, x, mod + 2 * D, ldm, S) ||
-            site_mlp(s, blk, x, M, x, mod + 5 * D, ldm, S))
-            return -1;
+    int r0[kMaxChains], rows[kMaxChains];
+    const int nrun = stack_runs(s, B, S, r0, rows);
+    if (nrun == 1) {
+        const SiteBufs o = site_bufs(s, 0);
+        for (int blk = 0; blk < s->blocks; ++blk) {
+            const float *mod = s->mod + (size_t)blk * s->ada_np;
+            if (site_qkvg(s, o, blk, x, M) || site_wo(s, o, blk, o.v, M, x, mod + 2 * D, ldm, S) ||
+                site_mlp(s, o, blk, x, M, x, mod + 5 * D, ldm, S))
+                return -1;
+        }
+        return 0;
     }
-    return 0;
+    // Fork the runs off the context stream after the modulation GEMM,
+    // issue their launches block by block, join them back.
+    hipStream_t main = ctx->stream;
+    IRO_HIP_TRY(ctx, hipEventRecord(s->fork, main));
+    for (int c = 0; c < nrun; ++c) IRO_HIP_TRY(ctx, hipStreamWaitEvent(s->side[c], s->fork, 0));
+    int rc = 0;
+    for (int blk = 0; blk < s->blocks && !rc; ++blk) {
+        for (int c = 0; c < nrun && !rc; ++c) {
+            ctx->stream = s->side[c];
+            ctx->ws_override = s->chain_ws[c];
+            ctx->ws_override_bytes = s->chain_ws_bytes;
+            const SiteBufs o = site_bufs(s, r0[c]);
+            float *xc = x + (size_t)r0[c] * D;
+            const float *mod = s->mod + (size_t)(r0[c] / S) * ldm + (size_t)blk * s->ada_np;
+            rc = site_qkvg(s, o, blk, xc, rows[c]) ||
+                 site_wo(s, o, blk, o.v, rows[c], xc, mod + 2 * D, ldm, S) ||
+                 site_mlp(s, o, blk, xc, rows[c], xc, mod + 5 * D, ldm, S);
+        }
+    }
+    ctx->stream = main;
+    ctx->ws_override = nullptr;
+    ctx->ws_override_bytes = 0;
+    for (int c = 0; c < nrun; ++c) {
+        IRO_HIP_TRY(ctx, hipEventRecord(s->join[c], s->side[c]));
+        IRO_HIP_TRY(ctx, hipStreamWaitEvent(main, s->join[c], 0));
+    }
+    return rc ? -1 : 0;
 }
 
 }  // namespace
@@ -1272,8 +1393,13 @@ int iro_hip_dit_stack_step(IroHipDiTStack *s, float *x, const float *cond, int B
             return set_error(ctx, "dit_stack: block %d has no weights or no modulation weight", b);
     if (stack_reserve(s, B * S, B)) return -1;
     if (stack_persistent(s) && stack_persist_prepare(s, B, S)) return -1;
+    {
+        int r0[kMaxChains], rows[kMaxChains];
+        const int nrun = stack_persistent(s) ? 1 : stack_runs(s, B, S, r0, rows);
+        if (nrun > 1 && stack_chain_prepare(s, nrun, rows)) return -1;
+    }
     const std::vector<long long> args = {(long long)(uintptr_t)x, (long long)(uintptr_t)cond, B,
-                                         S};
+                                         S, s->chains};
     return graph_step(ctx, s->graphs, s->use_graph != 0, args,
                       [&]() { return stack_launch(s, x, cond, B, S); }) ||
                    ctx->has_err
@@ -1297,17 +1423,18 @@ int iro_hip_dit_stack_block_forward(IroHipDiTStack *s, int block, float *x, int 
     // dit.c:1003-1006: h = RMSNorm-modulate(x) with the attention shift/scale.
     if (iro_hip_dit_adaln_apply(ctx, x, B, S, D, ada_attn, ada_attn + BD, eps, s->h)) return -1;
     // dit.c:785-792: one quantization of h, Q/K/V/gate from the fused weight.
-    if (site_qkvg(s, block, s->h, M)) return -1;
+    const SiteBufs o = site_bufs(s, 0);
+    if (site_qkvg(s, o, block, s->h, M)) return -1;
     // dit.c:803, 808-870, 872: norm + RoPE, attention core, sigmoid gate.
     if (iro_hip_dit_qk_norm_rope(ctx, s->q, q_norm, s->k, k_norm, B, S, D, eps)) return -1;
     if (iro_hip_dit_attention(ctx, actx, s->q, s->k, s->v, s->g, B, S, D, context_k, context_v,
                               s->mix))
         return -1;
     // dit.c:878-881, 1012-1020: Wo, then x += gate * branch.
-    if (site_wo(s, block, s->mix, M, x, ada_attn + 2 * BD, D, S)) return -1;
+    if (site_wo(s, o, block, s->mix, M, x, ada_attn + 2 * BD, D, S)) return -1;
     // dit.c:1022-1039: the MLP half.
     if (iro_hip_dit_adaln_apply(ctx, x, B, S, D, ada_mlp, ada_mlp + BD, eps, s->h)) return -1;
-    if (site_mlp(s, block, s->h, M, x, ada_mlp + 2 * BD, D, S)) return -1;
+    if (site_mlp(s, o, block, s->h, M, x, ada_mlp + 2 * BD, D, S)) return -1;
     return ctx->has_err ? -1 : 0;
 }
 
@@ -1422,6 +1549,16 @@ int iro_hip_dit_stack_set_int8_mask(IroHipDiTStack *s, int mask) {
 
 int iro_hip_dit_stack_get_int8_mask(const IroHipDiTStack *s) { return s ? s->int8_mask : -1; }
 
+int iro_hip_dit_stack_set_runs(IroHipDiTStack *s, int runs) {
+    if (!s) return -1;
+    if (runs < 0 || runs > kMaxChains)
+        return set_error(s->ctx, "dit_stack: runs %d outside 0..%d", runs, kMaxChains);
+    IRO_HIP_TRY(s->ctx, hipStreamSynchronize(s->ctx->stream));
+    s->chains = runs;
+    s->graphs.drop();
+    return 0;
+}
+
 size_t iro_hip_dit_stack_bytes(const IroHipDiTStack *s) {
     if (!s) return 0;
     size_t n = 0;
@@ -1458,6 +1595,13 @@ void iro_hip_dit_stack_destroy(IroHipDiTStack *s) {
     for (auto *v : {&s->qkvg, &s->wo, &s->w13, &s->w2})
         for (IroHipWeight *w : *v) iro_hip_weight_destroy(w);
     for (auto &f : s->f32w) f32_weights_free(f);
+    for (int c = 0; c < s->nstreams; ++c) {
+        (void)hipStreamDestroy(s->side[c]);
+        (void)hipEventDestroy(s->join[c]);
+    }
+    if (s->fork) (void)hipEventDestroy(s->fork);
+    for (void *p : s->chain_ws)
+        if (p) (void)hipFree(p);
     stack_free_acts(s);
     delete s;
 }

@@ -51,6 +51,10 @@ struct IroHipContext {
     // inner calls use ws
     void *ws_outer = nullptr;
     size_t ws_outer_bytes = 0;
+    // while set, the inner workspace of the calls being issued (a chain of
+    // launches on its own stream, sized beforehand; never grown)
+    void *ws_override = nullptr;
+    size_t ws_override_bytes = 0;
     char backend[256] = {0};
     int cus = 0;        // compute units of the device
     void *zero16 = nullptr;  // 256 zero bytes: the source of padding k pieces
@@ -148,7 +152,9 @@ struct Workspace {
     int commit();  // ensures ctx->ws holds `need` bytes
     template <class T>
     T *at(size_t off) const {
-        return reinterpret_cast<T *>(static_cast<char *>(outer ? ctx->ws_outer : ctx->ws) + off);
+        return reinterpret_cast<T *>(
+            static_cast<char *>(outer ? ctx->ws_outer : ctx->ws_override ? ctx->ws_override : ctx->ws) +
+            off);
     }
 };
 

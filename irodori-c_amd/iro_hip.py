@@ -173,6 +173,7 @@ def load() -> C.CDLL:
         "iro_hip_dit_condition": ([_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
         "iro_hip_dit_stack_set_int8_mask": ([_vp, _i], _i),
         "iro_hip_dit_stack_get_int8_mask": ([_vp], _i),
+        "iro_hip_dit_stack_set_runs": ([_vp, _i], _i),
         "iro_hip_selfcheck_inject_fault": ([_i], _i),
         "iro_hip_selfcheck_codes": ([_vp, C.POINTER(C.c_ulonglong)], _i),
         "iro_hip_snake_bias": ([_vp, _vp, _i, _i, _vp, _vp, _vp], _i),
@@ -798,6 +799,11 @@ class DiTStack:
         """IRO_INT8_MASK (dit.c:273-291); before the first set_block."""
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_set_int8_mask(self.h, mask),
                         "dit_stack_set_int8_mask")
+
+    def set_runs(self, runs: int):
+        """Concurrent row runs of the stack step (0/1 off)."""
+        self.ctx._check(self.ctx.lib.iro_hip_dit_stack_set_runs(self.h, runs),
+                        "dit_stack_set_runs")
 
     def use_persistent(self, on: bool):
         self.ctx._check(self.ctx.lib.iro_hip_dit_stack_use_persistent(self.h, int(bool(on))),

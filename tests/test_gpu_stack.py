@@ -148,3 +148,32 @@ def test_stacked_modulation_gemm_twelve_blocks(ctx, oracle):
             assert np.array_equal(got.view(np.int32), want.view(np.int32)), f"block {b} differs"
     finally:
         stack.destroy()
+
+
+@pytest.mark.parametrize("B,S,runs", [(3, 200, 3), (1, 300, 3), (2, 90, 4)])
+def test_concurrent_row_runs_equal_one_stream(ctx, B, S, runs):
+    """iro_hip_dit_stack_set_runs: the rows split over streams (one per CFG
+    branch, or slices of 32-row blocks) give x bit-identical to one stream,
+    eagerly and from the captured graph."""
+    D, H, blocks = 256, 320, 2
+    ws = _weights(D, H, blocks, 930)
+    x0 = gauss(931, (B * S, D))
+    cond = ctx.to_device(gauss(932, (B, D), 0.1))
+    stack = iro_hip.DiTStack(ctx, blocks, D, H, 8)
+    try:
+        for b in range(blocks):
+            stack.set_block(b, *[ctx.to_device(w) for w in ws[b]])
+        x = ctx.to_device(x0)
+        stack.step(x, cond, B, S)
+        want = x.numpy()
+        stack.set_runs(runs)
+        x = ctx.to_device(x0)
+        for i in range(4):  # eager, capture, replay, replay
+            ctx.copy(x, ctx.to_device(x0))
+            stack.step(x, cond, B, S)
+            ctx.sync()
+            got = x.numpy()
+            bad = int((got.view(np.int32) != want.view(np.int32)).sum())
+            assert bad == 0, f"step {i}: {bad} of {got.size} elements differ"
+    finally:
+        stack.destroy()
