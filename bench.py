@@ -351,6 +351,115 @@ def conv_main(args):
     print(json.dumps(out), flush=True)
 
 
+def decoder_ops(p, frames, residual_mask=12, residual_stages=8):
+    """Multiply-adds x2 of the int8 convolutions of the decoder core."""
+    t = frames
+    ops = 2 * t * p["channels"] * 7 * p["latent_channels"] * (2 if residual_mask & 1 else 1)
+    for si, st in enumerate(p["stages"]):
+        k, s_, pad, op = st["kernel"], st["stride"], st["padding"], st["output_padding"]
+        ops += 2 * t * k * st["c_out"] * st["c_in"] * (2 if residual_mask & 2 else 1)
+        t = (t - 1) * s_ - 2 * pad + k + op
+        on = residual_stages >> si & 1
+        C = st["c_out"]
+        for _ in st["residual"]:
+            ops += 2 * t * C * 7 * C * (2 if (residual_mask & 4) and on else 1)
+            ops += 2 * t * C * C * (2 if (residual_mask & 8) and on else 1)
+    return ops
+
+
+def decoder_main(args):
+    """The DACVAE decoder's int8 core (dacvae.c:1221-1277) at the reference's
+    channel counts: one step = one decode of `frames` latent frames from the
+    quantizer_out state (initial Conv7, four stages of snake + int8
+    ConvTranspose and three residual units of snake, int8 Conv7, snake_bias
+    and int8 1x1 onto the skip), state and weights resident in HBM."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import codec_params as cp
+    frames = args.decoder_frames
+    conv = iro_hip.STRICT if args.convention == "strict" else iro_hip.GCC_FASTMATH
+    p = cp.decoder(77)
+    ops = decoder_ops(p, frames)
+    state = np.random.default_rng(78).standard_normal((frames, cp.LATENT), dtype=np.float32)
+    ctx = iro_hip.Context(0, conv)
+    log("backend:", ctx.backend())
+    d = iro_hip.DACVAE(ctx, cp.to_device(ctx, p))
+    T = d.output_frames(frames)
+    sd = ctx.to_device(state)
+    out = ctx.empty((T, cp.FINAL), np.float32)
+
+    def step():
+        d.decode_int8(sd, frames, out)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    log(f"decoder: {frames} frames -> {T} x {cp.FINAL}: {ms_step:.3f} ms per decode")
+    ctx.profile(True)
+    for _ in range(args.profile_steps):
+        step()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    kernels = log_profile(prof)
+    roof = roofline_of(prof)
+    # parity and CPU baseline on a bounded sample of the same decode
+    sf = min(frames, 2)
+    small = ctx.empty((d.output_frames(sf), cp.FINAL), np.float32)
+    d.decode_int8(ctx.to_device(state[:sf]), sf, small)
+    g_small = small.numpy()
+    int8_bytes = d.nbytes()
+    d.destroy()
+    ctx.close()
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import Oracle
+        o = Oracle()
+        times = []
+        start = time.perf_counter()
+        while len(times) < 3 and time.perf_counter() - start < args.cpu_seconds:
+            t1 = time.perf_counter()
+            want = o.decode_core(0 if conv == iro_hip.STRICT else 1, state[:sf], p)
+            times.append(time.perf_counter() - t1)
+        med = sorted(times)[len(times) // 2]
+        same = bool(np.array_equal(want.view(np.uint32), g_small.view(np.uint32)))
+        sops = decoder_ops(p, sf)
+        log(f"cpu baseline: oracle decode of {sf} frames, median {med:.2f} s on {o.threads} "
+            f"threads; GPU output bit-identical: {same}")
+        cpu = {"value": round(sops / med / 1e12, 5), "unit": "TOPS", "cores": o.threads,
+               "kind": "port", "sample": (f"the oracle's decoder core on {sf} of the {frames} "
+                                          f"latent frames ({len(times)} runs, median)"),
+               "gpu_output_bit_identical": same}
+    out = {
+        "metric": "int8 DACVAE decoder core TOPS and ms per decode, 1 GPU",
+        "value": round(ops * args.steps / wall / 1e12, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded Gaussian state, random-init weights at the decoder's shapes)",
+        "config": {"workload": (f"DACVAE decoder int8 core: {frames} latent frames -> {T} "
+                                f"samples x 96 channels, residual planes in stage 3"),
+                   "frames": frames, "output_frames": T, "ops_per_step": ops,
+                   "latent_frames_per_s": round(frames / (ms_step / 1e3), 1),
+                   "resident_int8_bytes": int8_bytes, "convention": args.convention,
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def adaln_main(args):
     """The adaLN apply step (dit.c:593-606) on the stack's rows: one step =
     one call of iro_hip_dit_adaln_apply on x [B*S, D] resident in HBM.  The
@@ -1011,12 +1120,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["stack", "weights", "adaln", "qknorm", "attention",
-                                           "block", "sampler-step"]
+                                           "block", "sampler-step", "decoder"]
                     + sorted(CONV_WORKLOADS)
                     + sorted(CONVT_WORKLOADS),
                     default="stack",
                     help="stack (default): the DiT linear stack; conv7*: the codec int8 Conv1d; "
                          "convt-*: the codec int8 ConvTranspose1d")
+    ap.add_argument("--decoder-frames", type=int, default=250,
+                    help="decoder workload: latent frames per decode (1920 samples each)")
     ap.add_argument("--conv-residual", action="store_true",
                     help="conv workloads: add the fixed-scale second plane")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -1052,6 +1163,9 @@ def main():
         return
     if args.workload == "adaln":
         adaln_main(args)
+        return
+    if args.workload == "decoder":
+        decoder_main(args)
         return
     if args.workload == "qknorm":
         qknorm_main(args)
