@@ -140,7 +140,7 @@ int weight_alloc(IroHipContext *ctx, int N, int K, int layout, int nparts, const
     w->ctx = ctx;
     w->N = N;
     w->K = K;
-    w->Np = (int)round_up((size_t)N, kNPad);
+    w->Np = packed_rows(N, layout, nparts);
     w->Kp = (int)round_up((size_t)K, kKPad);
     w->layout = layout;
     w->nparts = nparts;

@@ -28,10 +28,22 @@ constexpr int kSnakeMaxChannels = 1536;  // dacvae.c:808 SNAKE_MAX_CHANNELS
 // 16-byte aligned).  BIAS: v = x + bias (snake_bias_forward).  INV: the
 // hoisted-reciprocal form.  FMA: the fast build's contraction of the final
 // add into one fma.
+// With INV (C <= 1536) the block first stages alpha and inv = 1 / (alpha +
+// 1e-9) per channel in LDS, as the reference hoists its reciprocal
+// (dacvae.c:827-828).
 template <bool BIAS, bool INV, bool FMA>
 __global__ __launch_bounds__(256) void snake_kernel(const float *__restrict__ x, int C,
                                                     long long n4, const float *__restrict__ bias,
                                                     const float *__restrict__ alpha, float *y) {
+    __shared__ float s_alpha[INV ? kSnakeMaxChannels : 1], s_inv[INV ? kSnakeMaxChannels : 1];
+    if (INV) {
+        for (int c = threadIdx.x; c < C; c += 256) {
+            const float a = alpha[c];
+            s_alpha[c] = a;
+            s_inv[c] = 1.0f / (a + 1e-9f);
+        }
+        __syncthreads();
+    }
     for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n4; i += (long long)gridDim.x * 256) {
         const long long e = 4 * i;
         const int c = (int)(e % C);
@@ -41,11 +53,11 @@ __global__ __launch_bounds__(256) void snake_kernel(const float *__restrict__ x,
         for (int k = 0; k < 4; ++k) {
             float xv = o[k];
             if (BIAS) xv = xv + bias[c + k];
-            const float a = alpha[c + k];
+            const float a = INV ? s_alpha[c + k] : alpha[c + k];
             const float s = sinf_glibc(a * xv);
             const float ss = s * s;
             if (INV) {
-                const float inv = 1.0f / (a + 1e-9f);
+                const float inv = s_inv[c + k];
                 o[k] = FMA ? __builtin_fmaf(ss, inv, xv) : xv + ss * inv;
             } else {
                 o[k] = xv + ss / (a + 1e-9f);

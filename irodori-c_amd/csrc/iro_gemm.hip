@@ -737,7 +737,8 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     if (a.M <= 0) return 0;
     if (a.K <= 0 || a.K % 16 || a.K > w->Kp || a.K < w->K || a.K > 65536 || a.lda < a.K ||
         a.lda % 16 ||
-        (((uintptr_t)a.a1) & 15) || (a.a2 && (((uintptr_t)a.a2) & 15)) || w->Np % 256)
+        (((uintptr_t)a.a1) & 15) || (a.a2 && (((uintptr_t)a.a2) & 15)) || w->Np % 128 ||
+        (w->Np % 256 && (epi == EPI_SWIGLU || epi == EPI_QKVG)))
         return set_error(ctx, "gemm: unsupported operand shape (K=%d lda=%d Kp=%d Np=%d)", a.K,
                          a.lda, w->Kp, w->Np);
     if (epi == EPI_SWIGLU && (w->layout != 1 || w->part_N[0] % 32))
@@ -789,7 +790,12 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
         return set_error(ctx, "gemm: packed weight of %d x %d bytes exceeds 2 GiB", w->Np, w->Kp);
     kp.wbytes = w->Np * w->Kp;
     // Signed codes with whole k blocks take the LDS-pipelined kernel.
-    const int lcfg = a.a_signed ? gemm_lds_cfg(ctx, epi, two, a.M, a.K) : 0;
+    int lcfg = a.a_signed ? gemm_lds_cfg(ctx, epi, two, a.M, a.K) : 0;
+    if (lcfg) {
+        int bm = 0, bn = 0;
+        lds_tile_shape(lcfg, &bm, &bn);
+        if (w->Np % bn) lcfg = 0;  // a narrow weight: the 128-column tiles below
+    }
     kp.akbp = a.a_kbp;
     if (a.a_kbp > 0 && (!lcfg || a.a_kbp * 32 != a.K))
         return set_error(ctx, "gemm: fragment-layout codes need the LDS-pipelined kernel");
@@ -823,6 +829,10 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     } else {
         t = choose_tile(a.M, w->Np, ctx->cus > 0 ? ctx->cus : 256, two, epi, ctx->gemm_tile);
         if (two && t.ti * t.tj > 4) t.tj = 1;  // as launch_tile runs it
+        if (w->Np % 256) {  // a narrow weight (128 padded rows): 128-column tiles
+            t.tj = 1;
+            if (t.ti == 1) t.ti = 2;
+        }
         // Signed single-plane codes with K <= 1024 fit a whole 64-row tile
         // in LDS: the barrier-free whole-tile kernel.
         if (a.a_signed && !two && a.K <= 1024 && t.ti == 2) {

@@ -118,6 +118,14 @@ struct IroHipWeight {
 namespace iro {
 
 constexpr int kNPad = 256;  // packed rows padded to a multiple of this
+// Packed rows of a weight of N rows: narrow single-part weights (N <= 128,
+// the decoder's 96-channel convolutions) pad to 128 rows, which the
+// 128-column tiles cover; all others to kNPad.
+inline int packed_rows(int N, int layout, int nparts) {
+    return (N <= 128 && layout == 0 && nparts == 1)
+               ? 128
+               : (int)(((size_t)N + kNPad - 1) / kNPad * kNPad);
+}
 constexpr int kKPad = 128;  // packed k padded to a multiple of this
 
 int set_error(IroHipContext *ctx, const char *fmt, ...);

@@ -493,7 +493,7 @@ int iro_hip_weight_load(IroHipContext *ctx, const char *path, IroHipWeight **out
     std::vector<uint8_t> payload;
     bool ok = std::fread(&h, sizeof(h), 1, f) == 1 && std::memcmp(h.magic, kMagic, 8) == 0;
     const long long N = ok ? h.N : 0, K = ok ? h.K : 0;
-    ok = ok && N > 0 && K > 0 && h.Np == (int)round_up((size_t)N, kNPad) &&
+    ok = ok && N > 0 && K > 0 && h.Np == packed_rows((int)N, (int)h.layout, (int)h.nparts) &&
          h.Kp == (int)round_up((size_t)K, kKPad) && (h.layout == 0 || h.layout == 1) &&
          h.nparts >= 1 && h.nparts <= 8 && (h.separate_rowsum == 0 || h.separate_rowsum == 1);
     long long parts = 0;
