@@ -46,19 +46,20 @@ from iro_synth import gauss  # noqa: E402
 PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA
 PEAK_HBM_GBS = 8000.0
 
-# HBM bytes per launch of each kernel kind at this workload, from two
-# rocprofv3 --pmc runs of this script (FETCH_SIZE, then WRITE_SIZE, per
-# dispatch), scaled by what the same counters read for a 64 MiB device copy
+# HBM bytes per launch of each kernel kind at the M = 2250 step (the one the
+# profiling steps run), from two rocprofv3 --pmc runs of this script
+# (FETCH_SIZE, then WRITE_SIZE, per dispatch, separated by grid size),
+# scaled by what the same counters read for a 64 MiB device copy
 # (--copy-calibration 64: FETCH_SIZE x 1.999, WRITE_SIZE x 1.000); summary
 # and commands in profiles/dit_stack_M2250_hbm_traffic.md.  Counters cannot
 # be read from inside the process, so the figure is the last profile's.
 MEASURED_TRAFFIC = {
     "gemm_swiglu": 74.9e6,
     "gemm_gated_two_term": 56.1e6,
-    "gemm_qkvg": 80.4e6,
+    "gemm_qkvg": 60.2e6,
     "gemm_gated": 29.7e6,
     "quant_rows_residual": 38.2e6,
-    "quant_rows": 11.3e6,
+    "quant_rows": 11.6e6,
 }
 
 
