@@ -61,7 +61,15 @@ void *iro_hip_stream(IroHipContext *ctx);
    -3 column slabs per whole-tile block (0 chosen per GEMM, else 1..64),
    -4 the LDS-pipelined kernel of signed-code GEMMs (0 shape chosen per GEMM,
       -1 off, 1 192x256, 2 96x128, 3 128x256, 4 96x256, 5 64x128 rows x
-      columns per workgroup; shapes a GEMM cannot take fall back).
+      columns per workgroup; shapes a GEMM cannot take fall back),
+   -5 rows per whole-tile block (0 chosen per GEMM, 64, 128),
+   -6 kernel-7 convolution codes (1 window ranges and codes in one pass,
+      the default; 0 two passes),
+   -7 SwiGLU hidden state (0, the default: stored in fp32 and quantized by
+      a row quantization launch; 1: the W1/W3 kernel quantizes it for W2
+      itself, its blocks exchanging row ranges through device memory, when
+      the GEMM's grid fits the GPU at once and the caller does not ask for
+      the fp32 hidden state -- measured slower at the DiT shapes).
    Tuning knobs only: results are identical for every setting.  No
    counterpart in the reference (oneMKL picks its own blocking). */
 int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj);

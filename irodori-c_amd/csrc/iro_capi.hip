@@ -51,7 +51,8 @@ const char *const kProfNames[PK_COUNT] = {
     "quant_rows",        "quant_rows_residual", "gemm_linear",  "gemm_linear_two_term",
     "gemm_qkvg",         "gemm_qkvg_two_term",  "gemm_swiglu",  "gemm_swiglu_two_term",
     "gemm_gated",        "gemm_gated_two_term", "conv_rows",    "conv_im2col",
-    "convt_gather",      "persist_stack",       "snake",        "other"};
+    "convt_gather",      "persist_stack",       "snake",        "gemm_swiglu_quant",
+    "other"};
 
 struct ProfState {
     struct Rec {
@@ -325,6 +326,7 @@ void iro_hip_destroy(IroHipContext *ctx) {
     if (ctx->ws_outer) (void)hipFree(ctx->ws_outer);
     if (ctx->zero16) (void)hipFree(ctx->zero16);
     if (ctx->dev_err) (void)hipFree(ctx->dev_err);
+    if (ctx->band_state) (void)hipFree(ctx->band_state);
     if (ctx->rope) (void)hipFree(ctx->rope);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -349,10 +351,14 @@ int iro_hip_sync(IroHipContext *ctx) {
     IRO_HIP_TRY(ctx, hipMemcpy(&code, ctx->dev_err, sizeof(int), hipMemcpyDeviceToHost));
     if (code) {
         IRO_HIP_TRY(ctx, hipMemset(ctx->dev_err, 0, sizeof(int)));
-        return set_error(ctx, "device error 0x%x: %s%s%s", code,
+        // A band that gave up waiting leaves its exchange state behind.
+        if ((code & 8) && ctx->band_state)
+            IRO_HIP_TRY(ctx, hipMemset(ctx->band_state, 0, ctx->band_state_bytes));
+        return set_error(ctx, "device error 0x%x: %s%s%s%s", code,
                          code & 1 ? "a persistent-kernel wait timed out; " : "",
                          code & 2 ? "a persistent-kernel queue was not completed; " : "",
-                         code & 4 ? "unexpected XCC id" : "");
+                         code & 4 ? "unexpected XCC id; " : "",
+                         code & 8 ? "a W1/W3 band wait timed out" : "");
     }
     return ctx->has_err ? -1 : 0;
 }
@@ -383,6 +389,11 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
     }
     if (ti == -6) {  // tj: 1 kernel-7 im2col in one pass (default), 0 the two-pass form
         ctx->conv_fused = tj != 0;
+        return 0;
+    }
+    if (ti == -7) {  // tj: 1 the W1/W3 kernel quantizes the hidden state, 0 off (default)
+        if (tj != 0 && tj != 1) return set_error(ctx, "set_gemm_tile: band quantization 0 or 1");
+        ctx->band_quant = tj;
         return 0;
     }
     if (ti == -5) {  // tj: rows per whole-tile block, 0 per GEMM, 64 or 128

@@ -603,9 +603,11 @@ int swiglu_w13(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w1
     return launch_gemm(ctx, w13, a, EPI_SWIGLU);
 }
 
+// keep_hidden: the caller reads the fp32 hidden state; otherwise the W1/W3
+// kernel may quantize it for W2 itself (same codes) and not store it.
 int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w13,
                 const IroHipWeight *w2, int residual_w13, int residual_w2, float *hidden,
-                float *out, float *x_res, const float *gate, int ldg, int S) {
+                bool keep_hidden, float *out, float *x_res, const float *gate, int ldg, int S) {
     const int D = w13->K, H = w13->part_N[0];
     const bool p1 = gemm_lds_cfg(ctx, EPI_SWIGLU, residual_w13 != 0, M, D) != 0;
     const bool p2 = gemm_lds_cfg(ctx, x_res ? EPI_GATED : EPI_LINEAR, residual_w2 != 0, M, H) != 0;
@@ -622,8 +624,21 @@ int swiglu_impl(IroHipContext *ctx, const float *h, int M, const IroHipWeight *w
     GemmArgs a = gemm_args(b1, M, D);
     a.hidden = hid;
     a.ldh = H;
-    if (launch_gemm(ctx, w13, a, EPI_SWIGLU)) return -1;
-    if (quantize_into(ctx, hid, M, H, H, b2)) return -1;
+    int fused = 1;
+    if (!keep_hidden && !p2) {
+        GemmArgs aq = a;
+        aq.hq1 = b2.q1;
+        aq.hq2 = b2.q2;
+        aq.ldhq = b2.ld;
+        aq.hs1 = b2.s1;
+        aq.hz1 = b2.z1;
+        aq.hs2 = b2.s2;
+        aq.hz2 = b2.z2;
+        fused = launch_gemm(ctx, w13, aq, EPI_SWIGLU);
+        if (fused < 0) return -1;
+    }
+    if (fused && (launch_gemm(ctx, w13, a, EPI_SWIGLU) || quantize_into(ctx, hid, M, H, H, b2)))
+        return -1;
     GemmArgs a2 = gemm_args(b2, M, H);
     if (x_res) {
         a2.xres = x_res;
@@ -913,8 +928,8 @@ int site_mlp(IroHipDiTStack *s, const SiteBufs &o, int blk, const float *h, int 
     const int D = s->D, H = s->H, rm = s->residual_mask;
     const bool i13 = (s->int8_mask & 4) != 0, i2 = (s->int8_mask & 8) != 0;
     if (i13 && i2)
-        return swiglu_impl(ctx, h, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, o.hidden, nullptr,
-                           x, gate, ldg, S);
+        return swiglu_impl(ctx, h, M, s->w13[blk], s->w2[blk], rm & 4, rm & 8, o.hidden, false,
+                           nullptr, x, gate, ldg, S);
     const IroHipDiTStack::F32Weights &f = s->f32w[blk];
     if (i13) {
         if (swiglu_w13(ctx, h, M, s->w13[blk], rm & 4, o.hidden)) return -1;
@@ -1112,8 +1127,8 @@ int iro_hip_dit_swiglu(IroHipContext *ctx, const float *h, int M, const IroHipWe
         w2->N != w13->K || (M && (!h || (!x_res && !out) || (x_res && (!gate || S <= 0)))))
         return set_error(ctx, "dit_swiglu: invalid arguments or weight shapes");
     if (M == 0) return 0;
-    return swiglu_impl(ctx, h, M, w13, w2, residual_w13, residual_w2, hidden, out, x_res, gate,
-                       w13->K, S);
+    return swiglu_impl(ctx, h, M, w13, w2, residual_w13, residual_w2, hidden, hidden != nullptr,
+                       out, x_res, gate, w13->K, S);
 }
 
 int iro_hip_dit_adaln_apply(IroHipContext *ctx, const float *x, int B, int S, int D,

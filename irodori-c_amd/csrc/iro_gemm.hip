@@ -309,6 +309,213 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel_o2(KParams p) {
     gemm_tile_body<CONV, EPI, TWO, TI, TJ>(p);
 }
 
+// ---- SwiGLU hidden state quantized in the W1/W3 kernel ------------------
+//
+// Instead of storing the hidden state in fp32 for a row quantization
+// launch (ops.c:321-348, two-term ops.c:427-442: the W2 input of
+// dit.c:958-966), the W1/W3 kernel can quantize it itself.  A row's range
+// needs all of its columns, and the columns of a 64-row band come from the
+// band's groups_n blocks, so those blocks exchange per-row partial ranges
+// through device memory: each block merges its partials with agent-scope
+// atomic max on magnitudes (lo <= 0 <= hi, and non-negative floats order
+// like their bit patterns), counts itself in and waits until the whole
+// band has; min and max are exact in any order, so the merged range is the
+// row's range and the codes are those of the row quantizer.  Agent-scope
+// read-modify-writes are coherent across the XCDs' L2 caches, and every
+// exchange goes through them.  The host launches this form only when the
+// whole grid is resident at once, so every wait ends; a bounded spin still
+// sets the device error word and gives up rather than hang.  The block
+// that leaves its band last zeroes the band's state for the next launch.
+
+// Wave-uniform min / max over each row of 16 lanes (DPP), in every lane.
+__device__ __forceinline__ float row16_min(float v) {
+    v = __builtin_fminf(v, dpp_mov<0xB1>(v));
+    v = __builtin_fminf(v, dpp_mov<0x4E>(v));
+    v = __builtin_fminf(v, dpp_mov<0x141>(v));
+    return __builtin_fminf(v, dpp_mov<0x140>(v));
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = __builtin_fmaxf(v, dpp_mov<0xB1>(v));
+    v = __builtin_fmaxf(v, dpp_mov<0x4E>(v));
+    v = __builtin_fmaxf(v, dpp_mov<0x141>(v));
+    return __builtin_fmaxf(v, dpp_mov<0x140>(v));
+}
+
+// w holds the codes of rows e = 0..3 (byte e) of this lane's column;
+// across each quad of lanes the 4 x 4 bytes are transposed, so lane
+// 4q + k returns row k's codes of the quad's columns (byte c = column c of
+// the quad).  Two butterfly stages: exchange with lane ^ 1, then lane ^ 2,
+// v_perm_b32 picking the kept and received bytes.
+__device__ __forceinline__ uint32_t quad_transpose(uint32_t w, int lane) {
+    uint32_t p = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xB1, 0xF, 0xF, true);
+    w = __builtin_amdgcn_perm(p, w, (lane & 1) ? 0x03070105u : 0x06020400u);
+    p = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x4E, 0xF, 0xF, true);
+    return __builtin_amdgcn_perm(p, w, (lane & 2) ? 0x03020706u : 0x05040100u);
+}
+
+// The SwiGLU epilogue's values (dit.c:945-956 as EPI_SWIGLU computes them
+// from raw sums that already include 128 * rowsum) kept in registers: the
+// wave's one W1/W3 column-block pair, h[i][r] at row
+// m0 + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4.  Rows past M and columns
+// past the hidden width hold 0, which lies inside every row range and
+// leaves every range and code of the valid rows unchanged.
+template <int CONV, int TI, int BM>
+__device__ __forceinline__ void swiglu_hold(const KParams &p, const v16i (&acc)[TI][2],
+                                            const ColParams<2> &cp, const RowLds<BM, false> &rl,
+                                            const uint64_t *exptab, int m0, int nb0, int lane,
+                                            float (&h)[TI][16]) {
+    const int half = lane >> 5;
+    const bool hok = (nb0 >> 1) * 32 + (lane & 31) < p.hidden_n;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        float sx[16];
+        int zx[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int rb = i * 32 + g * 8 + half * 4;
+            const float4 s4 = *reinterpret_cast<const float4 *>(&rl.sx[0][rb]);
+            const int4 z4 = *reinterpret_cast<const int4 *>(&rl.zx[0][rb]);
+            sx[g * 4 + 0] = s4.x; sx[g * 4 + 1] = s4.y; sx[g * 4 + 2] = s4.z; sx[g * 4 + 3] = s4.w;
+            zx[g * 4 + 0] = z4.x; zx[g * 4 + 1] = z4.y; zx[g * 4 + 2] = z4.z; zx[g * 4 + 3] = z4.w;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float y[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float t = (float)(acc[i][j][r] - __mul24(zx[r], cp.cs[j]));
+                y[j] = t * (sx[r] * cp.sw[j]);
+            }
+            const bool ok = hok && m0 + i * 32 + (r >> 2) * 8 + (r & 3) + half * 4 < p.M;
+            const float v = silu_mul(y[0], y[1], exptab);
+            h[i][r] = ok ? v : 0.0f;
+        }
+    }
+}
+
+// This block's partial ranges of every row of the band (both held slabs),
+// merged over the wave's 32 columns per row with DPP and over the waves
+// with LDS atomics into s_lo / s_hi (magnitude bits).
+template <int TI>
+__device__ __forceinline__ void band_partials(const float (&h)[2][TI][16], unsigned *s_lo,
+                                              unsigned *s_hi, int lane) {
+    const int half = lane >> 5;
+    const bool lead = (lane & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float lo =
+                row16_min(__builtin_fminf(__builtin_fminf(h[0][i][r], h[1][i][r]), 0.0f));
+            const float hi =
+                row16_max(__builtin_fmaxf(__builtin_fmaxf(h[0][i][r], h[1][i][r]), 0.0f));
+            if (lead) {
+                const int row = i * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                atomicMax(&s_lo[row], __float_as_uint(lo) & 0x7fffffffu);
+                atomicMax(&s_hi[row], __float_as_uint(hi) & 0x7fffffffu);
+            }
+        }
+}
+
+// Thread 0: count this block into the band and wait for the rest (bounded;
+// error bit 8 past the limit, and no further waiting once it is set).
+__device__ __forceinline__ void band_arrive_wait(unsigned *ctr, unsigned nblk, int *err,
+                                                 int spin_limit) {
+    unsigned seen = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    for (int n = 0; seen < nblk; ++n) {
+        if (n >= spin_limit) {
+            __hip_atomic_fetch_or(err, 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        if ((n & 63) == 63 &&
+            (__hip_atomic_fetch_or(err, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 8))
+            break;
+        __builtin_amdgcn_s_sleep(1);
+        seen = __hip_atomic_fetch_or(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// One range phase of the band: publish this block's partials, wait for the
+// band, and leave the rows' parameters in s_rq (and, from the band's first
+// block, in s / z).  All threads of the block take part.
+template <int CONV, int BM>
+__device__ __forceinline__ void band_phase(const KParams &p, unsigned *cnt, unsigned *rng,
+                                           const unsigned (&s_lo)[BM], const unsigned (&s_hi)[BM],
+                                           float4 (&s_rq)[BM], float *s, int32_t *z, int m0,
+                                           bool first, int tid) {
+    __syncthreads();
+    if (tid < 2 * BM) {
+        const int row = tid % BM, which = tid / BM;
+        const unsigned v = which ? s_hi[row] : s_lo[row];
+        if (v && m0 + row < p.M)
+            (void)__hip_atomic_fetch_max(&rng[4 * row + which], v, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // every merge of this block has been performed before it counts itself
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
+    __syncthreads();
+    if (tid == 0) band_arrive_wait(cnt, (unsigned)p.groups_n, p.err, p.spin_limit);
+    __syncthreads();
+    if (tid < BM) {
+        const unsigned ulo = __hip_atomic_fetch_or(&rng[4 * tid], 0u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned uhi = __hip_atomic_fetch_or(&rng[4 * tid + 1], 0u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+        const RowQ r = row_params<CONV>(-__uint_as_float(ulo), __uint_as_float(uhi));
+        s_rq[tid] = make_float4(r.s, r.inv, r.zpf, __int_as_float(r.zp));
+        if (first && m0 + tid < p.M) {
+            s[m0 + tid] = r.s;
+            z[m0 + tid] = r.zp;
+        }
+    }
+    __syncthreads();
+}
+
+// Codes of the held values with the rows' parameters in s_rq, stored as
+// signed codes at (row, column) of q; with RES the values become the
+// remainders x - s (q - zp) (ops.c:437-439) for the second plane.
+template <int CONV, int TI, int BM, bool RES>
+__device__ __forceinline__ void band_codes(const KParams &p, float (&h)[2][TI][16],
+                                           const float4 (&s_rq)[BM], uint8_t *q, int m0,
+                                           const int (&hcol)[2], const bool (&colok)[2],
+                                           int lane) {
+    const int half = lane >> 5, k = lane & 3;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            RowQ rq[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 f = s_rq[i * 32 + g * 8 + half * 4 + e];
+                rq[e].s = f.x;
+                rq[e].inv = f.y;
+                rq[e].zpf = f.z;
+                rq[e].zp = __float_as_int(f.w);
+            }
+            const int row = m0 + i * 32 + g * 8 + half * 4 + k;
+#pragma unroll
+            for (int sl = 0; sl < 2; ++sl) {
+                float *v = &h[sl][i][g * 4];
+                const uint32_t w = pack_codes4(quant_pre<CONV>(v[0], rq[0]),
+                                               quant_pre<CONV>(v[1], rq[1]),
+                                               quant_pre<CONV>(v[2], rq[2]),
+                                               quant_pre<CONV>(v[3], rq[3]));
+                if (RES) {
+                    const float4 c = unpack_codes4(w);
+                    v[0] = residual_value<CONV>(v[0], c.x, rq[0]);
+                    v[1] = residual_value<CONV>(v[1], c.y, rq[1]);
+                    v[2] = residual_value<CONV>(v[2], c.z, rq[2]);
+                    v[3] = residual_value<CONV>(v[3], c.w, rq[3]);
+                }
+                const uint32_t t = quad_transpose(w, lane) ^ 0x80808080u;
+                if (colok[sl] && row < p.M)
+                    *reinterpret_cast<uint32_t *>(q + (size_t)row * p.ldhq + hcol[sl] +
+                                                  4 * ((lane & 31) >> 2)) = t;
+            }
+        }
+}
+
 // Whole-tile kernel (one activation plane, K <= 1024, codes stored signed):
 // the block's entire 64-row activation tile, 64 x K bytes, is copied into
 // LDS by direct global-to-LDS loads (global_load_lds_dwordx4: lane L of a
@@ -324,10 +531,13 @@ __global__ __launch_bounds__(256, 2) void gemm_tile_kernel_o2(KParams p) {
 // slab's first R k blocks are in flight while this slab's epilogue runs.
 // k past K is copied from a zero page.  The accumulators start at
 // 128 * rowsum[n] (the signed-operand correction), so they end as the
-// reference's raw u8 x s8 sums.
-template <int CONV, int EPI, int TJ, int R, int TI>
+// reference's raw u8 x s8 sums.  BQ: the SwiGLU hidden state is held in
+// registers over the block's (at most two) slabs and quantized by the
+// band exchange above instead of stored.
+template <int CONV, int EPI, int TJ, int R, int TI, bool BQ = false>
 __global__ __launch_bounds__(256, (TI == 2 && (EPI == EPI_QKVG || EPI == EPI_SWIGLU)) ? 2 : 1) void gemm_wt_kernel(KParams p) {
     static_assert(TI == 2 || TI == 4, "64- or 128-row tiles");
+    static_assert(!BQ || (EPI == EPI_SWIGLU && TI == 2 && TJ == 2), "band quantization: W1/W3, 64 x 256");
     constexpr int BM = 32 * TI, KMAX = 1024;
     constexpr int P = R * TI / 4;  // activation pieces per thread per ring turn
     // Sweeping several slabs pays for the projections with the largest N
@@ -338,6 +548,9 @@ __global__ __launch_bounds__(256, (TI == 2 && (EPI == EPI_QKVG || EPI == EPI_SWI
     __shared__ __attribute__((aligned(16))) uint8_t lds_sink[1024];  // never read
     __shared__ __attribute__((aligned(16))) RowLds<BM, false> rl;
     __shared__ uint64_t exptab[32];
+    __shared__ unsigned s_rng[BQ ? 4 : 1][BQ ? BM : 1];  // |lo|, hi of each range phase
+    __shared__ float4 s_rq[BQ ? BM : 1];                  // s, inv, zp (float), zp (int bits)
+    __shared__ int s_last;
 
     // Work item = (row tile, group of spb slabs), dealt to the XCDs in the
     // order that splits the larger operand (see tile_of).
@@ -352,6 +565,15 @@ __global__ __launch_bounds__(256, (TI == 2 && (EPI == EPI_QKVG || EPI == EPI_SWI
 
     stage_rows<EPI, false, BM>(p, rl, m0, tid);
     if (EPI == EPI_SWIGLU && tid < 32) exptab[tid] = kExp2Tab[tid];
+    if constexpr (BQ) s_rng[tid / BM][tid % BM] = 0;  // 4 * BM == 256 threads
+    // BQ: hs[1] holds the current slab's values, hs[0] the previous slab's
+    float hs[BQ ? 2 : 1][BQ ? TI : 1][16];
+    if constexpr (BQ) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) hs[1][i][r] = 0.0f;
+    }
 
     const int nkb = (p.K + 31) / 32;             // k blocks holding activation data
     const int nkr = (nkb + R - 1) / R * R;       // whole ring turns (<= KMAX / 32)
@@ -465,7 +687,48 @@ __global__ __launch_bounds__(256, (TI == 2 && (EPI == EPI_QKVG || EPI == EPI_SWI
             }
             if (sl == 0) copy_turn(t + 2);
         }
-        epilogue<CONV, EPI, false, TI, TJ, BM, true>(p, acc, acc2, cp, rl, exptab, m0, nb0, lane);
+        if constexpr (BQ) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) hs[0][i][r] = hs[1][i][r];
+            swiglu_hold<CONV, TI, BM>(p, acc, cp, rl, exptab, m0, nb0, lane, hs[1]);
+        } else {
+            epilogue<CONV, EPI, false, TI, TJ, BM, true>(p, acc, acc2, cp, rl, exptab, m0, nb0,
+                                                         lane);
+        }
+    }
+    if constexpr (BQ) {
+        // hs[1] is slab nslab - 1, hs[0] slab 0 when there were two (else
+        // zeros); wave column block of slab s: (bx0 + s) * 4 + wave.
+        const int hcol[2] = {(bx0 * 4 + wave) * 32, ((bx0 + nslab - 1) * 4 + wave) * 32};
+        const bool colok[2] = {nslab == 2 && hcol[0] < p.hidden_n, hcol[1] < p.hidden_n};
+        unsigned *cnt = p.band_cnt + 4 * by;
+        unsigned *rng = p.band_rng + 4 * (size_t)m0;
+        const bool first = gx == 0;
+        band_partials<TI>(hs, s_rng[0], s_rng[1], lane);
+        band_phase<CONV, BM>(p, cnt, rng, s_rng[0], s_rng[1], s_rq, p.hs1, p.hz1, m0, first, tid);
+        if (p.hq2) {
+            band_codes<CONV, TI, BM, true>(p, hs, s_rq, p.hq1, m0, hcol, colok, lane);
+            band_partials<TI>(hs, s_rng[2], s_rng[3], lane);
+            band_phase<CONV, BM>(p, cnt + 1, rng + 2, s_rng[2], s_rng[3], s_rq, p.hs2, p.hz2, m0,
+                                 first, tid);
+            band_codes<CONV, TI, BM, false>(p, hs, s_rq, p.hq2, m0, hcol, colok, lane);
+        } else {
+            band_codes<CONV, TI, BM, false>(p, hs, s_rq, p.hq1, m0, hcol, colok, lane);
+        }
+        // Every block of the band has read the merged ranges once it has
+        // departed: the last one zeroes the band's state.
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(cnt + 2, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT) + 1 == (unsigned)p.groups_n;
+        __syncthreads();
+        if (s_last) {
+            (void)__hip_atomic_fetch_and(&rng[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (tid < 3)
+                (void)__hip_atomic_fetch_and(&cnt[tid], 0u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     // No copy into this block's LDS may still be in flight when it exits.
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
@@ -590,6 +853,13 @@ enum Mode { MODE_TILE = 0, MODE_SKINNY = 1, MODE_WHOLE = 2 };
 
 template <int CONV, int EPI>
 void launch_wt(const KParams &kp, int ti, int tj, int ring, unsigned grid, hipStream_t st) {
+    if constexpr (EPI == EPI_SWIGLU) {
+        if (kp.hq1) {  // the caller checked ti == 2, tj == 2, ring 4
+            hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 2, 4, 2, true>), dim3(grid), dim3(256),
+                               0, st, kp);
+            return;
+        }
+    }
     if (ti == 4) {
         if (tj == 1)
             hipLaunchKernelGGL((gemm_wt_kernel<CONV, EPI, 1, 8, 4>), dim3(grid), dim3(256), 0, st,
@@ -633,6 +903,51 @@ void launch_c(const KParams &kp, Epi epi, bool two, Mode mode, TileCfg t, int ri
         case EPI_SWIGLU: launch_e<CONV, EPI_SWIGLU>(kp, two, mode, t, ring, grid, st); break;
         case EPI_GATED: launch_e<CONV, EPI_GATED>(kp, two, mode, t, ring, grid, st); break;
     }
+}
+
+// Whether the band-quantizing W1/W3 kernel can take a launch of `grid`
+// blocks whose shape fits it (`shape`): no concurrent chain of launches
+// shares the GPU (a context workspace override marks one) and the GPU holds
+// every block at once, so no block waits for one that cannot start.  Then
+// the band state is sized (allocated zeroed, outside graph capture) and
+// its pointers set: returns 0.  Returns 1 to decline, -1 on error.
+int band_quant_setup(IroHipContext *ctx, KParams &kp, bool shape, unsigned grid) {
+    if (!shape || !ctx->band_quant || ctx->ws_override) return 1;
+    const int conv = ctx->convention == IRO_HIP_GCC_FASTMATH ? 1 : 0;
+    if (!ctx->band_occ[conv]) {
+        int n = 0;
+        const hipError_t e =
+            conv ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                       &n, reinterpret_cast<const void *>(
+                               &gemm_wt_kernel<1, EPI_SWIGLU, 2, 4, 2, true>), 256, 0)
+                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                       &n, reinterpret_cast<const void *>(
+                               &gemm_wt_kernel<0, EPI_SWIGLU, 2, 4, 2, true>), 256, 0);
+        if (e != hipSuccess) return set_error(ctx, "gemm: occupancy query failed");
+        ctx->band_occ[conv] = n > 0 ? n : -1;
+    }
+    const int cus = ctx->cus > 0 ? ctx->cus : 256;
+    if (ctx->band_occ[conv] < 0 || (long long)grid > (long long)ctx->band_occ[conv] * cus)
+        return 1;
+    // [tiles_m][4] counters, then [64 tiles_m][4] row ranges
+    const size_t need = sizeof(unsigned) * 4 * (size_t)kp.tiles_m * 65;
+    if (need > ctx->band_state_bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess ||
+            cs != hipStreamCaptureStatusNone)
+            return 1;  // never allocate under capture: the eager run sized it
+        IRO_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->band_state) (void)hipFree(ctx->band_state);
+        ctx->band_state = nullptr;
+        ctx->band_state_bytes = 0;
+        const size_t bytes = round_up(need, 4096);
+        IRO_HIP_TRY(ctx, hipMalloc(&ctx->band_state, bytes));
+        if (launch_fill(ctx, ctx->band_state, 0, bytes)) return -1;
+        ctx->band_state_bytes = bytes;
+    }
+    kp.band_cnt = ctx->band_state;
+    kp.band_rng = ctx->band_state + 4 * (size_t)kp.tiles_m;
+    return 0;
 }
 
 // Tile choice (measured on MI355X at the DiT shapes): 64-row tiles keep
@@ -724,11 +1039,16 @@ int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K) {
     if (ctx->gemm_lds == 0 && epi != EPI_QKVG) return 0;
     int cfg = ctx->gemm_lds > 0 ? ctx->gemm_lds : LDS_192x256_CFG;
     // Few rows: 96 x 128 tiles keep every CU busy (measured at M = 750,
-    // N = 4096: 15.4 us against 22.0 for 192 x 256).
+    // N = 4096: 15.4 us against 22.0 for 192 x 256).  Past K = 1024 the
+    // tile kernel is faster there (M = 750, K = 1280, N = 5120: 17.4 us
+    // against 27.3 for 96 x 128 and 21-24 for the larger shapes).
     if (ctx->gemm_lds == 0) {
         const int cus = ctx->cus > 0 ? ctx->cus : 256;
         // the QKVG output is 4K wide: K / 64 column tiles of 256
-        if ((long long)((M + 191) / 192) * (K / 64) * 2 < cus) cfg = LDS_96x128_CFG;
+        if ((long long)((M + 191) / 192) * (K / 64) * 2 < cus) {
+            if (K > 1024) return 0;
+            cfg = LDS_96x128_CFG;
+        }
     }
     return lds_cfg_ok(cfg, two, epi) ? cfg : 0;
 }
@@ -789,6 +1109,21 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     if ((long long)w->Np * w->Kp >= (1LL << 31))
         return set_error(ctx, "gemm: packed weight of %d x %d bytes exceeds 2 GiB", w->Np, w->Kp);
     kp.wbytes = w->Np * w->Kp;
+    const bool bq = a.hq1 != nullptr;
+    kp.hq1 = a.hq1;
+    kp.hq2 = a.hq2;
+    kp.ldhq = a.ldhq;
+    kp.hs1 = a.hs1;
+    kp.hs2 = a.hs2;
+    kp.hz1 = a.hz1;
+    kp.hz2 = a.hz2;
+    kp.band_cnt = kp.band_rng = nullptr;
+    kp.err = ctx->dev_err;
+    kp.spin_limit = 1 << 20;
+    if (bq && (epi != EPI_SWIGLU || !a.hs1 || !a.hz1 || (a.hq2 && (!a.hs2 || !a.hz2)) ||
+               a.ldhq < w->part_N[0] || a.ldhq % 4 || (((uintptr_t)a.hq1) & 3) ||
+               (((uintptr_t)a.hq2) & 3)))
+        return set_error(ctx, "gemm: invalid hidden-state code buffers");
     // Signed codes with whole k blocks take the LDS-pipelined kernel.
     int lcfg = a.a_signed ? gemm_lds_cfg(ctx, epi, two, a.M, a.K) : 0;
     if (lcfg) {
@@ -799,6 +1134,7 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     kp.akbp = a.a_kbp;
     if (a.a_kbp > 0 && (!lcfg || a.a_kbp * 32 != a.K))
         return set_error(ctx, "gemm: fragment-layout codes need the LDS-pipelined kernel");
+    if (lcfg && bq) return 1;
     if (lcfg) {
         int bm = 0, bn = 0;
         lds_tile_shape(lcfg, &bm, &bn);
@@ -888,6 +1224,11 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
             grid = (unsigned)(8 * kp.tiles_per_xcd);
         }
     }
+    if (bq) {
+        const int rc = band_quant_setup(ctx, kp, mode == MODE_WHOLE && t.ti == 2 && t.tj == 2 &&
+                                                     ring == 4 && kp.spb <= 2, grid);
+        if (rc) return rc;
+    }
     prof_begin(ctx);
     if (ctx->convention == IRO_HIP_GCC_FASTMATH)
         launch_c<1>(kp, epi, two, mode, t, ring, grid, ctx->stream);
@@ -909,6 +1250,11 @@ void gemm_prof_end(IroHipContext *ctx, const GemmArgs &a, const IroHipWeight *w,
         out_bytes *= 1 + (a.accumulate ? 1 : 0) + (a.work ? 1 : 0);
     } else if (epi == EPI_QKVG) {
         kind = two ? PK_GEMM_QKVG_2T : PK_GEMM_QKVG;
+    } else if (epi == EPI_SWIGLU && a.hq1) {
+        // W1/W3 quantizing its hidden state: codes of each plane, row
+        // parameters
+        kind = PK_GEMM_SWIGLU_Q;
+        out_bytes = (M * N / 2 + 8 * M) * (a.hq2 ? 2 : 1);
     } else if (epi == EPI_SWIGLU) {
         kind = two ? PK_GEMM_SWIGLU_2T : PK_GEMM_SWIGLU;
         out_bytes /= 2;

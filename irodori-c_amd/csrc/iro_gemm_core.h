@@ -51,6 +51,17 @@ struct KParams {
     const uint8_t *zero16; // 256 zero bytes
     int wbytes;            // bytes of the packed weight (< 2^31)
     int akbp;              // > 0: A codes in the MFMA fragment layout, akbp k blocks per row block
+    // SwiGLU epilogue that quantizes the hidden state itself (hq1 set):
+    // signed codes [M, ldhq] of each plane, row scales and zero points, and
+    // the band exchange state (per band: arrivals of the two range phases
+    // and departures; per row: |lo|, hi of each phase as float bits).
+    uint8_t *hq1, *hq2;
+    int ldhq;
+    float *hs1, *hs2;
+    int32_t *hz1, *hz2;
+    unsigned *band_cnt, *band_rng;
+    int *err;
+    int spin_limit;
 };
 
 namespace {

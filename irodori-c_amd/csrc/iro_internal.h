@@ -27,6 +27,7 @@ enum ProfKind {
     PK_CONVT_GATHER,
     PK_PERSIST_STACK,
     PK_SNAKE,
+    PK_GEMM_SWIGLU_Q,
     PK_OTHER,
     PK_COUNT
 };
@@ -65,6 +66,11 @@ struct IroHipContext {
     int gemm_lds = 0;     // LDS-pipelined GEMM: 0 shape chosen per GEMM, -1 off, > 0 forced shape
     int gemm_wt_rows = 0; // rows per whole-tile block: 0 chosen per GEMM, 64 or 128
     int conv_fused = 1;   // kernel-7 convolutions: window ranges and codes in one pass
+    int band_quant = 0;   // W1/W3 kernel quantizes the SwiGLU hidden state itself (opt-in)
+    // band exchange state of that kernel: zero between launches
+    unsigned *band_state = nullptr;
+    size_t band_state_bytes = 0;
+    int band_occ[2] = {0, 0};  // resident blocks per CU of its two conventions' kernels
     iro::ProfState *prof = nullptr;  // non-null while profiling is on
     float *rope = nullptr;  // rotation table: per position cos[32] then sin[32]
     int rope_S = 0;         // positions held by rope
@@ -219,6 +225,14 @@ struct GemmArgs {
     int a_signed = 0;  // codes already stored as a ^ 0x80 (quantize_into)
     int a_kbp = 0;     // > 0: codes in the MFMA fragment layout with a_kbp k blocks
                        // per 32-row block (LDS-pipelined kernel only)
+    // EPI_SWIGLU only: when hq1 is set the kernel quantizes the hidden state
+    // itself (one plane, two with hq2) into these row-major signed codes
+    // instead of storing it; launch_gemm returns 1, launching nothing, when
+    // the GEMM's shape does not allow that.
+    uint8_t *hq1 = nullptr, *hq2 = nullptr;
+    int ldhq = 0;
+    float *hs1 = nullptr, *hs2 = nullptr;
+    int32_t *hz1 = nullptr, *hz2 = nullptr;
 };
 
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi);

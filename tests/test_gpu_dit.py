@@ -134,6 +134,62 @@ def test_swiglu_mlp_single_term_w2(ctx, oracle):
     assert_bits_equal(got, want, "x += gate * W2(one-term)")
 
 
+# The bench's rows, one CFG branch, a last band of 2 rows (M = 130), and a
+# hidden width (320) that leaves padded 32-column blocks in the last slab.
+BAND_SHAPES = [  # (B, S, D, H)
+    (3, 750, 1024, 2816),
+    (1, 750, 1024, 2816),
+    (2, 65, 256, 320),
+]
+
+
+@pytest.mark.parametrize("B,S,D,H", BAND_SHAPES)
+@pytest.mark.parametrize("residual_w2", [True, False], ids=["two-term", "one-term"])
+def test_swiglu_band_quant_equals_row_quant(ctx, B, S, D, H, residual_w2):
+    """With the band quantization switched on and no hidden buffer, the
+    W1/W3 kernel quantizes the hidden state itself (the blocks of each
+    64-row band merge their row ranges through device memory); x must equal
+    the path that stores the hidden state in fp32 and quantizes its rows, on
+    two launches in a row and then on fewer rows (the band state is back to
+    zero after every launch)."""
+    M = B * S
+    h = heavy_tail(gauss(51, (M, D)), 52)  # ranges set by a few columns
+    w1, w3 = gauss(53, (H, D), 0.02), gauss(54, (H, D), 0.02)
+    w2 = gauss(55, (D, H), 0.02)
+    gate = ctx.to_device(gauss(56, (B, D), 0.5))
+    x0 = gauss(57, (M, D))
+    W13 = ctx.weight_fused([ctx.to_device(w1), ctx.to_device(w3)], [H, H], D, layout=1)
+    W2 = ctx.weight(ctx.to_device(w2), D, H)
+    hd = ctx.to_device(h)
+    hidden = ctx.empty((M, H), np.float32)
+
+    def run(rows, b, s, hid):
+        xres = ctx.to_device(x0[:rows])
+        ctx.dit_swiglu(hd, rows, W13, W2, residual_w2=residual_w2, hidden=hid, x_res=xres,
+                       gate=gate, S=s)
+        ctx.sync()  # a band wait that gave up is reported here
+        return xres.numpy()
+
+    want = run(M, B, S, hidden)
+    ctx.set_gemm_tile(-7, 1)
+    ctx.profile(True)
+    ctx.profile_reset()
+    try:
+        first = run(M, B, S, None)
+        second = run(M, B, S, None)
+        M2 = M // 3 if M >= 99 else M - 33
+        want2 = run(M2, 1, M2, hidden)
+        third = run(M2, 1, M2, None)
+        kinds = ctx.profile_read()
+    finally:
+        ctx.profile(False)
+        ctx.set_gemm_tile(-7, 0)
+    assert kinds.get("gemm_swiglu_quant", (0,))[0] == 3, f"fused W1/W3 not taken: {kinds}"
+    assert_bits_equal(first, want, "band-quantized hidden state, first launch")
+    assert_bits_equal(second, want, "band-quantized hidden state, second launch")
+    assert_bits_equal(third, want2, f"band-quantized hidden state at {M2} rows")
+
+
 @pytest.mark.parametrize("B,S,D", [
     (3, 750, 1024), (3, 40, 1280), (1, 1, 1024),    # registers, 2 rows per wave
     (2, 5, 600), (1, 3, 1500),                      # partial chunks; 1 row per wave
