@@ -1105,6 +1105,115 @@ def convt_main(args):
     print(json.dumps(out), flush=True)
 
 
+def vendor_gemm_main(args):
+    """The vendor library's int8 GEMM beside this library's fused kernels at
+    the same shapes: hipBLASLt through torch._int_mm (s8 x s8 -> s32, no
+    dequantization, activation, quantization or fp32 store; B given
+    row-major and column-major, the faster counted) against the event
+    profiler's mean launch time of the stack's four GEMM kinds (an eagerly
+    launched step at M = 2250 and at M = 750, D = 1024, H = 2816) and of
+    the kernel-7 Conv1d's GEMM (T = 24000, 512 -> 512).  The two-term W2
+    runs two activation planes per launch; the vendor figure for it is two
+    single-plane calls.  A reference point for what the hardware and its
+    library reach at these sizes, not a parity check."""
+    import torch
+    D, H, blocks = args.hidden, args.mlp, 2
+    base = base_weights(D, H)
+    ctx = iro_hip.Context(0, iro_hip.STRICT)
+    log("backend:", ctx.backend())
+    stack = iro_hip.DiTStack(ctx, blocks, D, H, args.residual_mask)
+    for b in range(blocks):
+        dev = [ctx.to_device(w) for w in block_weights(base, b)]
+        stack.set_block(b, *dev)
+        for a in dev:
+            a.free()
+    ours = {}
+    for B in (3, 1):
+        M = B * args.frames
+        xd = ctx.to_device(gauss(7, (M, D)))
+        cd = ctx.to_device(gauss(8, (B, D), 0.1))
+        for _ in range(2):
+            stack.step(xd, cd, B, args.frames)
+        ctx.sync()
+        ctx.profile(True)
+        ctx.profile_reset()
+        for _ in range(3):
+            stack.step(xd, cd, B, args.frames)
+        prof = ctx.profile_read()
+        ctx.profile(False)
+        for kind, (n_, ms, _ops, _by) in prof.items():
+            ours[(M, kind)] = ms * 1e3 / n_
+    T, Cin, N, k, st, dil, pad = CONV_WORKLOADS["conv7"]
+    W = ctx.weight(ctx.to_device(gauss(43, (N, k * Cin), 0.02)), N, k * Cin)
+    xc, bc = ctx.to_device(gauss(42, (T, Cin))), ctx.to_device(gauss(44, (N,), 0.01))
+    yc = ctx.empty((T, N), np.float32)
+    for _ in range(2):
+        ctx.conv1d(xc, T, Cin, W, k, st, dil, pad, bc, False, yc)
+    ctx.sync()
+    ctx.profile(True)
+    ctx.profile_reset()
+    for _ in range(5):
+        ctx.conv1d(xc, T, Cin, W, k, st, dil, pad, bc, False, yc)
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    ours[(T, "conv7")] = prof["gemm_linear"][1] * 1e3 / prof["gemm_linear"][0]
+    ctx.close()
+
+    def vendor_us(M, K, N):
+        a = torch.randint(-128, 127, (M, K), dtype=torch.int8, device="cuda")
+        b = torch.randint(-128, 127, (K, N), dtype=torch.int8, device="cuda")
+        best = None
+        for bb in (b, b.t().contiguous().t()):
+            torch._int_mm(a, bb)
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                torch._int_mm(a, bb)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / args.steps
+            best = us if best is None else min(best, us)
+        return best
+
+    rows = []
+    for M in (3 * args.frames, args.frames):
+        for name, kind, K, Nn, planes in (("QKVG", "gemm_qkvg", D, 4 * D, 1),
+                                          ("Wo + gated residual", "gemm_gated", D, D, 1),
+                                          ("W1/W3 + SiLU gate", "gemm_swiglu", D, 2 * H, 1),
+                                          ("W2 two-term + gated residual", "gemm_gated_two_term",
+                                           H, D, 2)):
+            rows.append((f"{name}, M={M}", M, K, Nn, planes, ours[(M, kind)],
+                         planes * vendor_us(M, K, Nn)))
+    rows.append(("Conv1d k7 GEMM + bias, T=24000", T, k * Cin, N, 1, ours[(T, "conv7")],
+                 vendor_us(T, k * Cin, N)))
+    shapes = []
+    for name, M, K, Nn, planes, o, v in rows:
+        ops = 2.0 * M * K * Nn * planes
+        log(f"{name:38s} ours {o:8.2f} us ({ops / o / 1e6:7.1f} TOPS)   "
+            f"hipBLASLt {v:8.2f} us ({ops / v / 1e6:7.1f} TOPS)")
+        shapes.append({"gemm": name, "M": M, "K": K, "N": Nn, "planes": planes,
+                       "ours_us": round(o, 2), "ours_tops": round(ops / o / 1e6, 1),
+                       "vendor_us": round(v, 2), "vendor_tops": round(ops / v / 1e6, 1)})
+    ratio = sum(r[6] for r in rows) / sum(r[5] for r in rows)
+    sq = vendor_us(8192, 8192, 8192)
+    sq_tops = 2.0 * 8192 ** 3 / sq / 1e6
+    log(f"hipBLASLt 8192 x 8192 x 8192: {sq:.1f} us ({sq_tops:.1f} TOPS, "
+        f"{sq_tops / PEAK_INT8_TOPS:.3f} of peak)")
+    out = {
+        "metric": "int8 GEMM time at the stack's and the Conv1d's shapes: vendor library "
+                  "(hipBLASLt, s32 output, no epilogue) time / this library's fused kernels' time",
+        "value": round(ratio, 3), "unit": "x", "n_gpus": 1, "steps": args.steps,
+        "higher_is_better": True, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "vendor int8 GEMM comparison", "parallelism": "single GPU"},
+        "shapes": shapes,
+        "vendor_square_8192": {"us": round(sq, 1), "tops": round(sq_tops, 1),
+                               "frac_of_peak": round(sq_tops / PEAK_INT8_TOPS, 3)},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1121,7 +1230,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["stack", "weights", "adaln", "qknorm", "attention",
-                                           "block", "sampler-step", "decoder"]
+                                           "block", "sampler-step", "decoder", "vendor-gemm"]
                     + sorted(CONV_WORKLOADS)
                     + sorted(CONVT_WORKLOADS),
                     default="stack",
@@ -1178,6 +1287,9 @@ def main():
         return sampler_step_main(args)
     if args.workload == "block":
         block_main(args)
+        return
+    if args.workload == "vendor-gemm":
+        vendor_gemm_main(args)
         return
 
     B, S, D, H = args.batch, args.frames, args.hidden, args.mlp
