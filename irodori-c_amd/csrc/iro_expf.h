@@ -29,9 +29,12 @@ __constant__ uint64_t kExp2Tab[32] = {
 // cases are selected afterwards, so a wavefront never splits on them.  The
 // scale 2^(k/32) is built in 32-bit halves: (k << 47) only touches the high
 // word of the table entry.
-__device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
-    constexpr float hi = 0x1.62e42ep6f, lo = -0x1.9fe368p6f;  // overflow / underflow bounds
-    const float xc = __builtin_amdgcn_fmed3f(x, lo, hi);
+constexpr float kExpfHi = 0x1.62e42ep6f, kExpfLo = -0x1.9fe368p6f;  // overflow / underflow bounds
+
+// The table path alone, on x clamped into [kExpfLo, kExpfHi]: expf(x) for
+// every x in that range; outside it (and for NaN) the callers select.
+__device__ __forceinline__ float expf_glibc_table(float x, const uint64_t *tab) {
+    const float xc = __builtin_amdgcn_fmed3f(x, kExpfLo, kExpfHi);
     const double invln2n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
                  c2 = 0x1.62e42ff0c52d6p-1 / 32;
@@ -47,9 +50,13 @@ __device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
-    float e = (float)(y * s);
-    e = x > hi ? __builtin_inff() : e;  // overflow
-    e = x < lo ? 0.0f : e;              // underflow (and -inf)
+    return (float)(y * s);
+}
+
+__device__ __forceinline__ float expf_glibc(float x, const uint64_t *tab) {
+    float e = expf_glibc_table(x, tab);
+    e = x > kExpfHi ? __builtin_inff() : e;  // overflow
+    e = x < kExpfLo ? 0.0f : e;              // underflow (and -inf)
     return x != x ? x + x : e;
 }
 

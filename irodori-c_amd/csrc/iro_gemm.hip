@@ -47,7 +47,8 @@ namespace {
 // expf digest term (bits(x) * 0x9E3779B97F4A7C15) ^ (bits(e) *
 // 0xC2B2AE3D27D4EB4F), NaN results as 0x7FC00000, summed into out[0]; and
 // into out[1] the inputs a whose silu_div(a, 1 + expf(-a)) differs from the
-// IEEE quotient (NaN == NaN).
+// IEEE quotient (NaN == NaN), or, where silu_q_common takes a, whose
+// silu_q_common differs from it.
 __global__ __launch_bounds__(256) void silu_selfcheck_kernel(unsigned long long *out, unsigned base) {
     __shared__ uint64_t tab[32];
     __shared__ unsigned long long part[2][4];
@@ -61,7 +62,10 @@ __global__ __launch_bounds__(256) void silu_selfcheck_kernel(unsigned long long 
                            ((unsigned long long)ue * 0xC2B2AE3D27D4EB4Full);
     const float b = 1.0f + expf_glibc(-x, tab);
     const float q0 = x / b, q1 = silu_div(x, b);
-    unsigned long long bad = __float_as_uint(q0) != __float_as_uint(q1) && !(q0 != q0 && q1 != q1);
+    bool ok;
+    const float q2 = silu_q_common(x, tab, ok);
+    unsigned long long bad = (__float_as_uint(q0) != __float_as_uint(q1) && !(q0 != q0 && q1 != q1)) ||
+                             (ok && __float_as_uint(q0) != __float_as_uint(q2));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         h += __shfl_xor(h, off, 64);
@@ -378,17 +382,20 @@ __device__ __forceinline__ void swiglu_hold(const KParams &p, const v16i (&acc)[
             sx[g * 4 + 0] = s4.x; sx[g * 4 + 1] = s4.y; sx[g * 4 + 2] = s4.z; sx[g * 4 + 3] = s4.w;
             zx[g * 4 + 0] = z4.x; zx[g * 4 + 1] = z4.y; zx[g * 4 + 2] = z4.z; zx[g * 4 + 3] = z4.w;
         }
+        float y[2][16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float y[2];
+        for (int r = 0; r < 16; ++r)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const float t = (float)(acc[i][j][r] - __mul24(zx[r], cp.cs[j]));
-                y[j] = t * (sx[r] * cp.sw[j]);
+                y[j][r] = t * (sx[r] * cp.sw[j]);
             }
+        float v[16];
+        silu_mul16(y[0], y[1], exptab, v);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
             const bool ok = hok && m0 + i * 32 + (r >> 2) * 8 + (r & 3) + half * 4 < p.M;
-            const float v = silu_mul(y[0], y[1], exptab);
-            h[i][r] = ok ? v : 0.0f;
+            h[i][r] = ok ? v[r] : 0.0f;
         }
     }
 }

@@ -121,6 +121,42 @@ __device__ __forceinline__ float silu_mul(float a, float g, const uint64_t *tab)
     return silu_div(a, 1.0f + e) * g;
 }
 
+// The quotient a / (1 + expf(-a)) on the gate's common inputs (ok):
+// -44 < a, |a| < 2^126, and |a| >= 2^-100 or a == 0.  There expf(-a) <
+// 2^64 cannot overflow, and where glibc's expf underflows to 0 (a > 103.97)
+// the table value of the clamped input is below 2^-24, so 1 + e is the
+// same without expf's special-case selects, and silu_div's fast quotient
+// applies (b < 2^64).  Inputs with ok false must take silu_mul.  Checked
+// against the IEEE quotient for every float a by iro_hip_selfcheck_silu.
+__device__ __forceinline__ float silu_q_common(float a, const uint64_t *tab, bool &ok) {
+    const float aa = __builtin_fabsf(a);
+    ok = a > -44.0f && aa < 0x1p126f && (aa >= 0x1p-100f || a == 0.0f);
+    const float b = 1.0f + expf_glibc_table(-a, tab);
+    const float y = __builtin_amdgcn_rcpf(b);
+    const float y1 = __builtin_fmaf(__builtin_fmaf(-b, y, 1.0f), y, y);
+    const float q0 = a * y1;
+    const float q = __builtin_fmaf(__builtin_fmaf(-b, q0, a), y1, q0);
+    return a == 0.0f ? a : q;
+}
+
+// silu_mul over 16 values: the common path for all of them, then one
+// (rarely taken) branch that redoes the others with silu_mul.
+__device__ __forceinline__ void silu_mul16(const float (&a)[16], const float (&g)[16],
+                                           const uint64_t *tab, float (&h)[16]) {
+    uint32_t rare = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        bool ok;
+        h[r] = silu_q_common(a[r], tab, ok) * g[r];
+        rare |= ok ? 0u : 1u << r;
+    }
+    if (__builtin_expect(rare != 0, 0)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if ((rare >> r) & 1u) h[r] = silu_mul(a[r], g[r], tab);
+    }
+}
+
 // Per-row parameters of a block's rows, staged in LDS: scale and zero
 // point of each plane and the gate row offset of the gated epilogue.
 template <int BM, bool TWO>
@@ -349,11 +385,12 @@ __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc
 #pragma unroll
             for (int j = 0; j + 1 < TJ; j += 2) {
                 const bool hok = FULL || ((nb0 + j) >> 1) * 32 + (lane & 31) < p.hidden_n;
+                float hv[16];
+                silu_mul16(yv[j], yv[j + 1], exptab, hv);
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float h = silu_mul(yv[j][r], yv[j + 1][r], exptab);
                     if (row_ok(r) && hok)
-                        __builtin_nontemporal_store(h, &p.hidden[(size_t)rowu(r) * p.ldh + offh[j / 2]]);
+                        __builtin_nontemporal_store(hv[r], &p.hidden[(size_t)rowu(r) * p.ldh + offh[j / 2]]);
                 }
             }
         }
