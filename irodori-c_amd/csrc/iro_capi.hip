@@ -755,7 +755,7 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
     // The one-pass kernel can store the signed operand form the
     // LDS-pipelined GEMM reads.
     const bool fused = conv_im2col7_ok(C, kernel, ldc) && ctx->conv_fused;
-    const bool sgn = fused && gemm_lds_cfg(ctx, EPI_LINEAR, residual != 0, T_out, ldc) != 0;
+    const bool sgn = fused && gemm_lds_cfg(ctx, EPI_LINEAR, residual != 0, T_out, ldc, w->N) != 0;
     if (fused) {
         if (launch_conv_im2col7(ctx, input, T, C, T_out, stride, dilation, padding, c1, c2, ldc,
                                 s1, z1, s2, z2, sgn))

@@ -1038,12 +1038,20 @@ int launch_silu_selfcheck(IroHipContext *ctx, unsigned long long *out) {
 void gemm_prof_end(IroHipContext *ctx, const GemmArgs &a, const IroHipWeight *w, Epi epi,
                    bool two);
 
-int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K) {
+int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K, int N) {
     if (M <= 32 || ctx->gemm_lds < 0 || K % 32) return 0;
-    // Default: the QKVG projection only (measured at 2250 x 1024 -> 4096:
-    // 23.2 us against 25.8 us for the register-streamed whole-tile kernel;
-    // the W1/W3, Wo and W2 shapes ran slower through it).
-    if (ctx->gemm_lds == 0 && epi != EPI_QKVG) return 0;
+    // Default: the QKVG projection (measured at 2250 x 1024 -> 4096: 23.2 us
+    // against 25.8 us for the register-streamed whole-tile kernel; the
+    // W1/W3, Wo and W2 shapes ran slower through it), and long, wide
+    // one-plane linears such as the kernel-7 Conv1d's GEMM (24000 rows,
+    // K = 3584, N = 512: 66.5 us against 71.3 us for the tile kernel; at
+    // 6000 rows, K = 7168, N = 256 it was slower, 60 against 34 us).
+    if (ctx->gemm_lds == 0 && epi != EPI_QKVG) {
+        if (epi == EPI_LINEAR && !two && M >= 16384 && K >= 2048 && N >= 512 &&
+            lds_cfg_ok(LDS_192x256_CFG, two, epi))
+            return LDS_192x256_CFG;
+        return 0;
+    }
     int cfg = ctx->gemm_lds > 0 ? ctx->gemm_lds : LDS_192x256_CFG;
     // Few rows: 96 x 128 tiles keep every CU busy (measured at M = 750,
     // N = 4096: 15.4 us against 22.0 for 192 x 256).  Past K = 1024 the
@@ -1132,7 +1140,7 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
                (((uintptr_t)a.hq2) & 3)))
         return set_error(ctx, "gemm: invalid hidden-state code buffers");
     // Signed codes with whole k blocks take the LDS-pipelined kernel.
-    int lcfg = a.a_signed ? gemm_lds_cfg(ctx, epi, two, a.M, a.K) : 0;
+    int lcfg = a.a_signed ? gemm_lds_cfg(ctx, epi, two, a.M, a.K, w->N) : 0;
     if (lcfg) {
         int bm = 0, bn = 0;
         lds_tile_shape(lcfg, &bm, &bn);

@@ -238,7 +238,7 @@ struct GemmArgs {
 int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi);
 // The LDS-pipelined kernel's shape a GEMM of M rows and k extent K with
 // signed codes would take, or 0 when it takes another kernel.
-int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K);
+int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K, int N = 0);
 int launch_silu_selfcheck(IroHipContext *ctx, unsigned long long *out);
 int launch_fp32_selfcheck(IroHipContext *ctx, unsigned long long *out);
 
