@@ -17,9 +17,9 @@
 //   attn_softmax  RW rows per wave: the row maximum from the tile maxima,
 //                 p = expf(score - max) written in place, the key-order sum
 //                 of p by one lane per row (through LDS)
-//   attn_pv       64 queries x 64 dims per block: p / sum staged per 64-key
-//                 chunk, 16 key-order chains per thread, the gate applied at
-//                 the store
+//   attn_pv       64 (or, for small grids, 32) queries x 64 dims per block:
+//                 p / sum staged per 64-key chunk, 16 (8) key-order chains
+//                 per thread, the gate applied at the store
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -192,7 +192,8 @@ __global__ __launch_bounds__(64) void attn_softmax_kernel(float *__restrict__ sc
     if (lane < RW && g0 + lane < R) sums[g0 + lane] = sum;
 }
 
-// QT queries x 64 dims per block; thread: QT/16 queries x 4 dims.
+// QT queries x 64 dims per block; thread: QT/16 queries x 4 dims (QT 32,
+// 64 or 128).
 template <int QT>
 __global__ __launch_bounds__(256) void attn_pv_kernel(
     const float *__restrict__ sc, const float *__restrict__ sums, const float *__restrict__ v,
@@ -253,9 +254,13 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
         if (kc + kPVK < J) load(kc + kPVK);
         auto step = [&](int kk) {
             float p[QPT];
-            if constexpr (QPT == 4) {
-                const float4 pv = *reinterpret_cast<const float4 *>(&Ps[kk * PP + tq * 4]);
-                p[0] = pv.x, p[1] = pv.y, p[2] = pv.z, p[3] = pv.w;
+            if constexpr (QPT % 4 == 0) {
+#pragma unroll
+                for (int c = 0; c < QPT; c += 4) {
+                    const float4 pv =
+                        *reinterpret_cast<const float4 *>(&Ps[kk * PP + tq * QPT + c]);
+                    p[c] = pv.x, p[c + 1] = pv.y, p[c + 2] = pv.z, p[c + 3] = pv.w;
+                }
             } else {
                 const float2 pv = *reinterpret_cast<const float2 *>(&Ps[kk * PP + tq * 2]);
                 p[0] = pv.x, p[1] = pv.y;
@@ -382,10 +387,18 @@ int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *a, const 
     hipLaunchKernelGGL((attn_softmax_kernel<RW>), dim3((unsigned)((R + RW - 1) / RW)), dim3(64), 0,
                        ctx->stream, sc, pm, a->nvalid, (int)R, S, H, (int)Jp, sums);
     IRO_HIP_CHECK_LAUNCH(ctx);
-    constexpr int PQT = 32;  // 4.5 waves per SIMD at 3 x 750 queries, 16 heads
-    hipLaunchKernelGGL((attn_pv_kernel<PQT>), dim3((S + PQT - 1) / PQT, B * H), dim3(256), 0,
-                       ctx->stream, sc, sums, v, context_v, a->rows, a->nvalid, gate, S, D, H, C,
-                       (int)Jp, mix);
+    // 64 queries per block (16 chains per thread) where that still gives two
+    // blocks per CU, else 32 (measured at 3 x 750 queries, 20 heads: the call
+    // 0.479 ms at 64, 0.512 at 32, 0.500 at 128).
+    const int cus = ctx->cus > 0 ? ctx->cus : 256;
+    if ((long long)((S + 63) / 64) * B * H >= 2LL * cus)
+        hipLaunchKernelGGL((attn_pv_kernel<64>), dim3((S + 63) / 64, B * H), dim3(256), 0,
+                           ctx->stream, sc, sums, v, context_v, a->rows, a->nvalid, gate, S, D, H,
+                           C, (int)Jp, mix);
+    else
+        hipLaunchKernelGGL((attn_pv_kernel<32>), dim3((S + 31) / 32, B * H), dim3(256), 0,
+                           ctx->stream, sc, sums, v, context_v, a->rows, a->nvalid, gate, S, D, H,
+                           C, (int)Jp, mix);
     IRO_HIP_CHECK_LAUNCH(ctx);
     return 0;
 }
