@@ -80,6 +80,69 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
     }
 }
 
+// Narrow outputs (N <= 32: the output head's 1280 -> 32 projection): a
+// block is 8 rows x 32 outputs, one K-order chain per thread, so the grid
+// has a block per 8 rows instead of one 64 x 128 tile per 64 rows of which
+// three quarters would be padding.  x and w pass through LDS in 64-k
+// chunks, the next chunk's loads in flight while one is summed; only k < K
+// enters a chain, as in the reference loop.
+constexpr int kNR = 8, kNK = 64, kNP = 65;
+
+__global__ __launch_bounds__(256) void linear_f32_narrow_kernel(const float *__restrict__ x,
+                                                                int M, int K,
+                                                                const float *__restrict__ w,
+                                                                int N,
+                                                                const float *__restrict__ bias,
+                                                                float *__restrict__ y) {
+    __shared__ float Xs[kNR * kNP];
+    __shared__ float Ws[32 * kNP];
+    const int tid = threadIdx.x, r = tid >> 5, n = tid & 31;
+    const int m0 = blockIdx.x * kNR;
+    // Staging: x element tid + 256 i (i < 2) and w element tid + 256 i
+    // (i < 8) of a chunk, row e / 64, column e % 64.
+    float xr[2], wr[8];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = tid + 256 * i, rr = e >> 6, c = e & 63;
+            const int m = m0 + rr < M ? m0 + rr : M - 1;
+            xr[i] = k0 + c < K ? x[(size_t)m * K + k0 + c] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = tid + 256 * i, rr = e >> 6, c = e & 63;
+            const int nn = rr < N ? rr : N - 1;
+            wr[i] = k0 + c < K ? w[(size_t)nn * K + k0 + c] : 0.0f;
+        }
+    };
+    float acc = 0.0f;
+    load(0);
+    for (int k0 = 0; k0 < K; k0 += kNK) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = tid + 256 * i;
+            Xs[(e >> 6) * kNP + (e & 63)] = xr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = tid + 256 * i;
+            Ws[(e >> 6) * kNP + (e & 63)] = wr[i];
+        }
+        __syncthreads();
+        if (k0 + kNK < K) load(k0 + kNK);
+        const float *xs = &Xs[r * kNP], *ws = &Ws[n * kNP];
+        if (K - k0 >= kNK) {
+#pragma unroll 16
+            for (int c = 0; c < kNK; ++c) acc = acc + xs[c] * ws[c];
+        } else {
+            for (int c = 0; c < K - k0; ++c) acc = acc + xs[c] * ws[c];
+        }
+        __syncthreads();
+    }
+    const int m = m0 + r;
+    if (m < M && n < N) y[(size_t)m * N + n] = acc + (bias ? bias[n] : 0.0f);
+}
+
 // sampler.c:281-297, the CFG combine and Euler update after the DiT
 // velocity of a step: guided = v + sum_k s_k * (v - v_k) over the active
 // unconditional rows k (text, speaker, caption order), state += guided * dt.
@@ -137,8 +200,14 @@ int iro_hip_linear_f32(IroHipContext *ctx, const float *x, int M, int K, const f
     if (M == 0) return 0;
     if ((long long)M * K > INT64_MAX / 8 || (M + kLM - 1) / kLM > 65535)
         return set_error(ctx, "linear_f32: too many rows");
-    hipLaunchKernelGGL(linear_f32_kernel, dim3((N + kLN - 1) / kLN, (M + kLM - 1) / kLM),
-                       dim3(256), 0, ctx->stream, x, M, K, w, N, bias, y);
+    if (N <= 32 && K >= 128) {
+        if ((M + kNR - 1) / kNR > INT32_MAX / 2) return set_error(ctx, "linear_f32: too many rows");
+        hipLaunchKernelGGL(linear_f32_narrow_kernel, dim3((M + kNR - 1) / kNR), dim3(256), 0,
+                           ctx->stream, x, M, K, w, N, bias, y);
+    } else {
+        hipLaunchKernelGGL(linear_f32_kernel, dim3((N + kLN - 1) / kLN, (M + kLM - 1) / kLM),
+                           dim3(256), 0, ctx->stream, x, M, K, w, N, bias, y);
+    }
     IRO_HIP_CHECK_LAUNCH(ctx);
     return 0;
 }
