@@ -5,6 +5,8 @@
 // index order, so the parameters are bit-identical to it.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <cstdint>
 
 #include "iro_expf.h"
@@ -221,6 +223,93 @@ __global__ __launch_bounds__(64) void ada_low_kernel(const float *__restrict__ a
     low[(((size_t)a * 3 + br) * B + b) * R + r] = acc + 0.0f;
 }
 
+// The same sums with the down rows through LDS, for B <= 4 batch rows and
+// D % 4 == 0 with 16-byte aligned rows: a block takes 64 rows r of one
+// (adaLN a, branch br) for every batch row; its four waves read 64 x 64
+// tiles of those rows (each row's 256 bytes by 16 consecutive lanes) and of
+// the act rows into a three-deep LDS ring, two tiles ahead of the sums (the
+// loads themselves go out six tiles ahead, through registers), and
+// wave b runs the in-order sums of batch row b from LDS.  Each down row is
+// read once per block instead of once per batch row with one strided load
+// per lane and step.
+constexpr int kRingK = 64, kRingP = 65;
+__global__ __launch_bounds__(256) void ada_low_ring_kernel(const float *__restrict__ act,
+                                                           AdaWeights w, int B, int D, int R,
+                                                           float *__restrict__ low) {
+    __shared__ float tile[3][64 * kRingP];
+    __shared__ __attribute__((aligned(16))) float xs[3][4][kRingK];
+    const int br = blockIdx.y, a = blockIdx.z, r0 = blockIdx.x * 64;
+    const float *down = w.w[a * 9 + br * 3];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nc = (D + kRingK - 1) / kRingK;
+    // Loads of chunk c: float4 q = tid + 256 i of the tile (row q / 16,
+    // columns 4 (q % 16) ..), and for tid < 16 B the float4 of act row
+    // tid / 16.  Past D or R: zeros (never summed or stored).
+    float4 rt[4][4], rx[4];
+    auto load = [&](float4 (&t)[4], float4 &x, int c) {
+        const int k0 = c * kRingK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 256 * i, rr = q >> 4, k = k0 + (q & 15) * 4;
+            t[i] = (c < nc && r0 + rr < R && k < D)
+                       ? *reinterpret_cast<const float4 *>(down + (size_t)(r0 + rr) * D + k)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        const int k = k0 + (tid & 15) * 4;
+        x = (c < nc && tid < 16 * B && k < D)
+                ? *reinterpret_cast<const float4 *>(act + ((size_t)br * B + (tid >> 4)) * D + k)
+                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    auto store = [&](const float4 (&t)[4], const float4 &x, int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 256 * i;
+            float *dst = &tile[slot][(q >> 4) * kRingP + (q & 15) * 4];
+            dst[0] = t[i].x;
+            dst[1] = t[i].y;
+            dst[2] = t[i].z;
+            dst[3] = t[i].w;
+        }
+        if (tid < 64) *reinterpret_cast<float4 *>(&xs[slot][tid >> 4][(tid & 15) * 4]) = x;
+    };
+    float acc = 0.0f;
+    // Iteration c stores chunk c + 2 (loaded four iterations before) into
+    // the slot chunk c - 1 left, loads chunk c + 6, and sums chunk c.
+    auto iter = [&](int c, auto par) {
+        constexpr int P = decltype(par)::value;  // c % 4
+        __syncthreads();
+        store(rt[P], rx[P], (c + 2) % 3);
+        load(rt[P], rx[P], c + 6);
+        if (wave < B) {
+            const float *tr = &tile[c % 3][lane * kRingP];
+            const float *xr = xs[c % 3][wave];
+            const int n = D - c * kRingK < kRingK ? D - c * kRingK : kRingK;
+            if (n == kRingK) {
+#pragma unroll 16
+                for (int k = 0; k < kRingK; ++k) acc = acc + xr[k] * tr[k];
+            } else {
+                for (int k = 0; k < n; ++k) acc = acc + xr[k] * tr[k];
+            }
+        }
+    };
+    load(rt[0], rx[0], 0);
+    load(rt[1], rx[1], 1);
+    store(rt[0], rx[0], 0);
+    store(rt[1], rx[1], 1);
+    load(rt[0], rx[0], 2);
+    load(rt[1], rx[1], 3);
+    load(rt[2], rx[2], 4);
+    load(rt[3], rx[3], 5);
+    for (int c = 0; c < nc; c += 4) {
+        iter(c, std::integral_constant<int, 0>{});
+        if (c + 1 < nc) iter(c + 1, std::integral_constant<int, 1>{});
+        if (c + 2 < nc) iter(c + 2, std::integral_constant<int, 2>{});
+        if (c + 3 < nc) iter(c + 3, std::integral_constant<int, 3>{});
+    }
+    const int r = r0 + lane;
+    if (wave < B && r < R) low[(((size_t)a * 3 + br) * B + wave) * R + r] = acc + 0.0f;
+}
+
 // out [A][3][B][D]: (sum_r low * up in index order) + bias, + the cond slice;
 // the gate branch through tanhf.  The block's low row is staged in LDS.
 __global__ __launch_bounds__(64) void ada_out_kernel(const float *__restrict__ low,
@@ -267,8 +356,15 @@ int iro_hip_dit_adaln_params(IroHipContext *ctx, const float *cond, int B, int D
     hipLaunchKernelGGL(ada_act_kernel, dim3((3 * B * D + 255) / 256), dim3(256), 0, ctx->stream,
                        cond, B, D, act);
     IRO_HIP_CHECK_LAUNCH(ctx);
-    hipLaunchKernelGGL(ada_low_kernel, dim3((R + 63) / 64, 3 * B, n_adaln), dim3(64), 0,
-                       ctx->stream, act, w, B, D, R, low);
+    bool ring = B <= 4 && D % 4 == 0;
+    for (int i = 0; i < n_adaln * 3; ++i)
+        ring = ring && (((uintptr_t)w.w[(i / 3) * 9 + (i % 3) * 3]) & 15) == 0;
+    if (ring)
+        hipLaunchKernelGGL(ada_low_ring_kernel, dim3((R + 63) / 64, 3, n_adaln), dim3(256), 0,
+                           ctx->stream, act, w, B, D, R, low);
+    else
+        hipLaunchKernelGGL(ada_low_kernel, dim3((R + 63) / 64, 3 * B, n_adaln), dim3(64), 0,
+                           ctx->stream, act, w, B, D, R, low);
     IRO_HIP_CHECK_LAUNCH(ctx);
     hipLaunchKernelGGL(ada_out_kernel, dim3((D + 63) / 64, 3 * B, n_adaln), dim3(64), 0,
                        ctx->stream, low, cond, w, B, D, R, out);

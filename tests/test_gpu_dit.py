@@ -280,6 +280,26 @@ def _attn_case(seed, B, S, C, D, shared, keep):
     return q, k, v, gate, ck, cv, mask
 
 
+@pytest.mark.parametrize("B,D,R", [(1, 1280, 192), (4, 96, 40), (2, 200, 70), (3, 102, 30)])
+def test_adaln_params_shapes(ctx, oracle, B, D, R):
+    """dit.c:543-588 on the device against the oracle for both adaLNs of a
+    block: one batch row (a plain step), four rows, widths and ranks that
+    leave partial 64-wide tiles, and a width that is not a multiple of 4
+    (the per-row-chain kernel instead of the LDS ring)."""
+    cond = gauss(770, (B, 3 * D), 0.8)
+    w = []
+    for i in range(6):
+        w += [gauss(771 + 3 * i, (R, D), 0.05), gauss(772 + 3 * i, (D, R), 0.05),
+              gauss(773 + 3 * i, (D,), 0.1)]
+    out = ctx.empty((2, 3, B, D), np.float32)
+    ctx.dit_adaln_params(ctx.to_device(cond), B, D, R, [ctx.to_device(a) for a in w], out)
+    got = out.numpy()
+    for a in range(2):
+        ws = w[9 * a:9 * a + 9]
+        want = oracle.adaln_params(cond, ws[0::3], ws[1::3], ws[2::3])
+        assert_bits_equal(got[a], want, f"adaLN {a}")
+
+
 @pytest.mark.parametrize("B,S,C,D,shared,keep", [
     (2, 24, 9, 1280, 0, 4),       # reference-sized heads, per-batch context
     (3, 150, 40, 1024, 1, 40),    # shared context, ragged key tiles
