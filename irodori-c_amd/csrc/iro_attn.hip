@@ -387,11 +387,12 @@ int iro_hip_dit_attention(IroHipContext *ctx, const IroHipAttnContext *a, const 
     hipLaunchKernelGGL((attn_softmax_kernel<RW>), dim3((unsigned)((R + RW - 1) / RW)), dim3(64), 0,
                        ctx->stream, sc, pm, a->nvalid, (int)R, S, H, (int)Jp, sums);
     IRO_HIP_CHECK_LAUNCH(ctx);
-    // 64 queries per block (16 chains per thread) where that still gives two
-    // blocks per CU, else 32 (measured at 3 x 750 queries, 20 heads: the call
-    // 0.479 ms at 64, 0.512 at 32, 0.500 at 128).
+    // 64 queries per block (16 chains per thread) where that gives at least
+    // 2.5 blocks per CU, else 32 (measured on one box at 3 x 750 queries:
+    // 20 heads, 2.8 blocks per CU at 64: the call 0.469 ms at 64, 0.516 at 32,
+    // 0.500 at 128; 16 heads, 2.25 per CU: 0.407 at 64, 0.397 at 32).
     const int cus = ctx->cus > 0 ? ctx->cus : 256;
-    if ((long long)((S + 63) / 64) * B * H >= 2LL * cus)
+    if ((long long)((S + 63) / 64) * B * H * 2 >= 5LL * cus)
         hipLaunchKernelGGL((attn_pv_kernel<64>), dim3((S + 63) / 64, B * H), dim3(256), 0,
                            ctx->stream, sc, sums, v, context_v, a->rows, a->nvalid, gate, S, D, H,
                            C, (int)Jp, mix);
