@@ -58,25 +58,52 @@ __device__ __forceinline__ float sincos_poly(double x, double x2, const SinCosTa
     return (float)__builtin_fma(x6, c2, c);
 }
 
-// cosine = 0: sinf(y); 1: cosf(y).
+// sincos_poly of the first table, with the second table's cosine taken as
+// the first's negated (its cosine coefficients are exactly the first's
+// negated, and negation commutes with every rounding, so `neg` negates the
+// cosine result), without per-lane table loads; both polynomials are
+// formed and the lane's one (sin for even k) selected.
+__device__ __forceinline__ float sincos_poly_sel(double x, double x2, int k, bool neg) {
+    constexpr double c0 = 0x1p0, c1 = -0x1.ffffffd0c621cp-2, c2 = 0x1.55553e1068f19p-5,
+                     c3 = -0x1.6c087e89a359dp-10, c4 = 0x1.99343027bf8c3p-16;
+    constexpr double s1 = -0x1.555545995a603p-3, s2 = 0x1.1107605230bc4p-7,
+                     s3 = -0x1.994eb3774cf24p-13;
+    const double x3 = x * x2;
+    const double sp = __builtin_fma(x2, s3, s2);
+    const double x7 = x3 * x2;
+    const double sq = __builtin_fma(x3, s1, x);
+    const float rs = (float)__builtin_fma(x7, sp, sq);
+    const double x4 = x2 * x2;
+    const double cp = __builtin_fma(x2, c4, c3);
+    const double cq = __builtin_fma(x2, c1, c0);
+    const double x6 = x4 * x2;
+    const double cr = __builtin_fma(x4, c2, cq);
+    float rc = (float)__builtin_fma(x6, cp, cr);
+    rc = neg ? -rc : rc;
+    return (k & 1) ? rc : rs;
+}
+
+// cosine = 0: sinf(y); 1: cosf(y).  |y| < 120 (and NaN-free) takes one
+// branch-free path for every lane: below pi/4 the reduction below gives
+// n = 0 and leaves x = y exactly, which is glibc's |y| < pi/4 case, and
+// below 2^-12 glibc's own result (y, or 1) is selected.
 __device__ __forceinline__ float sincosf_glibc(float y, int cosine) {
     const uint32_t yi = __float_as_uint(y);
     const uint32_t top = (yi >> 20) & 0x7ff;
     double x = y;
-    if (top < 0x3f4) {  // |y| < pi/4 (top 12 bits of the float pi/4)
-        if (top < 0x398) return cosine ? 1.0f : y;  // |y| < 2^-12
-        return sincos_poly(x, x * x, kSinCosTab[0], cosine);
+    if (__builtin_expect(top < 0x42f, 1)) {  // |y| < 120
+        const double r = x * 0x1.45F306DC9C883p+23;
+        const int n = ((int32_t)r + 0x800000) >> 24;
+        x = __builtin_fma(-(double)n, 0x1.921FB54442D18p0, x);
+        // sign of quadrant n & 3: +1, -1, -1, +1 (an exact sign flip)
+        const double xs = ((n + 1) & 2) ? -x : x;
+        const float v = sincos_poly_sel(xs, x * x, n ^ cosine, (n & 2) != 0);
+        return top < 0x398 ? (cosine ? 1.0f : y) : v;  // |y| < 2^-12
     }
     int n;
     int t;  // table: negated cosine coefficients for quadrants 2, 3
     double sgn;
-    if (top < 0x42f) {  // |y| < 120
-        const double r = x * kSinCosTab[0].hpi_inv;
-        n = ((int32_t)r + 0x800000) >> 24;
-        x = __builtin_fma(-(double)n, kSinCosTab[0].hpi, x);
-        sgn = kSinCosTab[0].sign[n & 3];
-        t = (n & 2) ? 1 : 0;
-    } else if (top < 0x7f8) {  // finite
+    if (top < 0x7f8) {  // finite
         const uint32_t *arr = &kInvPio4[(yi >> 26) & 15];
         const int shift = (yi >> 23) & 7;
         uint32_t xi = ((yi & 0xffffff) | 0x800000) << shift;
