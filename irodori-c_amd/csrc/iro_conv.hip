@@ -163,16 +163,21 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(
 // share are read through one L2.
 constexpr int kIm2colRows = 4;  // output steps (wavefronts) per workgroup
 
-template <int CONV, bool RES, int CHN>
+// CHN == 0 (C <= 128): each 32-lane half of a wavefront takes its own
+// output step, so narrow rows fill the lanes.
+template <int CONV, bool RES, int CHN0>
 __global__ __launch_bounds__(64 * kIm2colRows) void conv_im2col7_kernel(
     const float *__restrict__ x, int T, int C, int T_out, int stride, int dilation, int padding,
     uint8_t *__restrict__ cols1, uint8_t *__restrict__ cols2, int ldc, float *__restrict__ s1,
     int32_t *__restrict__ z1, float *__restrict__ s2, int32_t *__restrict__ z2, uint32_t flip,
     int per) {
     constexpr int KT = 7;
+    constexpr bool HALF = CHN0 == 0;
+    constexpr int CHN = HALF ? 1 : CHN0;
     const int blk = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    const int r = blk * kIm2colRows + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
+    const int r = HALF ? (blk * kIm2colRows + (threadIdx.x >> 6)) * 2 + ((threadIdx.x >> 5) & 1)
+                       : blk * kIm2colRows + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & (HALF ? 31 : 63);
     if (r >= T_out) return;
     float4 v[KT][CHN];
     bool inside[KT];
@@ -197,8 +202,8 @@ __global__ __launch_bounds__(64 * kIm2colRows) void conv_im2col7_kernel(
             lo = sel_min(lo, e.x); lo = sel_min(lo, e.y); lo = sel_min(lo, e.z); lo = sel_min(lo, e.w);
             hi = sel_max(hi, e.x); hi = sel_max(hi, e.y); hi = sel_max(hi, e.z); hi = sel_max(hi, e.w);
         }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
+    lo = HALF ? half_range<false>(lo) : wave_min(lo);
+    hi = HALF ? half_range<true>(hi) : wave_max(hi);
     const RowQ q = row_params<CONV>(lo, hi);
     float sc2 = 0.0f, inv2 = 0.0f;
     if (RES) {
@@ -333,16 +338,18 @@ int launch_conv_im2col7(IroHipContext *ctx, const float *x, int T, int C, int T_
                         int dilation, int padding, uint8_t *cols1, uint8_t *cols2, int ldc,
                         float *s1, int32_t *z1, float *s2, int32_t *z2, bool signed_codes) {
     const uint32_t flip = signed_codes ? 0x80808080u : 0u;
-    const int per = ((T_out + kIm2colRows - 1) / kIm2colRows + 7) / 8;  // row blocks per XCD
+    const int chn = C <= 128 ? 0 : (C + 255) / 256;
+    const int rows_per_block = kIm2colRows * (chn == 0 ? 2 : 1);
+    const int per = ((T_out + rows_per_block - 1) / rows_per_block + 7) / 8;  // row blocks per XCD
     const dim3 grid(8 * per), block(64 * kIm2colRows);
     const bool res = cols2 != nullptr;
-    const int chn = (C + 255) / 256;
     prof_begin(ctx);
 #define IRO_IM2COL7(CV, RS, CH)                                                                 \
     hipLaunchKernelGGL((conv_im2col7_kernel<CV, RS, CH>), grid, block, 0, ctx->stream, x, T, C, \
                        T_out, stride, dilation, padding, cols1, cols2, ldc, s1, z1, s2, z2, flip, per)
 #define IRO_IM2COL7_C(CV, RS)          \
     switch (chn) {                     \
+        case 0: IRO_IM2COL7(CV, RS, 0); break; \
         case 1: IRO_IM2COL7(CV, RS, 1); break; \
         case 2: IRO_IM2COL7(CV, RS, 2); break; \
         case 3: IRO_IM2COL7(CV, RS, 3); break; \

@@ -136,6 +136,17 @@ __device__ __forceinline__ float wave_range(float v) {
     return op(__builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 0)),
               __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, 32)));
 }
+// The same over each 32-lane half of the wave (the result in every lane of
+// the half; no lane of the other half is read).
+template <bool MAX>
+__device__ __forceinline__ float half_range(float v) {
+    auto op = [](float a, float b) { return MAX ? __builtin_fmaxf(a, b) : __builtin_fminf(a, b); };
+    v = op(v, dpp_mov<0xB1>(v));
+    v = op(v, dpp_mov<0x4E>(v));
+    v = op(v, dpp_mov<0x141>(v));
+    v = op(v, dpp_mov<0x140>(v));
+    return op(v, swz_xor16(v));
+}
 __device__ __forceinline__ float wave_min(float v) { return wave_range<false>(v); }
 __device__ __forceinline__ float wave_max(float v) { return wave_range<true>(v); }
 __device__ __forceinline__ int wave_sum(int v) {
