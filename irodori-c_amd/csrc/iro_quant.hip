@@ -35,6 +35,25 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const float *__restrict__ 
     quant_row<CONV, CH, RES, EXACT>(v, row, K, lane, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
 }
 
+// Narrow rows (K <= 128, the vector path's conditions otherwise): each
+// 32-lane half of a wavefront holds one row, eight rows per block.
+template <int CONV, bool RES>
+__global__ __launch_bounds__(256) void quant_rows_half(const float *__restrict__ x, int M, int K,
+                                                       int ldx, uint8_t *__restrict__ q1, int ldq,
+                                                       float *__restrict__ s1,
+                                                       int32_t *__restrict__ z1,
+                                                       float *__restrict__ res,
+                                                       uint8_t *__restrict__ q2,
+                                                       float *__restrict__ s2,
+                                                       int32_t *__restrict__ z2, uint32_t sflip) {
+    const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int lane = threadIdx.x & 31;
+    if (row >= M) return;
+    float4 v[1];
+    load_row<1, false>(x + (size_t)row * ldx, K, lane, v);
+    quant_row<CONV, 1, RES, false, true>(v, row, K, lane, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
+}
+
 // Generic path: any K and alignment; the row is re-read from cache.
 template <int CONV, bool RES>
 __global__ __launch_bounds__(256) void quant_rows_any(const float *__restrict__ x, int M, int K,
@@ -220,7 +239,10 @@ int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ld
                        ldq, s1, z1, res, q2, s2, z2, sflip)
     // The DiT row widths (1024, 2816) fill whole 256-column chunks: no
     // per-chunk bounds.
-    if (vec && K == 1024) IRO_QR(4, true);
+    if (vec && K <= 128)
+        hipLaunchKernelGGL((quant_rows_half<CONV, RES>), dim3((M + 7) / 8), block, 0, st, x, M, K,
+                           ldx, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
+    else if (vec && K == 1024) IRO_QR(4, true);
     else if (vec && K == 2816) IRO_QR(11, true);
     else if (vec && ch <= 1) IRO_QR(1, false);
     else if (vec && ch <= 2) IRO_QR(2, false);

@@ -49,7 +49,9 @@ __device__ __forceinline__ void load_row(const float *__restrict__ xr, int K, in
 // ops.c:321-348 (and, with RES, ops.c:427-442) on one row already in
 // registers: range, codes (xor sflip), row scale and zero point; the
 // two-term variant forms the remainder in place and quantizes it again.
-template <int CONV, int CH, bool RES, bool EXACT>
+// HALF: the row is held by one 32-lane half of the wavefront (K <= 128,
+// lane counted within the half) and the reductions stay inside the half.
+template <int CONV, int CH, bool RES, bool EXACT, bool HALF = false>
 __device__ __forceinline__ void quant_row(float4 (&v)[CH], int row, int K, int lane,
                                           uint8_t *__restrict__ q1, int ldq,
                                           float *__restrict__ s1, int32_t *__restrict__ z1,
@@ -64,8 +66,8 @@ __device__ __forceinline__ void quant_row(float4 (&v)[CH], int row, int K, int l
         hi = sel_max(hi, v[c].x); hi = sel_max(hi, v[c].y);
         hi = sel_max(hi, v[c].z); hi = sel_max(hi, v[c].w);
     }
-    lo = wave_min(lo);
-    hi = wave_max(hi);
+    lo = HALF ? half_range<false>(lo) : wave_min(lo);
+    hi = HALF ? half_range<true>(hi) : wave_max(hi);
     const RowQ r = row_params<CONV>(lo, hi);
     float lo2 = 0.0f, hi2 = 0.0f;
 #pragma unroll
@@ -93,8 +95,8 @@ __device__ __forceinline__ void quant_row(float4 (&v)[CH], int row, int K, int l
         z1[row] = r.zp;
     }
     if (RES) {
-        lo2 = wave_min(lo2);
-        hi2 = wave_max(hi2);
+        lo2 = HALF ? half_range<false>(lo2) : wave_min(lo2);
+        hi2 = HALF ? half_range<true>(hi2) : wave_max(hi2);
         const RowQ r2 = row_params<CONV>(lo2, hi2);
         float *rr = res ? res + (size_t)row * K : nullptr;
 #pragma unroll
