@@ -518,8 +518,9 @@ int iro_hip_convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_i
    output = skip + conv1(hidden) + bias, with hidden [T, C_in] quantized per
    row (two-term when residual: the IRO_CODEC_GROUP_CONV1 policy bit and
    stage mask of dacvae.c:27-73), w the [C_out, C_in] 1x1 weight, skip and
-   output [T, C_out] (output may be skip: it is then updated in place).  The
-   snake activations around it are fp32 neighbours, not part of this call. */
+   output [T, C_out] (output may be skip: it is then updated in place;
+   otherwise the two must not overlap).  The snake activations around it
+   are fp32 neighbours, not part of this call. */
 int iro_hip_conv1x1_skip_int8(IroHipContext *ctx, const float *hidden, const float *skip, int T,
                               const IroHipWeight *w, const float *bias, int residual,
                               float *output);

@@ -822,36 +822,6 @@ int iro_hip_convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_i
                                output);
 }
 
-// dacvae.c:974-1012 (the int8 1x1 projection of run_residual_int8): the skip
-// connection first (output = skip), then output += lin(q1) + bias and, with
-// `residual` (the IRO_CODEC_GROUP_CONV1 policy bit for this stage),
-// output += lin(q2), the rows of `hidden` quantized once per row.  Both
-// planes run in one GEMM pass with the reference's rounding order.
-int iro_hip_conv1x1_skip_int8(IroHipContext *ctx, const float *hidden, const float *skip, int T,
-                              const IroHipWeight *w, const float *bias, int residual,
-                              float *output) {
-    if (!ctx || !hidden || !skip || !w || !output || T <= 0)
-        return set_error(ctx, "conv1x1_skip_int8: invalid arguments");
-    const int C_in = w->K, C_out = w->N;
-    if (output != skip &&
-        iro_hip_copy(ctx, output, skip, sizeof(float) * (size_t)T * C_out))
-        return -1;
-    Workspace ws{ctx};
-    size_t off[6];
-    act_reserve(ws, T, C_in, residual != 0, off);
-    if (ws.commit()) return -1;
-    const ActBufs b = act_at(ws, C_in, residual != 0, off);
-    if (launch_quant_rows(ctx, hidden, T, C_in, C_in, b.q1, b.ld, b.s1, b.z1, nullptr, b.q2, b.s2,
-                          b.z2, true))
-        return -1;
-    GemmArgs a = gemm_args(b, T, C_in);
-    a.bias = bias;
-    a.y = output;
-    a.ldy = C_out;
-    a.accumulate = 1;
-    return launch_gemm(ctx, w, a, EPI_LINEAR);
-}
-
 // ---- backend queries -------------------------------------------------------------------
 
 // Test hook: while set, the known answer's first activation code is altered

@@ -17,12 +17,10 @@
 #include <algorithm>
 
 #include "iro_internal.h"
-#include "iro_sincosf.h"
+#include "iro_snake.h"
 
 namespace iro {
 namespace {
-
-constexpr int kSnakeMaxChannels = 1536;  // dacvae.c:808 SNAKE_MAX_CHANNELS
 
 // One thread per four consecutive elements of a row (C % 4 == 0, rows
 // 16-byte aligned).  BIAS: v = x + bias (snake_bias_forward).  INV: the
@@ -40,30 +38,25 @@ __global__ __launch_bounds__(256) void snake_kernel(const float *__restrict__ x,
         for (int c = threadIdx.x; c < C; c += 256) {
             const float a = alpha[c];
             s_alpha[c] = a;
-            s_inv[c] = 1.0f / (a + 1e-9f);
+            s_inv[c] = snake_inv(a);
         }
         __syncthreads();
     }
     for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n4; i += (long long)gridDim.x * 256) {
         const long long e = 4 * i;
         const int c = (int)(e % C);
-        const float4 v = *reinterpret_cast<const float4 *>(x + e);
-        float o[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float xv = o[k];
-            if (BIAS) xv = xv + bias[c + k];
-            const float a = INV ? s_alpha[c + k] : alpha[c + k];
-            const float s = sinf_glibc(a * xv);
-            const float ss = s * s;
-            if (INV) {
-                const float inv = s_inv[c + k];
-                o[k] = FMA ? __builtin_fmaf(ss, inv, xv) : xv + ss * inv;
-            } else {
-                o[k] = xv + ss / (a + 1e-9f);
-            }
+        float4 v = *reinterpret_cast<const float4 *>(x + e);
+        if (BIAS) {
+            v.x = v.x + bias[c];
+            v.y = v.y + bias[c + 1];
+            v.z = v.z + bias[c + 2];
+            v.w = v.w + bias[c + 3];
         }
-        *reinterpret_cast<float4 *>(y + e) = make_float4(o[0], o[1], o[2], o[3]);
+        const float *ap = INV ? s_alpha : alpha;
+        const float4 a = make_float4(ap[c], ap[c + 1], ap[c + 2], ap[c + 3]);
+        const float4 inv = INV ? make_float4(s_inv[c], s_inv[c + 1], s_inv[c + 2], s_inv[c + 3])
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4 *>(y + e) = snake_value4<INV, FMA>(v, a, inv);
     }
 }
 
@@ -137,6 +130,42 @@ bool snake_args_ok(const float *x, int T, int C, const float *alpha, const float
            ((((uintptr_t)x) | ((uintptr_t)y)) & 15) == 0;
 }
 
+// dacvae.c:974-1012 (the int8 1x1 projection of run_residual_int8): the skip
+// connection first (output = skip), then output += lin(q1) + bias and, with
+// `residual` (the IRO_CODEC_GROUP_CONV1 policy bit for this stage),
+// output += lin(q2), the rows of `hidden` quantized once per row.  Both
+// planes run in one GEMM pass with the reference's rounding order; the
+// epilogue reads the skip rows where the reference reads its copy of them,
+// so no copy is made (output and skip are the same buffer or disjoint).
+// With `snake` the rows are snaked (bias + alpha, reciprocal form) as they
+// are quantized; returns 1, launching nothing, when that path declines.
+int conv1x1_skip(IroHipContext *ctx, const float *hidden, const float *skip, int T,
+                 const IroHipWeight *w, const float *bias, int residual, float *output,
+                 const SnakePre *snake) {
+    if (!ctx || !hidden || !skip || !w || !output || T <= 0)
+        return set_error(ctx, "conv1x1_skip_int8: invalid arguments");
+    const int C_in = w->K, C_out = w->N;
+    const size_t rows_bytes = sizeof(float) * (size_t)T * C_out;
+    const uintptr_t o = (uintptr_t)output, s = (uintptr_t)skip;
+    if (o != s && o < s + rows_bytes && s < o + rows_bytes)
+        return set_error(ctx, "conv1x1_skip_int8: output partly overlaps skip");
+    Workspace ws{ctx};
+    size_t off[6];
+    act_reserve(ws, T, C_in, residual != 0, off);
+    if (ws.commit()) return -1;
+    const ActBufs b = act_at(ws, C_in, residual != 0, off);
+    const int rc = launch_quant_rows(ctx, hidden, T, C_in, C_in, b.q1, b.ld, b.s1, b.z1, nullptr,
+                                     b.q2, b.s2, b.z2, true, snake);
+    if (rc) return rc;
+    GemmArgs a = gemm_args(b, T, C_in);
+    a.bias = bias;
+    a.y = output;
+    a.yin = skip;
+    a.ldy = C_out;
+    a.accumulate = 1;
+    return launch_gemm(ctx, w, a, EPI_LINEAR);
+}
+
 // The groups of the codec's int8 policy (dacvae.c:38-43).
 enum { GROUP_INITIAL = 1, GROUP_UPSAMPLE = 2, GROUP_CONV7 = 4, GROUP_CONV1 = 8 };
 
@@ -155,10 +184,17 @@ int residual_unit(IroHipContext *ctx, const float *input, int T, int C, const Ir
                             hidden, &t_out))
         return -1;
     if (t_out != T) return set_error(ctx, "dacvae residual: Conv7 changed the length");
-    // dacvae.c:967-968: snake with conv0's bias and alpha1, in place.
+    // dacvae.c:967-968: snake with conv0's bias and alpha1, in place, then
+    // dacvae.c:983-1012: output = input, then += conv1(hidden) + bias.  The
+    // in-place snake is the 1x1 quantizer's pre-op where it takes the shape
+    // (its reciprocal form, C <= 1536), else its own pass.
+    if (conv0_bias && alpha1 && C <= kSnakeMaxChannels) {
+        const SnakePre sp{conv0_bias, alpha1};
+        const int rc = conv1x1_skip(ctx, hidden, input, T, conv1, conv1_bias, two1, output, &sp);
+        if (rc <= 0) return rc;
+    }
     if (iro_hip_snake_bias(ctx, hidden, T, C, conv0_bias, alpha1, hidden)) return -1;
-    // dacvae.c:983-1012: output = input, then += conv1(hidden) + bias.
-    return iro_hip_conv1x1_skip_int8(ctx, hidden, input, T, conv1, conv1_bias, two1, output);
+    return conv1x1_skip(ctx, hidden, input, T, conv1, conv1_bias, two1, output, nullptr);
 }
 
 bool weight_is(const IroHipWeight *w, int N, int K) {
@@ -193,6 +229,12 @@ int iro_hip_snake(IroHipContext *ctx, const float *x, int T, int C, const float 
     // iro_snake_forward (dacvae.c:830-857): the reciprocal form up to 1536
     // channels, in place or not.
     return launch_snake(ctx, x, T, C, nullptr, alpha, y, C <= kSnakeMaxChannels);
+}
+
+int iro_hip_conv1x1_skip_int8(IroHipContext *ctx, const float *hidden, const float *skip, int T,
+                              const IroHipWeight *w, const float *bias, int residual,
+                              float *output) {
+    return conv1x1_skip(ctx, hidden, skip, T, w, bias, residual, output, nullptr);
 }
 
 int iro_hip_snake_bias(IroHipContext *ctx, const float *x, int T, int C, const float *bias,

@@ -1100,6 +1100,7 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     kp.rowsum = w->rowsum;
     kp.bias = a.bias;
     kp.y = a.y;
+    kp.yin = a.yin;
     kp.ldy = a.ldy;
     kp.work = a.work;
     kp.ldw = a.ldw;

@@ -29,6 +29,7 @@ struct KParams {
     const int32_t *rowsum;
     const float *bias;
     float *y;
+    const float *yin;  // accumulate: the prior output rows, nullptr = y itself
     int ldy;
     int32_t *work;
     int ldw;
@@ -331,9 +332,10 @@ __device__ __forceinline__ void epilogue_body(const KParams &p, const v16i (&acc
             const bool col_ok = FULL || pc[j] < p.N;
             float old[16], gv[16];
             if (EPI == EPI_LINEAR && p.accumulate) {
+                const float *yo = p.yin ? p.yin : p.y;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    old[r] = col_ok ? p.y[(long long)row_ld(r) * p.ldy + off[j]] : 0.0f;
+                    old[r] = col_ok ? yo[(long long)row_ld(r) * p.ldy + off[j]] : 0.0f;
             }
             if (EPI == EPI_GATED) {
 #pragma unroll

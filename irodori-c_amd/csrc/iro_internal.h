@@ -174,9 +174,18 @@ struct Workspace {
 
 // ---- kernel launchers (iro_quant.hip, iro_gemm.hip, iro_conv.hip) -------
 
+// Snake applied to each element before it is quantized: x + bias[c], then
+// the reciprocal-form snake with alpha[c] (the in-place snake_bias of a
+// residual unit, at most 1536 channels).
+struct SnakePre {
+    const float *bias;
+    const float *alpha;
+};
+// With `snake`, returns 1 (nothing launched) for shapes the fused path does
+// not take; the caller then runs the snake as its own pass.
 int launch_quant_rows(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
                       int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
-                      int32_t *z2, bool signed_codes = false);
+                      int32_t *z2, bool signed_codes = false, const SnakePre *snake = nullptr);
 int launch_weight_quant(IroHipContext *ctx, const float *w, int N, int K, long long stride_n,
                         long long stride_k, int8_t *q, float *scale, int32_t *colsum);
 int launch_pack(IroHipContext *ctx, const int8_t *q, const float *scale, const int32_t *colsum,
@@ -209,6 +218,9 @@ struct GemmArgs {
     int K = 0;  // k extent read from A (multiple of 16, <= w->Kp)
     const float *bias = nullptr;
     float *y = nullptr;  // EPI_LINEAR output [M, ldy]
+    // accumulate: y = yin + ... with yin [M, ldy] the prior rows (the same
+    // buffer as y, or one that does not overlap it); nullptr = y itself.
+    const float *yin = nullptr;
     int ldy = 0;
     int32_t *work = nullptr;  // raw plane-1 sums [M, ldw], nullable
     int ldw = 0;

@@ -11,6 +11,7 @@
 // quantizes it again, so the input is read from HBM exactly once.
 // Roofline: HBM, 4K + K (+K) + 8 bytes per row.
 #include "iro_quant_row.h"
+#include "iro_snake.h"
 
 namespace iro {
 
@@ -52,6 +53,81 @@ __global__ __launch_bounds__(256) void quant_rows_half(const float *__restrict__
     float4 v[1];
     load_row<1, false>(x + (size_t)row * ldx, K, lane, v);
     quant_row<CONV, 1, RES, false, true>(v, row, K, lane, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
+}
+
+// The residual unit's in-place snake of conv0's biased output
+// (snake_bias_forward, dacvae.c:910-931, called at dacvae.c:967-968) fused
+// into the quantization of the 1x1 projection's input rows, the snaked rows'
+// only reader (dacvae.c:983-1012): they never reach HBM.  Reciprocal form
+// only (K <= 1536).  A block takes R rows.  Phase 1 reads them as flat
+// float4 chunks, so every lane works whatever K is (the decoder's 3 * 2^k
+// channels would leave a quarter of a row-per-wave layout idle), snakes them
+// with per-channel bias, alpha and reciprocal staged in LDS, and writes the
+// tile [R, K] to LDS.  Phase 2 quantizes the tile's rows as quant_rows_vec
+// (HALF: quant_rows_half) does.  Dynamic LDS: 3 K + R K floats.
+template <int CONV, int CH, bool RES, bool HALF>
+__global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict__ x, int M, int K,
+                                                        int ldx, int R, unsigned k4_magic,
+                                                        const float *__restrict__ bias,
+                                                        const float *__restrict__ alpha,
+                                                        uint8_t *__restrict__ q1, int ldq,
+                                                        float *__restrict__ s1,
+                                                        int32_t *__restrict__ z1,
+                                                        uint8_t *__restrict__ q2,
+                                                        float *__restrict__ s2,
+                                                        int32_t *__restrict__ z2, uint32_t sflip) {
+    static_assert(!HALF || CH == 1, "a half-wave row holds at most 128 columns");
+    extern __shared__ __attribute__((aligned(16))) float snake_lds[];
+    float *s_b = snake_lds, *s_a = s_b + K, *s_i = s_a + K, *tile = s_i + K;
+    for (int c = threadIdx.x; c < K; c += 256) {
+        const float a = alpha[c];
+        s_b[c] = bias[c];
+        s_a[c] = a;
+        s_i[c] = snake_inv(a);
+    }
+    const int row0 = blockIdx.x * R;
+    const int rows = min(R, M - row0);
+    const int k4 = K >> 2, chunks = rows * k4;
+    // Phase 1: at most 4 chunks per thread (R K <= 4096); loads first.
+    float4 v4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = threadIdx.x + 256 * j;
+        if (f < chunks) {
+            const int r = __umulhi(2u * f, k4_magic), c4 = f - r * k4;
+            v4[j] = *reinterpret_cast<const float4 *>(x + (size_t)(row0 + r) * ldx + 4 * c4);
+        }
+    }
+    __syncthreads();  // the staged parameters
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = threadIdx.x + 256 * j;
+        if (f < chunks) {
+            const int r = __umulhi(2u * f, k4_magic), c4 = f - r * k4;
+            const float4 b = *reinterpret_cast<const float4 *>(s_b + 4 * c4);
+            const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
+            const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
+            const float4 xv = make_float4(v4[j].x + b.x, v4[j].y + b.y, v4[j].z + b.z,
+                                          v4[j].w + b.w);
+            *reinterpret_cast<float4 *>(tile + r * K + 4 * c4) =
+                snake_value4<true, CONV == 1>(xv, a, i);
+        }
+    }
+    __syncthreads();
+    // Phase 2: rows of the tile, one per wave (HALF: per 32-lane half).
+    constexpr int WL = HALF ? 32 : 64, RPB = 256 / WL;
+    const int lane = threadIdx.x & (WL - 1);
+    for (int r = threadIdx.x / WL; r < rows; r += RPB) {
+        float4 v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int col = (c * 64 + lane) * 4;
+            v[c] = col < K ? *reinterpret_cast<const float4 *>(tile + r * K + col)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        quant_row<CONV, CH, RES, false, HALF>(v, row0 + r, K, lane, q1, ldq, s1, z1, nullptr, q2,
+                                              s2, z2, sflip);
+    }
 }
 
 // Generic path: any K and alignment; the row is re-read from cache.
@@ -223,6 +299,47 @@ __global__ __launch_bounds__(256) void fill_kernel(uint8_t *__restrict__ dst, ui
     }
 }
 
+// The shapes quant_rows_snake takes: the vector path's, at most 1536 columns.
+bool quant_snake_ok(const float *x, int K, int ldx, const uint8_t *q1, int ldq,
+                    const uint8_t *q2, const SnakePre &sp) {
+    return (K % 4 == 0) && (ldx % 4 == 0) && (ldq % 4 == 0) && (((uintptr_t)x) & 15) == 0 &&
+           (((uintptr_t)q1) & 3) == 0 && (((uintptr_t)q2) & 3) == 0 && sp.bias && sp.alpha &&
+           K <= kSnakeMaxChannels;
+}
+
+// Rows per block of quant_rows_snake: the tile holds at most 4096 floats,
+// a whole number of phase-2 passes where it holds that many rows.
+int snake_tile_rows(int K) {
+    const int rpp = K <= 128 ? 8 : 4, fit = 4096 / K;
+    return fit >= rpp ? fit / rpp * rpp : fit;
+}
+
+template <int CONV, bool RES>
+int quant_rows_snake_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ldx,
+                              const SnakePre &sp, uint8_t *q1, int ldq, float *s1, int32_t *z1,
+                              uint8_t *q2, float *s2, int32_t *z2, uint32_t sflip) {
+    const int R = snake_tile_rows(K);
+    const unsigned k4 = (unsigned)K / 4;
+    // floor(f / k4) == umulhi(2 f, ceil(2^31 / k4)) for the chunk indices
+    // f < 1024 used: the rounding adds less than 2^11 / 2^32 < 1 / k4.
+    const unsigned magic = (unsigned)((0x80000000ull + k4 - 1) / k4);
+    const dim3 grid((unsigned)((M + R - 1) / R)), block(256);
+    const size_t lds = sizeof(float) * ((size_t)3 * K + (size_t)R * K);
+    hipStream_t st = ctx->stream;
+#define IRO_QS(CH, HALF)                                                                          \
+    hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF>), grid, block, lds, st, x, M, K, ldx, \
+                       R, magic, sp.bias, sp.alpha, q1, ldq, s1, z1, q2, s2, z2, sflip)
+    const int ch = (K + 255) / 256;
+    if (K <= 128) IRO_QS(1, true);
+    else if (ch <= 1) IRO_QS(1, false);
+    else if (ch <= 2) IRO_QS(2, false);
+    else if (ch <= 4) IRO_QS(4, false);
+    else IRO_QS(6, false);
+#undef IRO_QS
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    return 0;
+}
+
 template <int CONV, bool RES>
 int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
                         int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
@@ -262,13 +379,21 @@ int quant_rows_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ld
 
 int launch_quant_rows(IroHipContext *ctx, const float *x, int M, int K, int ldx, uint8_t *q1,
                       int ldq, float *s1, int32_t *z1, float *res, uint8_t *q2, float *s2,
-                      int32_t *z2, bool signed_codes) {
+                      int32_t *z2, bool signed_codes, const SnakePre *snake) {
     const uint32_t sflip = signed_codes ? 0x80808080u : 0u;
     if (M <= 0 || K <= 0) return 0;
     const bool two = q2 != nullptr;
+    // The fused snake keeps no remainder rows and takes the vector shapes only.
+    if (snake && (res || !quant_snake_ok(x, K, ldx, q1, ldq, q2, *snake))) return 1;
     prof_begin(ctx);
     int rc;
-    if (ctx->convention == IRO_HIP_GCC_FASTMATH)
+    if (snake && ctx->convention == IRO_HIP_GCC_FASTMATH)
+        rc = two ? quant_rows_snake_dispatch<1, true>(ctx, x, M, K, ldx, *snake, q1, ldq, s1, z1, q2, s2, z2, sflip)
+                 : quant_rows_snake_dispatch<1, false>(ctx, x, M, K, ldx, *snake, q1, ldq, s1, z1, q2, s2, z2, sflip);
+    else if (snake)
+        rc = two ? quant_rows_snake_dispatch<0, true>(ctx, x, M, K, ldx, *snake, q1, ldq, s1, z1, q2, s2, z2, sflip)
+                 : quant_rows_snake_dispatch<0, false>(ctx, x, M, K, ldx, *snake, q1, ldq, s1, z1, q2, s2, z2, sflip);
+    else if (ctx->convention == IRO_HIP_GCC_FASTMATH)
         rc = two ? quant_rows_dispatch<1, true>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2, sflip)
                  : quant_rows_dispatch<1, false>(ctx, x, M, K, ldx, q1, ldq, s1, z1, res, q2, s2, z2, sflip);
     else

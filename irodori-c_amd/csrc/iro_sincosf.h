@@ -23,18 +23,6 @@
 namespace iro {
 namespace {
 
-struct SinCosTab {
-    double sign[4], hpi_inv, hpi, c0, c1, c2, c3, c4, s1, s2, s3;
-};
-
-__constant__ SinCosTab kSinCosTab[2] = {
-    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, 0x1p0,
-     -0x1.ffffffd0c621cp-2, 0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10, 0x1.99343027bf8c3p-16,
-     -0x1.555545995a603p-3, 0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
-    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, -0x1p0,
-     0x1.ffffffd0c621cp-2, -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10, -0x1.99343027bf8c3p-16,
-     -0x1.555545995a603p-3, 0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13}};
-
 // 4/pi in 192 bits; word i holds bits 8i .. 8i+31 of the expansion.
 __constant__ uint32_t kInvPio4[24] = {
     0xa2,       0xa2f9,     0xa2f983,   0xa2f9836e, 0xf9836e4e, 0x836e4e44,
@@ -42,27 +30,12 @@ __constant__ uint32_t kInvPio4[24] = {
     0x2757d1f5, 0x57d1f534, 0xd1f534dd, 0xf534ddc0, 0x34ddc0db, 0xddc0db62,
     0xc0db6295, 0xdb629599, 0x6295993c, 0x95993c43, 0x993c4390, 0x3c439041};
 
-__device__ __forceinline__ float sincos_poly(double x, double x2, const SinCosTab &p, int n) {
-    if ((n & 1) == 0) {
-        const double x3 = x * x2;
-        const double s1 = __builtin_fma(x2, p.s3, p.s2);
-        const double x7 = x3 * x2;
-        const double s = __builtin_fma(x3, p.s1, x);
-        return (float)__builtin_fma(x7, s1, s);
-    }
-    const double x4 = x2 * x2;
-    const double c2 = __builtin_fma(x2, p.c4, p.c3);
-    const double c1 = __builtin_fma(x2, p.c1, p.c0);
-    const double x6 = x4 * x2;
-    const double c = __builtin_fma(x4, p.c2, c1);
-    return (float)__builtin_fma(x6, c2, c);
-}
-
-// sincos_poly of the first table, with the second table's cosine taken as
-// the first's negated (its cosine coefficients are exactly the first's
-// negated, and negation commutes with every rounding, so `neg` negates the
-// cosine result), without per-lane table loads; both polynomials are
-// formed and the lane's one (sin for even k) selected.
+// The polynomial of quadrant k: sin (even k) or cos (odd k) of x, with
+// x2 = x * x, in double, rounded to float.  glibc keeps a second table for
+// quadrants 2 and 3 whose cosine coefficients are exactly the first's
+// negated; negation commutes with every rounding, so `neg` negates the
+// cosine result instead.  Both polynomials are formed from constants (no
+// per-lane table loads) and the lane's one selected.
 __device__ __forceinline__ float sincos_poly_sel(double x, double x2, int k, bool neg) {
     constexpr double c0 = 0x1p0, c1 = -0x1.ffffffd0c621cp-2, c2 = 0x1.55553e1068f19p-5,
                      c3 = -0x1.6c087e89a359dp-10, c4 = 0x1.99343027bf8c3p-16;
@@ -83,46 +56,65 @@ __device__ __forceinline__ float sincos_poly_sel(double x, double x2, int k, boo
     return (k & 1) ? rc : rs;
 }
 
-// cosine = 0: sinf(y); 1: cosf(y).  |y| < 120 (and NaN-free) takes one
-// branch-free path for every lane: below pi/4 the reduction below gives
-// n = 0 and leaves x = y exactly, which is glibc's |y| < pi/4 case, and
-// below 2^-12 glibc's own result (y, or 1) is selected.
-__device__ __forceinline__ float sincosf_glibc(float y, int cosine) {
+// Whether y takes the fast reduction: |y| < 120 (NaN excluded).
+__device__ __forceinline__ bool sincosf_is_small(float y) {
+    return ((__float_as_uint(y) >> 20) & 0x7ff) < 0x42f;
+}
+
+// y reduced to x (double, |x| <= pi/4) in quadrant n; m is n plus the sign
+// bit of y on the large path (n on the fast one): quadrant m & 3 gives the
+// sign of x (+, -, -, +) and, for 2 and 3, the negated cosine.
+struct SinCosArg {
+    double x;
+    int n, m;
+};
+
+// The fast reduction, for sincosf_is_small(y): n = round(y * 2/pi) through
+// a 2^24-scaled product and an integer shift, x = fma(-n, pi/2, y).  Below
+// pi/4 it gives n = 0 and x = y exactly, glibc's |y| < pi/4 case.  No
+// branches, so callers can run several side by side.
+__device__ __forceinline__ SinCosArg sincosf_reduce_small(float y) {
+    const double x = y;
+    const double r = x * 0x1.45F306DC9C883p+23;
+    const int n = ((int32_t)r + 0x800000) >> 24;
+    return {__builtin_fma(-(double)n, 0x1.921FB54442D18p0, x), n, n};
+}
+
+// The large reduction, for finite |y| >= 120 (other y give some SinCosArg
+// that sincosf_finish replaces): a 32 x 96-bit product of the mantissa with
+// 4/pi gives n and a 2.62 fixed-point remainder, scaled by pi * 2^-62.
+__device__ __forceinline__ SinCosArg sincosf_reduce_large(float y) {
     const uint32_t yi = __float_as_uint(y);
-    const uint32_t top = (yi >> 20) & 0x7ff;
-    double x = y;
-    if (__builtin_expect(top < 0x42f, 1)) {  // |y| < 120
-        const double r = x * 0x1.45F306DC9C883p+23;
-        const int n = ((int32_t)r + 0x800000) >> 24;
-        x = __builtin_fma(-(double)n, 0x1.921FB54442D18p0, x);
-        // sign of quadrant n & 3: +1, -1, -1, +1 (an exact sign flip)
-        const double xs = ((n + 1) & 2) ? -x : x;
-        const float v = sincos_poly_sel(xs, x * x, n ^ cosine, (n & 2) != 0);
-        return top < 0x398 ? (cosine ? 1.0f : y) : v;  // |y| < 2^-12
-    }
-    int n;
-    int t;  // table: negated cosine coefficients for quadrants 2, 3
-    double sgn;
-    if (top < 0x7f8) {  // finite
-        const uint32_t *arr = &kInvPio4[(yi >> 26) & 15];
-        const int shift = (yi >> 23) & 7;
-        uint32_t xi = ((yi & 0xffffff) | 0x800000) << shift;
-        uint64_t res0 = (uint32_t)(xi * arr[0]);
-        const uint64_t res1 = (uint64_t)xi * arr[4];
-        const uint64_t res2 = (uint64_t)xi * arr[8];
-        res0 = (res2 >> 32) | (res0 << 32);
-        res0 += res1;
-        const uint64_t nn = (res0 + (1ull << 61)) >> 62;
-        res0 -= nn << 62;
-        x = (double)(int64_t)res0 * 0x1.921FB54442D18p-62;
-        n = (int)nn;
-        const int sign = (int)(yi >> 31);
-        sgn = kSinCosTab[0].sign[(n + sign) & 3];
-        t = ((n + sign) & 2) ? 1 : 0;
-    } else {
-        return (y - y) / (y - y);
-    }
-    return sincos_poly(x * sgn, x * x, kSinCosTab[t], n ^ cosine);
+    const uint32_t *arr = &kInvPio4[(yi >> 26) & 15];
+    const int shift = (yi >> 23) & 7;
+    uint32_t xi = ((yi & 0xffffff) | 0x800000) << shift;
+    uint64_t res0 = (uint32_t)(xi * arr[0]);
+    const uint64_t res1 = (uint64_t)xi * arr[4];
+    const uint64_t res2 = (uint64_t)xi * arr[8];
+    res0 = (res2 >> 32) | (res0 << 32);
+    res0 += res1;
+    const uint64_t nn = (res0 + (1ull << 61)) >> 62;
+    res0 -= nn << 62;
+    const int n = (int)nn;
+    return {(double)(int64_t)res0 * 0x1.921FB54442D18p-62, n, n + (int)(yi >> 31)};
+}
+
+// cosine = 0: sinf(y); 1: cosf(y) from y's reduction: the quadrant's
+// polynomial, or glibc's own result for |y| < 2^-12 (y, or 1) and for
+// non-finite y (NaN).
+__device__ __forceinline__ float sincosf_finish(float y, const SinCosArg &a, int cosine) {
+    const double xs = ((a.m + 1) & 2) ? -a.x : a.x;  // an exact sign flip
+    const float v = sincos_poly_sel(xs, a.x * a.x, a.n ^ cosine, (a.m & 2) != 0);
+    const uint32_t top = (__float_as_uint(y) >> 20) & 0x7ff;
+    if (top >= 0x7f8) return (y - y) / (y - y);
+    return top < 0x398 ? (cosine ? 1.0f : y) : v;
+}
+
+// cosine = 0: sinf(y); 1: cosf(y), every float y.
+__device__ __forceinline__ float sincosf_glibc(float y, int cosine) {
+    const SinCosArg a = __builtin_expect(sincosf_is_small(y), 1) ? sincosf_reduce_small(y)
+                                                                  : sincosf_reduce_large(y);
+    return sincosf_finish(y, a, cosine);
 }
 
 __device__ __forceinline__ float sinf_glibc(float y) { return sincosf_glibc(y, 0); }

@@ -64,8 +64,12 @@ def test_snake_refuses_unaligned_channels(ctx_strict):
         ctx_strict.snake(x, 3, 6, a, x)
 
 
+# The in-place snake before the 1x1 runs inside its quantizer up to 1536
+# channels (one row per half wave up to 128, 1..6 column chunks above) and as
+# its own quotient-form pass beyond.
 UNITS = [(96, 300, 9, True), (96, 300, 1, False), (192, 120, 3, True), (384, 50, 1, False),
-         (96, 5, 9, True), (768, 24, 3, False), (96, 20000, 9, True)]
+         (96, 5, 9, True), (768, 24, 3, False), (96, 20000, 9, True), (4, 33, 1, True),
+         (136, 40, 3, False), (1280, 7, 1, True), (1536, 6, 1, True), (1540, 4, 3, False)]
 
 
 @pytest.mark.parametrize("C,T,dil,two", UNITS)
@@ -81,6 +85,24 @@ def test_residual_unit(ctx, oracle, C, T, dil, two):
                         ctx.to_device(u["b0"]), ctx.to_device(u["alpha1"]), dil, w1,
                         ctx.to_device(u["b1"]), two, two, out)
     assert_bits_equal(out.numpy(), oracle.residual_unit(conv, x, u, two, two), "residual unit")
+
+
+@pytest.mark.parametrize("C,T", [(96, 50), (192, 30), (768, 9)])
+def test_residual_unit_large_hidden(ctx, oracle, C, T):
+    """Inputs scaled so some sines of the fused snake take sinf's |y| >= 120
+    path next to ordinary ones in the same four columns."""
+    conv = ctx.convention
+    rng = np.random.default_rng(7 * C + T)
+    u = cp.residual_unit(rng, C, 3)
+    x = (rng.standard_normal((T, C), dtype=np.float32) * 400).astype(np.float32)
+    w0 = ctx.weight(ctx.to_device(u["w0"]), C, 7 * C)
+    w1 = ctx.weight(ctx.to_device(u["w1"]), C, C)
+    out = ctx.empty((T, C), np.float32)
+    ctx.dacvae_residual(ctx.to_device(x), T, C, w0, ctx.to_device(u["alpha0"]),
+                        ctx.to_device(u["b0"]), ctx.to_device(u["alpha1"]), 3, w1,
+                        ctx.to_device(u["b1"]), True, True, out)
+    want = oracle.residual_unit(conv, x, u, True, True)
+    assert_bits_equal(out.numpy(), want, "residual unit, large hidden values")
 
 
 def _decoder(ctx, seed):

@@ -103,3 +103,5 @@ def test_conv1x1_skip(ctx, oracle, T, C, residual, in_place):
     want = oracle.conv1x1_skip(conv, hidden, skip, *oracle.weight_quantize(conv, w), bias=b,
                                residual=residual)
     assert_bits_equal(out.numpy(), want, "conv1x1 onto skip")
+    if not in_place:
+        assert_bits_equal(sd.numpy(), skip, "skip rows left unchanged")
