@@ -52,7 +52,7 @@ const char *const kProfNames[PK_COUNT] = {
     "gemm_qkvg",         "gemm_qkvg_two_term",  "gemm_swiglu",  "gemm_swiglu_two_term",
     "gemm_gated",        "gemm_gated_two_term", "conv_rows",    "conv_im2col",
     "convt_gather",      "persist_stack",       "snake",        "gemm_swiglu_quant",
-    "other"};
+    "conv_gemm",         "other"};
 
 struct ProfState {
     struct Rec {
@@ -387,8 +387,10 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
         ctx->gemm_lds = tj;
         return 0;
     }
-    if (ti == -6) {  // tj: 1 kernel-7 im2col in one pass (default), 0 the two-pass form
-        ctx->conv_fused = tj != 0;
+    if (ti == -6) {  // tj: kernel-7 convolutions, 2 the GEMM codes its rows (default),
+                     // 1 a one-pass im2col, 0 the two-pass im2col
+        if (tj < 0 || tj > 2) return set_error(ctx, "set_gemm_tile: conv mode 0, 1 or 2");
+        ctx->conv_mode = tj;
         return 0;
     }
     if (ti == -7) {  // tj: 1 the W1/W3 kernel quantizes the hidden state, 0 off (default)
@@ -727,8 +729,20 @@ int iro_hip_int8_linear_two_term(IroHipContext *ctx, const uint8_t *q1, const fl
 int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
                         const IroHipWeight *w, int kernel, int stride, int dilation, int padding,
                         const float *bias, int residual, float *output, int *t_out) {
+    return conv1d_int8(ctx, input, T, C, w, kernel, stride, dilation, padding, bias, residual,
+                       output, t_out, nullptr, nullptr);
+}
+
+}  // extern "C"
+
+namespace iro {
+
+int conv1d_int8(IroHipContext *ctx, const float *input, int T, int C, const IroHipWeight *w,
+                int kernel, int stride, int dilation, int padding, const float *bias,
+                int residual, float *output, int *t_out, const float *snake_alpha,
+                float *snake_out) {
     if (!ctx || !input || !w || !output || T <= 0 || C <= 0 || kernel <= 0 || stride <= 0 ||
-        dilation <= 0 || padding < 0)
+        dilation <= 0 || padding < 0 || (snake_alpha && !snake_out))
         return set_error(ctx, "conv1d_int8: invalid arguments");
     // dacvae.c:340-348
     const long long eff = (long long)dilation * (kernel - 1) + 1;
@@ -742,6 +756,24 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
     const int ldc = (int)round_up((size_t)inner, 16);
     Workspace ws{ctx};
     const size_t olo = ws.reserve(sizeof(float) * T), ohi = ws.reserve(sizeof(float) * T);
+    // Kernel 7: the GEMM codes the input rows itself from their ranges,
+    // which the snake pass (if any) produces with its output rows.
+    ConvRows cr{snake_alpha ? snake_out : input, nullptr, nullptr, T, C, stride, dilation, padding};
+    if (kernel == 7 && ctx->conv_mode == 2 && conv7_gemm_ok(w, cr) &&
+        (!snake_alpha || snake_rows_ok(input, C, snake_out))) {
+        if (ws.commit()) return -1;
+        float *lo = ws.at<float>(olo), *hi = ws.at<float>(ohi);
+        cr.row_lo = lo;
+        cr.row_hi = hi;
+        if (snake_alpha ? launch_snake_rows(ctx, input, T, C, snake_alpha, snake_out, lo, hi)
+                        : launch_conv_rows(ctx, input, T, C, lo, hi))
+            return -1;
+        return launch_conv7_gemm(ctx, w, cr, T_out, residual != 0, bias, output);
+    }
+    if (snake_alpha) {
+        if (iro_hip_snake(ctx, input, T, C, snake_alpha, snake_out)) return -1;
+        input = snake_out;
+    }
     const size_t oc1 = ws.reserve((size_t)ldc * T_out);
     const size_t oc2 = residual ? ws.reserve((size_t)ldc * T_out) : 0;
     const size_t os1 = ws.reserve(sizeof(float) * T_out), oz1 = ws.reserve(sizeof(int32_t) * T_out);
@@ -754,7 +786,7 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
     int32_t *z1 = ws.at<int32_t>(oz1), *z2 = residual ? ws.at<int32_t>(oz2) : nullptr;
     // The one-pass kernel can store the signed operand form the
     // LDS-pipelined GEMM reads.
-    const bool fused = conv_im2col7_ok(C, kernel, ldc) && ctx->conv_fused;
+    const bool fused = conv_im2col7_ok(C, kernel, ldc) && ctx->conv_mode != 0;
     const bool sgn = fused && gemm_lds_cfg(ctx, EPI_LINEAR, residual != 0, T_out, ldc, w->N) != 0;
     if (fused) {
         if (launch_conv_im2col7(ctx, input, T, C, T_out, stride, dilation, padding, c1, c2, ldc,
@@ -781,6 +813,10 @@ int iro_hip_conv1d_int8(IroHipContext *ctx, const float *input, int T, int C,
     a.ldy = w->N;
     return launch_gemm(ctx, w, a, EPI_LINEAR);
 }
+
+}  // namespace iro
+
+extern "C" {
 
 // dacvae.c:696-795 (convtranspose1d_forward_impl with an int8 weight, no
 // snake): quantize the input rows (two-term when `residual`, the

@@ -17,6 +17,7 @@
 #include <algorithm>
 
 #include "iro_internal.h"
+#include "iro_round.h"
 #include "iro_snake.h"
 
 namespace iro {
@@ -125,6 +126,67 @@ int launch_snake(IroHipContext *ctx, const float *x, int T, int C, const float *
     return 0;
 }
 
+// iro_snake_forward (reciprocal form, C <= 1536) out of place, and each
+// output row's lo/hi over its channels as conv_rows computes them
+// (dacvae.c:607-616, lo and hi from 0): the snake a Conv7 applies to its
+// input rows (dacvae.c:599-603) with the row ranges its quantization needs,
+// in one pass.  A block takes R rows (R C <= 4096): phase 1 snakes them as
+// flat float4 chunks (every lane busy) into y and an LDS tile, phase 2
+// reduces each row of the tile with one wavefront.
+template <bool FMA>
+__global__ __launch_bounds__(256) void snake_rows_kernel(const float *__restrict__ x, int T, int C,
+                                                         int R, unsigned k4_magic,
+                                                         const float *__restrict__ alpha,
+                                                         float *__restrict__ y,
+                                                         float *__restrict__ row_lo,
+                                                         float *__restrict__ row_hi) {
+    extern __shared__ __attribute__((aligned(16))) float snake_rows_lds[];
+    float *s_a = snake_rows_lds, *s_i = s_a + C, *tile = s_i + C;
+    for (int c = threadIdx.x; c < C; c += 256) {
+        const float a = alpha[c];
+        s_a[c] = a;
+        s_i[c] = snake_inv(a);
+    }
+    const int row0 = blockIdx.x * R;
+    const int rows = min(R, T - row0);
+    const int k4 = C >> 2, chunks = rows * k4;
+    float4 v4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = threadIdx.x + 256 * j;
+        if (f < chunks) v4[j] = *reinterpret_cast<const float4 *>(x + (size_t)row0 * C + 4 * f);
+    }
+    __syncthreads();  // the staged parameters
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int f = threadIdx.x + 256 * j;
+        if (f < chunks) {
+            const int c4 = f - (int)__umulhi(2u * f, k4_magic) * k4;
+            const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
+            const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
+            const float4 o = snake_value4<true, FMA>(v4[j], a, i);
+            *reinterpret_cast<float4 *>(y + (size_t)row0 * C + 4 * f) = o;
+            *reinterpret_cast<float4 *>(tile + 4 * f) = o;
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    for (int r = threadIdx.x >> 6; r < rows; r += 4) {
+        float lo = 0.0f, hi = 0.0f;
+        for (int c4 = lane; c4 < k4; c4 += 64) {
+            const float4 v = *reinterpret_cast<const float4 *>(tile + r * C + 4 * c4);
+            lo = sel_min(lo, v.x); lo = sel_min(lo, v.y); lo = sel_min(lo, v.z); lo = sel_min(lo, v.w);
+            hi = sel_max(hi, v.x); hi = sel_max(hi, v.y); hi = sel_max(hi, v.z); hi = sel_max(hi, v.w);
+        }
+        lo = wave_min(lo);
+        hi = wave_max(hi);
+        if (lane == 0) {
+            row_lo[row0 + r] = lo;
+            row_hi[row0 + r] = hi;
+        }
+    }
+}
+
 bool snake_args_ok(const float *x, int T, int C, const float *alpha, const float *y) {
     return x && alpha && y && T >= 0 && C > 0 && C % 4 == 0 &&
            ((((uintptr_t)x) | ((uintptr_t)y)) & 15) == 0;
@@ -166,6 +228,38 @@ int conv1x1_skip(IroHipContext *ctx, const float *hidden, const float *skip, int
     return launch_gemm(ctx, w, a, EPI_LINEAR);
 }
 
+}  // namespace
+
+bool snake_rows_ok(const float *x, int C, const float *y) {
+    return C % 4 == 0 && C <= kSnakeMaxChannels && ((((uintptr_t)x) | ((uintptr_t)y)) & 15) == 0;
+}
+
+int launch_snake_rows(IroHipContext *ctx, const float *x, int T, int C, const float *alpha,
+                      float *y, float *row_lo, float *row_hi) {
+    if (T <= 0) return 0;
+    if (!snake_rows_ok(x, C, y)) return set_error(ctx, "snake_rows: unsupported shape");
+    const int R = 4096 / C;
+    const unsigned k4 = (unsigned)C / 4;
+    // floor(f / k4) == umulhi(2 f, ceil(2^31 / k4)) for the chunk indices
+    // f < 1024 used: the rounding adds less than 2^11 / 2^32 < 1 / k4.
+    const unsigned magic = (unsigned)((0x80000000ull + k4 - 1) / k4);
+    const size_t lds = sizeof(float) * ((size_t)2 * C + (size_t)R * C);
+    const dim3 grid((unsigned)((T + R - 1) / R)), block(256);
+    prof_begin(ctx);
+    if (ctx->convention == IRO_HIP_GCC_FASTMATH)
+        hipLaunchKernelGGL((snake_rows_kernel<true>), grid, block, lds, ctx->stream, x, T, C, R,
+                           magic, alpha, y, row_lo, row_hi);
+    else
+        hipLaunchKernelGGL((snake_rows_kernel<false>), grid, block, lds, ctx->stream, x, T, C, R,
+                           magic, alpha, y, row_lo, row_hi);
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    // Algorithmic HBM bytes: the rows in and out, two floats per row.
+    prof_end(ctx, PK_SNAKE, 0, 8.0 * T * C + 8.0 * T);
+    return 0;
+}
+
+namespace {
+
 // The groups of the codec's int8 policy (dacvae.c:38-43).
 enum { GROUP_INITIAL = 1, GROUP_UPSAMPLE = 2, GROUP_CONV7 = 4, GROUP_CONV1 = 8 };
 
@@ -179,9 +273,8 @@ int residual_unit(IroHipContext *ctx, const float *input, int T, int C, const Ir
     // input rows, not in place, dacvae.c:599-603): Conv7, dilation d,
     // padding 3d, no bias.
     int t_out = 0;
-    if (iro_hip_snake(ctx, input, T, C, alpha0, act) ||
-        iro_hip_conv1d_int8(ctx, act, T, C, conv0, 7, 1, dilation, 3 * dilation, nullptr, two7,
-                            hidden, &t_out))
+    if (conv1d_int8(ctx, input, T, C, conv0, 7, 1, dilation, 3 * dilation, nullptr, two7, hidden,
+                    &t_out, alpha0, act))
         return -1;
     if (t_out != T) return set_error(ctx, "dacvae residual: Conv7 changed the length");
     // dacvae.c:967-968: snake with conv0's bias and alpha1, in place, then

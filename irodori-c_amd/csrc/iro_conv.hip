@@ -17,7 +17,7 @@
 // Roofline: HBM.  conv_im2col reads kernel*C*4 bytes (mostly L2 hits: the
 // taps of neighbouring rows overlap) and writes kernel*C (x2) bytes per row.
 #include "iro_internal.h"
-#include "iro_round.h"
+#include "iro_conv_row.h"
 
 namespace iro {
 
@@ -62,13 +62,6 @@ __device__ __forceinline__ uint32_t plane2_code(float x, float v, const RowQ &r,
     return (uint32_t)v2;
 }
 
-// The same before rounding, for pack_codes4.
-template <int CONV>
-__device__ __forceinline__ float plane2_pre(float x, float v, const RowQ &r, float inv2) {
-    const float rem = residual_value<CONV>(x, v, r);
-    return CONV == 1 ? __builtin_fmaf(rem, inv2, 128.0f) : rem * inv2 + 128.0f;
-}
-
 template <int CONV, bool RES>
 __global__ __launch_bounds__(256) void conv_im2col_kernel(
     const float *__restrict__ x, int T, int C, int T_out, int kernel, int stride, int dilation,
@@ -88,16 +81,7 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(
     }
     const RowQ q = row_params<CONV>(lo, hi);
     float sc2 = 0.0f, inv2 = 0.0f;
-    if (RES) {
-        if (CONV == 1) {
-            const float d = hi - lo;
-            sc2 = q.s * c_inv255();
-            inv2 = d * c_inv255() > 0.0f ? c_255_inv255_b() / d : 255.0f;
-        } else {
-            sc2 = q.s / 255.0f;
-            inv2 = 255.0f / q.s;
-        }
-    }
+    if (RES) conv_plane2_params<CONV>(q, lo, hi, sc2, inv2);
     uint8_t *d1 = cols1 + (size_t)r * ldc;
     uint8_t *d2 = RES ? cols2 + (size_t)r * ldc : nullptr;
     const uint32_t zp4 = 0x01010101u * (uint32_t)q.zp;
@@ -206,16 +190,7 @@ __global__ __launch_bounds__(64 * kIm2colRows) void conv_im2col7_kernel(
     hi = HALF ? half_range<true>(hi) : wave_max(hi);
     const RowQ q = row_params<CONV>(lo, hi);
     float sc2 = 0.0f, inv2 = 0.0f;
-    if (RES) {
-        if (CONV == 1) {
-            const float d = hi - lo;
-            sc2 = q.s * c_inv255();
-            inv2 = d * c_inv255() > 0.0f ? c_255_inv255_b() / d : 255.0f;
-        } else {
-            sc2 = q.s / 255.0f;
-            inv2 = 255.0f / q.s;
-        }
-    }
+    if (RES) conv_plane2_params<CONV>(q, lo, hi, sc2, inv2);
     const uint32_t zp4 = (0x01010101u * (uint32_t)q.zp) ^ flip;
     const uint32_t h4 = 0x80808080u ^ flip;
     uint8_t *d1 = cols1 + (size_t)r * ldc;

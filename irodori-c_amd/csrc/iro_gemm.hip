@@ -1068,21 +1068,9 @@ int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K, int 
     return lds_cfg_ok(cfg, two, epi) ? cfg : 0;
 }
 
-int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi) {
-    if (a.M <= 0) return 0;
-    if (a.K <= 0 || a.K % 16 || a.K > w->Kp || a.K < w->K || a.K > 65536 || a.lda < a.K ||
-        a.lda % 16 ||
-        (((uintptr_t)a.a1) & 15) || (a.a2 && (((uintptr_t)a.a2) & 15)) || w->Np % 128 ||
-        (w->Np % 256 && (epi == EPI_SWIGLU || epi == EPI_QKVG)))
-        return set_error(ctx, "gemm: unsupported operand shape (K=%d lda=%d Kp=%d Np=%d)", a.K,
-                         a.lda, w->Kp, w->Np);
-    if (epi == EPI_SWIGLU && (w->layout != 1 || w->part_N[0] % 32))
-        return set_error(ctx, "gemm: SwiGLU epilogue needs an interleaved W1/W3 weight");
-    if (epi != EPI_SWIGLU && w->layout != 0)
-        return set_error(ctx, "gemm: an interleaved weight needs the SwiGLU epilogue");
-    if (epi == EPI_QKVG && (a.seg_n <= 0 || w->N > 4 * a.seg_n))
-        return set_error(ctx, "gemm: QKVG epilogue needs N <= 4 * segment width");
-    KParams kp;
+// The launch parameters every GEMM kernel takes from a weight and its
+// arguments (tiles and grid are the caller's).
+int fill_kparams(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, KParams &kp) {
     kp.a1 = a.a1;
     kp.a2 = a.a2;
     kp.lda = a.lda;
@@ -1118,14 +1106,11 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     kp.ldg = a.ldg > 0 ? a.ldg : a.ldx;
     kp.ldx = a.ldx;
     kp.rows_per_branch = a.rows_per_branch > 0 ? a.rows_per_branch : 1;
-    const bool two = a.a2 != nullptr;
-    const bool skinny = a.M <= 32;
     kp.aflip = a.a_signed ? 0 : (int)0x80808080;
     kp.zero16 = static_cast<const uint8_t *>(ctx->zero16);
     if ((long long)w->Np * w->Kp >= (1LL << 31))
         return set_error(ctx, "gemm: packed weight of %d x %d bytes exceeds 2 GiB", w->Np, w->Kp);
     kp.wbytes = w->Np * w->Kp;
-    const bool bq = a.hq1 != nullptr;
     kp.hq1 = a.hq1;
     kp.hq2 = a.hq2;
     kp.ldhq = a.ldhq;
@@ -1136,6 +1121,28 @@ int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Ep
     kp.band_cnt = kp.band_rng = nullptr;
     kp.err = ctx->dev_err;
     kp.spin_limit = 1 << 20;
+    return 0;
+}
+
+int launch_gemm(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, Epi epi) {
+    if (a.M <= 0) return 0;
+    if (a.K <= 0 || a.K % 16 || a.K > w->Kp || a.K < w->K || a.K > 65536 || a.lda < a.K ||
+        a.lda % 16 ||
+        (((uintptr_t)a.a1) & 15) || (a.a2 && (((uintptr_t)a.a2) & 15)) || w->Np % 128 ||
+        (w->Np % 256 && (epi == EPI_SWIGLU || epi == EPI_QKVG)))
+        return set_error(ctx, "gemm: unsupported operand shape (K=%d lda=%d Kp=%d Np=%d)", a.K,
+                         a.lda, w->Kp, w->Np);
+    if (epi == EPI_SWIGLU && (w->layout != 1 || w->part_N[0] % 32))
+        return set_error(ctx, "gemm: SwiGLU epilogue needs an interleaved W1/W3 weight");
+    if (epi != EPI_SWIGLU && w->layout != 0)
+        return set_error(ctx, "gemm: an interleaved weight needs the SwiGLU epilogue");
+    if (epi == EPI_QKVG && (a.seg_n <= 0 || w->N > 4 * a.seg_n))
+        return set_error(ctx, "gemm: QKVG epilogue needs N <= 4 * segment width");
+    KParams kp;
+    if (fill_kparams(ctx, w, a, kp)) return -1;
+    const bool two = a.a2 != nullptr;
+    const bool skinny = a.M <= 32;
+    const bool bq = a.hq1 != nullptr;
     if (bq && (epi != EPI_SWIGLU || !a.hs1 || !a.hz1 || (a.hq2 && (!a.hs2 || !a.hz2)) ||
                a.ldhq < w->part_N[0] || a.ldhq % 4 || (((uintptr_t)a.hq1) & 3) ||
                (((uintptr_t)a.hq2) & 3)))

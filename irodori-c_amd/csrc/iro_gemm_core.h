@@ -474,6 +474,9 @@ __device__ __forceinline__ bool tile_of(int w, int tiles_m, int tiles_n, int per
 
 }  // namespace
 
+// iro_gemm.hip: the launch parameters common to every GEMM kernel.
+int fill_kparams(IroHipContext *ctx, const IroHipWeight *w, const GemmArgs &a, KParams &kp);
+
 // iro_gemm_lds.hip: the LDS-pipelined kernel.  Shapes: 1 192x256, 2 96x128,
 // 3 128x256, 4 96x256, 5 64x128 (rows x columns per workgroup).
 constexpr int LDS_192x256_CFG = 1, LDS_96x128_CFG = 2;

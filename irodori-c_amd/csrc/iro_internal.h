@@ -28,6 +28,7 @@ enum ProfKind {
     PK_PERSIST_STACK,
     PK_SNAKE,
     PK_GEMM_SWIGLU_Q,
+    PK_CONV_GEMM,
     PK_OTHER,
     PK_COUNT
 };
@@ -65,7 +66,8 @@ struct IroHipContext {
     int gemm_spb = 0;     // column slabs per whole-tile block (0: chosen per GEMM)
     int gemm_lds = 0;     // LDS-pipelined GEMM: 0 shape chosen per GEMM, -1 off, > 0 forced shape
     int gemm_wt_rows = 0; // rows per whole-tile block: 0 chosen per GEMM, 64 or 128
-    int conv_fused = 1;   // kernel-7 convolutions: window ranges and codes in one pass
+    int conv_mode = 2;    // kernel-7 convolutions: 2 the GEMM codes its own rows,
+                          // 1 a one-pass im2col, 0 the two-pass im2col
     int band_quant = 0;   // W1/W3 kernel quantizes the SwiGLU hidden state itself (opt-in)
     // band exchange state of that kernel: zero between launches
     unsigned *band_state = nullptr;
@@ -173,6 +175,29 @@ struct Workspace {
 };
 
 // ---- kernel launchers (iro_quant.hip, iro_gemm.hip, iro_conv.hip) -------
+
+// Input rows of a kernel-7 Conv1d for the GEMM that codes them itself
+// (iro_conv_gemm.hip): x [T, C] and each row's lo/hi over channels.
+struct ConvRows {
+    const float *x;
+    const float *row_lo, *row_hi;
+    int T, C, stride, dilation, padding;
+};
+bool conv7_gemm_ok(const IroHipWeight *w, const ConvRows &cr);
+// iro_codec.hip: snake (reciprocal form) of x into y with each row's lo/hi.
+bool snake_rows_ok(const float *x, int C, const float *y);
+int launch_snake_rows(IroHipContext *ctx, const float *x, int T, int C, const float *alpha,
+                      float *y, float *row_lo, float *row_hi);
+// iro_capi.hip: iro_hip_conv1d_int8, optionally with the snake of
+// snake_alpha applied to the input rows first (into snake_out, [T, C]), as
+// conv1d_int8_forward does with a snake (dacvae.c:599-603).
+int conv1d_int8(IroHipContext *ctx, const float *input, int T, int C, const IroHipWeight *w,
+                int kernel, int stride, int dilation, int padding, const float *bias,
+                int residual, float *output, int *t_out, const float *snake_alpha,
+                float *snake_out);
+// Returns 1 (nothing launched) when conv7_gemm_ok refuses the shape.
+int launch_conv7_gemm(IroHipContext *ctx, const IroHipWeight *w, const ConvRows &cr, int T_out,
+                      bool two, const float *bias, float *y);
 
 // Snake applied to each element before it is quantized: x + bias[c], then
 // the reciprocal-form snake with alpha[c] (the in-place snake_bias of a

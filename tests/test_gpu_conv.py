@@ -22,6 +22,13 @@ CASES = [  # T, C, N, kernel, stride, dilation, padding
     (33, 6, 10, 7, 1, 1, 3),
     (300, 96, 96, 7, 1, 9, 27),
     (5, 4, 4, 7, 1, 1, 3),
+    # kernel 7 with C % 16 == 0, 64 <= C <= 256: the GEMM that codes its own rows
+    (50, 64, 64, 7, 1, 1, 3),
+    (70, 80, 40, 7, 2, 2, 6),
+    (130, 64, 300, 7, 1, 5, 15),
+    (100, 128, 256, 7, 1, 1, 3),
+    (90, 96, 96, 7, 1, 2, 0),
+    (3, 192, 192, 7, 1, 9, 27),
 ]
 
 
@@ -47,6 +54,19 @@ def _conv(ctx, oracle, T, C, N, k, st, dil, pad, residual, seed, zero_band=True)
 @pytest.mark.parametrize("residual", [0, 1], ids=["one-plane", "two-plane"])
 def test_conv_small(ctx, oracle, T, C, N, k, st, dil, pad, residual):
     got, want = _conv(ctx, oracle, T, C, N, k, st, dil, pad, residual, 70 + T + C)
+    assert_bits_equal(got, want, "conv output")
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2], ids=["two-pass", "one-pass", "gemm-codes"])
+@pytest.mark.parametrize("residual", [0, 1], ids=["one-plane", "two-plane"])
+def test_conv7_modes_agree(ctx, oracle, mode, residual):
+    """Each kernel-7 form (two-pass im2col, one-pass im2col, the GEMM that
+    codes its own rows) gives the reference's output."""
+    ctx.set_gemm_tile(-6, mode)
+    try:
+        got, want = _conv(ctx, oracle, 2000, 96, 96, 7, 1, 3, 9, residual, 55)
+    finally:
+        ctx.set_gemm_tile(-6, 2)
     assert_bits_equal(got, want, "conv output")
 
 
