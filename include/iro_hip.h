@@ -63,13 +63,18 @@ void *iro_hip_stream(IroHipContext *ctx);
       -1 off, 1 192x256, 2 96x128, 3 128x256, 4 96x256, 5 64x128 rows x
       columns per workgroup; shapes a GEMM cannot take fall back),
    -5 rows per whole-tile block (0 chosen per GEMM, 64, 128),
-   -6 kernel-7 convolution codes (1 window ranges and codes in one pass,
-      the default; 0 two passes),
+   -6 kernel-7 convolution codes (2, the default: the GEMM codes the input
+      rows itself from their ranges where that is measured faster -- 64..256
+      channels in multiples of 32, or up to 1024 on inputs of 65536 rows or
+      more -- else as 1; 1 window ranges and im2col codes in one pass; 0
+      two passes),
    -7 SwiGLU hidden state (0, the default: stored in fp32 and quantized by
       a row quantization launch; 1: the W1/W3 kernel quantizes it for W2
       itself, its blocks exchanging row ranges through device memory, when
       the GEMM's grid fits the GPU at once and the caller does not ask for
-      the fp32 hidden state -- measured slower at the DiT shapes).
+      the fp32 hidden state -- measured slower at the DiT shapes),
+   -8 output channels per block of the kernel-7 GEMM that codes its rows
+      (0 chosen per conv, 128, 256).
    Tuning knobs only: results are identical for every setting.  No
    counterpart in the reference (oneMKL picks its own blocking). */
 int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj);

@@ -398,6 +398,13 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
         ctx->band_quant = tj;
         return 0;
     }
+    if (ti == -8) {  // tj: output channels per block of the kernel-7 GEMM that codes its
+                     // rows, 0 chosen per conv, 128 or 256
+        if (tj != 0 && tj != 128 && tj != 256)
+            return set_error(ctx, "set_gemm_tile: conv GEMM columns 0, 128 or 256");
+        ctx->conv_cols = tj;
+        return 0;
+    }
     if (ti == -5) {  // tj: rows per whole-tile block, 0 per GEMM, 64 or 128
         if (tj != 0 && tj != 64 && tj != 128)
             return set_error(ctx, "set_gemm_tile: whole-tile rows 0, 64 or 128");
@@ -759,7 +766,7 @@ int conv1d_int8(IroHipContext *ctx, const float *input, int T, int C, const IroH
     // Kernel 7: the GEMM codes the input rows itself from their ranges,
     // which the snake pass (if any) produces with its output rows.
     ConvRows cr{snake_alpha ? snake_out : input, nullptr, nullptr, T, C, stride, dilation, padding};
-    if (kernel == 7 && ctx->conv_mode == 2 && conv7_gemm_ok(w, cr) &&
+    if (kernel == 7 && ctx->conv_mode == 2 && conv7_gemm_ok(w, cr) && conv7_gemm_pays(cr, T_out) &&
         (!snake_alpha || snake_rows_ok(input, C, snake_out))) {
         if (ws.commit()) return -1;
         float *lo = ws.at<float>(olo), *hi = ws.at<float>(ohi);

@@ -13,32 +13,39 @@
 //
 // Block: 256 threads, 64 output steps x 128*TJ output channels, four waves
 // side by side along N, each a 64 x 32*TJ tile of v_mfma_i32_32x32x32_i8.
-// k runs in chunks of 128 (C % 16 == 0, so each 16-column piece lies in one
-// tap): per chunk every thread codes two 16-value pieces per plane into LDS
-// in fragment order (signed operand form, a ^ 0x80), the inputs of the next
-// chunk being loaded into registers while the MFMAs of this one run; one
-// barrier per chunk.  Each wave streams its weight fragments from the packed
-// buffer one chunk ahead.  Padding taps code the zero point (plane 2: 128);
-// k at or past 7*C codes the signed zero, against zero weights.  Rows past
-// T_out repeat row T_out - 1 and are never stored.
-// Roofline: HBM, the input once (its taps re-read from L2) and the output
-// once, against 2 * 7C * N ops per output step and plane.
+// The reduction runs over 32-channel blocks with the 7 taps inside (integer
+// sums are exact in any order; the weight fragment of tap j, channel block
+// cb is k block j * C/32 + cb of the packed [N, 7C] weight).  Per
+// channel block the block loads its input window -- rows m0*stride -
+// padding .. + 63*stride + 6*dilation, 32 channels, rows outside [0, T) as
+// 0 -- once into LDS with coalesced loads (each input value is read once
+// per block instead of once per tap), codes the 7 taps' activation
+// fragments from it into LDS (signed operand form, a ^ 0x80; a padding row
+// of zeros codes the zero point, and 128 in plane 2, exactly the padding
+// codes), and runs the 7 k blocks of MFMAs, the next window's loads and the
+// weight fragments in flight meanwhile.  Rows past T_out repeat row
+// T_out - 1 and are never stored.
+// Roofline: HBM, the input once (its windows overlap by 6*dilation rows
+// from L2) and the output once, against 2 * 7C * N ops per output step and
+// plane.
 #include "iro_gemm_core.h"
 #include "iro_conv_row.h"
 
 namespace iro {
 namespace {
 
-constexpr int kCvKC = 128;  // k bytes per chunk
-constexpr int kCvBM = 64;   // output steps per block
+constexpr int kCvBM = 64;     // output steps per block
+constexpr int kCvWRows = 128;  // input window rows per block, at most
+constexpr int kCvWPitch = 36;  // floats per LDS window row (32 + 4: spreads banks)
 
 template <int CONV, bool TWO, int TJ>
 __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows cr) {
-    constexpr int TI = 2, BM = kCvBM, PL = TWO ? 2 : 1, KC = kCvKC, KBC = KC / 32;
-    constexpr int PLANE = BM * KC;         // LDS bytes per plane per chunk
-    constexpr int PPT = PLANE / 16 / 256;  // pieces per thread per plane
-    static_assert(BM == 32 * TI && PPT * 256 * 16 == PLANE, "piece geometry");
-    __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][PL * PLANE];
+    constexpr int TI = 2, BM = kCvBM, PL = TWO ? 2 : 1;
+    constexpr int FR = 7 * TI;             // activation fragments per plane per channel block
+    constexpr int APLANE = FR * 64 * 16;   // LDS bytes per plane
+    constexpr int WLD = kCvWRows * 8 / 256;  // window float4 loads per thread, at most
+    __shared__ __attribute__((aligned(16))) float xw[kCvWRows * kCvWPitch];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_a[PL * APLANE];
     __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
     __shared__ float r_inv[BM], r_zpf[BM], r_s[BM], r_inv2[BM];
 
@@ -49,7 +56,9 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int m0 = by * BM;
     const int nb0 = bx * 4 * TJ + wave * TJ;  // first packed 32-row weight block of this wave
-    const int C = cr.C;
+    const int C = cr.C, cbs = C / 32;
+    const int w0 = m0 * cr.stride - cr.padding;                // first window row
+    const int wrows = 63 * cr.stride + 6 * cr.dilation + 1;   // <= kCvWRows
 
     // Row parameters of the block's output steps (dacvae.c:617-652).
     if (tid < BM) {
@@ -81,94 +90,70 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
     }
     const ColParams<TJ> cp = load_cols<EPI_LINEAR, TJ>(p, nb0, lane, m0, BM);
 
-    // Pieces of this thread: piece q = tid + 256 i of a plane's chunk is
-    // fragment f = q / 64 = [k block q / 64 / TI][row block f % TI], lane
-    // q % 64 of it: row (f % TI) * 32 + q % 32, k offset 16 ((q % 64) / 32).
-    // Its tap and channel advance by 128 per chunk (C >= 64: at most two
-    // wraps per chunk).
-    int prow[PPT], pbase[PPT], ptap[PPT], pch[PPT];
+    // Window of channel block cb: float4 i = tid + 256 u is row i / 8,
+    // channels 4 (i % 8) .. +3 of the block.
+    float4 wv[WLD];
+    auto load_window = [&](int cb) {
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-        const int q = tid + 256 * i, f = q >> 6, ln = q & 63;
-        prow[i] = (f % TI) * 32 + (ln & 31);
-        int t = m0 + prow[i];
-        t = t < p.M ? t : p.M - 1;
-        pbase[i] = t * cr.stride - cr.padding;
-        const int k = (f / TI) * 32 + (ln >> 5) * 16;
-        ptap[i] = k / C;
-        pch[i] = k - ptap[i] * C;
-    }
-    // Inputs of one chunk: per piece 16 floats, or a marker for padding
-    // taps (kind 1) and k past 7C (kind 2).
-    float4 xv[PPT][4];
-    int kind[PPT];
-    auto load_x = [&]() {
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int it = pbase[i] + ptap[i] * cr.dilation;
-            kind[i] = ptap[i] >= 7 ? 2 : (it >= 0 && it < cr.T ? 0 : 1);
-            if (kind[i] == 0) {
-                const float4 *src = reinterpret_cast<const float4 *>(cr.x + (size_t)it * C + pch[i]);
-#pragma unroll
-                for (int g = 0; g < 4; ++g) xv[i][g] = src[g];
-            }
-            // next chunk's tap and channel
-            pch[i] += KC;
-            if (pch[i] >= C) { pch[i] -= C; ++ptap[i]; }
-            if (pch[i] >= C) { pch[i] -= C; ++ptap[i]; }
+        for (int u = 0; u < WLD; ++u) {
+            const int i = tid + 256 * u, r = i >> 3, gr = w0 + r;
+            wv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < wrows && gr >= 0 && gr < cr.T)
+                wv[u] = *reinterpret_cast<const float4 *>(cr.x + (size_t)gr * C + cb * 32 +
+                                                          4 * (i & 7));
         }
     };
-    auto code_x = [&](int buf) {
+    auto store_window = [&]() {
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int r = prow[i];
+        for (int u = 0; u < WLD; ++u) {
+            const int i = tid + 256 * u, r = i >> 3;
+            if (r < wrows) *reinterpret_cast<float4 *>(&xw[r * kCvWPitch + 4 * (i & 7)]) = wv[u];
+        }
+    };
+    // Fragment f = tap * TI + rb, lane ln: output row rb*32 + ln % 32,
+    // channels 16 (ln / 32) .. +15 of window row row*stride + tap*dilation.
+    auto code_window = [&]() {
+        for (int pc = tid; pc < FR * 64; pc += 256) {
+            const int f = pc >> 6, ln = pc & 63, tap = f / TI, rb = f - tap * TI;
+            const int r = rb * 32 + (ln & 31);
+            const float *src = &xw[(r * cr.stride + tap * cr.dilation) * kCvWPitch + (ln >> 5) * 16];
             RowQ q;
             q.s = r_s[r];
             q.inv = r_inv[r];
             q.zpf = r_zpf[r];
             q.zp = rl.zx[0][r];
             v4i w1, w2;
-            if (kind[i] == 0) {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 e = xv[i][g];
-                    const uint32_t c1 = pack_codes4(quant_pre<CONV>(e.x, q), quant_pre<CONV>(e.y, q),
-                                                    quant_pre<CONV>(e.z, q), quant_pre<CONV>(e.w, q));
-                    w1[g] = (int)(c1 ^ 0x80808080u);
-                    if (TWO) {
-                        const float inv2 = r_inv2[r];
-                        const float4 c4 = unpack_codes4(c1);
-                        const uint32_t c2 = pack_codes4(plane2_pre<CONV>(e.x, c4.x, q, inv2),
-                                                        plane2_pre<CONV>(e.y, c4.y, q, inv2),
-                                                        plane2_pre<CONV>(e.z, c4.z, q, inv2),
-                                                        plane2_pre<CONV>(e.w, c4.w, q, inv2));
-                        w2[g] = (int)(c2 ^ 0x80808080u);
-                    }
+            for (int g = 0; g < 4; ++g) {
+                const float4 e = *reinterpret_cast<const float4 *>(src + 4 * g);
+                const uint32_t c1 = pack_codes4(quant_pre<CONV>(e.x, q), quant_pre<CONV>(e.y, q),
+                                                quant_pre<CONV>(e.z, q), quant_pre<CONV>(e.w, q));
+                w1[g] = (int)(c1 ^ 0x80808080u);
+                if (TWO) {
+                    const float inv2 = r_inv2[r];
+                    const float4 c4 = unpack_codes4(c1);
+                    const uint32_t c2 = pack_codes4(plane2_pre<CONV>(e.x, c4.x, q, inv2),
+                                                    plane2_pre<CONV>(e.y, c4.y, q, inv2),
+                                                    plane2_pre<CONV>(e.z, c4.z, q, inv2),
+                                                    plane2_pre<CONV>(e.w, c4.w, q, inv2));
+                    w2[g] = (int)(c2 ^ 0x80808080u);
                 }
-            } else {
-                // padding tap: the zero point (plane 2: 128); past 7C: signed 0
-                const int z = kind[i] == 1 ? (int)((0x01010101u * (uint32_t)q.zp) ^ 0x80808080u) : 0;
-                w1 = v4i{z, z, z, z};
-                w2 = v4i{0, 0, 0, 0};
             }
-            const int q16 = (tid + 256 * i) * 16;
-            *reinterpret_cast<v4i *>(&lds_a[buf][q16]) = w1;
-            if (TWO) *reinterpret_cast<v4i *>(&lds_a[buf][PLANE + q16]) = w2;
+            *reinterpret_cast<v4i *>(&lds_a[pc * 16]) = w1;
+            if (TWO) *reinterpret_cast<v4i *>(&lds_a[APLANE + pc * 16]) = w2;
         }
     };
 
     const __amdgpu_buffer_rsrc_t wr = weight_rsrc(p);
     const int jstride = p.kb_count * 1024;  // bytes between 32-row weight blocks
     const int wbase = nb0 * jstride;
-    const int nc = (p.K + KC - 1) / KC;
-    auto load_b = [&](v4i (&dst)[KBC][TJ], int c) {
+    v4i bf[7][TJ];
+    auto load_b = [&](int cb) {
 #pragma unroll
-        for (int u = 0; u < KBC; ++u) {
-            int kb = c * KBC + u;
-            kb = kb < p.kb_count ? kb : p.kb_count - 1;
+        for (int tap = 0; tap < 7; ++tap)
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) dst[u][j] = load_frag(wr, lane * 16, wbase + j * jstride + kb * 1024);
-        }
+            for (int j = 0; j < TJ; ++j)
+                bf[tap][j] = load_frag(wr, lane * 16, wbase + j * jstride + (tap * cbs + cb) * 1024);
     };
 
     v16i acc[TI][TJ], acc2[TI][TJ];
@@ -182,44 +167,36 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
                 acc2[i][j][r] = 0;
             }
 
-    v4i bcur[KBC][TJ], bnext[KBC][TJ];
-    load_b(bcur, 0);
-    load_x();
-    __syncthreads();  // row parameters
-    code_x(0);
-    __syncthreads();
-    for (int c = 0; c < nc; ++c) {
-        const bool more = c + 1 < nc;
-        if (more) {
-            load_b(bnext, c + 1);
-            load_x();
-        }
-        const uint8_t *abuf = lds_a[c & 1];
+    load_window(0);
+    for (int cb = 0; cb < cbs; ++cb) {
+        load_b(cb);
+        store_window();
+        __syncthreads();  // the window (and, first time round, the row parameters)
+        code_window();
+        __syncthreads();
+        if (cb + 1 < cbs) load_window(cb + 1);
 #pragma unroll
-        for (int u = 0; u < KBC; ++u) {
+        for (int tap = 0; tap < 7; ++tap) {
             v4i a[PL][TI];
 #pragma unroll
             for (int pl = 0; pl < PL; ++pl)
 #pragma unroll
                 for (int i = 0; i < TI; ++i)
-                    a[pl][i] = *reinterpret_cast<const v4i *>(abuf + pl * PLANE +
-                                                             ((u * TI + i) * 64 + lane) * 16);
+                    a[pl][i] = *reinterpret_cast<const v4i *>(&lds_a[pl * APLANE +
+                                                                     ((tap * TI + i) * 64 + lane) * 16]);
 #pragma unroll
             for (int i = 0; i < TI; ++i)
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], bcur[u][j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], bf[tap][j], acc[i][j], 0, 0, 0);
                     if (TWO)
-                        acc2[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[PL - 1][i], bcur[u][j],
+                        acc2[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[PL - 1][i], bf[tap][j],
                                                                            acc2[i][j], 0, 0, 0);
                 }
         }
-        if (more) code_x((c + 1) & 1);
+        // The next round's window store and codes overwrite LDS the MFMAs
+        // above read: every wave passes the barrier after its MFMAs.
         __syncthreads();
-#pragma unroll
-        for (int u = 0; u < KBC; ++u)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) bcur[u][j] = bnext[u][j];
     }
 
     epilogue<CONV, EPI_LINEAR, TWO, TI, TJ, BM>(p, acc, acc2, cp, rl, nullptr, m0, nb0, lane);
@@ -227,17 +204,22 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
 
 }  // namespace
 
-// Shapes the kernel takes.  It is chosen only up to 256 channels: each lane
-// of an MFMA activation fragment holds its own row, so the loader's vector
-// loads touch 32 rows each and its coding work is repeated per column tile;
-// that beats writing and re-reading the im2col codes where they dominate
-// (C = 96: 323 against 530 us per decoder Conv7, C = 192: 314 against 350
-// us) and loses where the GEMM does (C = 384: 130 against 101 us, C = 768
-// and the 512-channel Conv1d: about twice the time).
+// Shapes the kernel takes: C a multiple of 32 from 64 to 1024, a window of
+// at most 128 rows (stride 1, dilation <= 10).
 bool conv7_gemm_ok(const IroHipWeight *w, const ConvRows &cr) {
-    return cr.C % 16 == 0 && cr.C >= 64 && cr.C <= 256 && (((uintptr_t)cr.x) & 15) == 0 &&
-           w->Np % 128 == 0 && w->K == 7 * cr.C && w->layout == 0;
+    return cr.C % 32 == 0 && cr.C >= 64 && cr.C <= 1024 && (((uintptr_t)cr.x) & 15) == 0 &&
+           63LL * cr.stride + 6LL * cr.dilation + 1 <= kCvWRows && w->Np % 128 == 0 &&
+           w->K == 7 * cr.C && w->layout == 0;
 }
+
+// Where it beats the im2col path (which writes the codes and reads them
+// back): up to 256 channels always (C = 96, two planes: 286 against 579 us
+// at T = 480000; C = 192: 224 against 373 us at T = 240000), wider rows on
+// long inputs only (C = 384, T = 120000: 347 against 489 us; C = 768,
+// T = 60000: 473 against 542 us), where the im2col traffic outweighs the
+// coding work each column tile repeats; on short ones it loses (C = 512,
+// T = 24000: 100 against 94 us; C = 1024, T = 6000: 77 against 51 us).
+bool conv7_gemm_pays(const ConvRows &cr, int T_out) { return cr.C <= 256 || T_out >= 65536; }
 
 int launch_conv7_gemm(IroHipContext *ctx, const IroHipWeight *w, const ConvRows &cr, int T_out,
                       bool two, const float *bias, float *y) {
@@ -250,9 +232,11 @@ int launch_conv7_gemm(IroHipContext *ctx, const IroHipWeight *w, const ConvRows 
     a.ldy = w->N;
     KParams kp;
     if (fill_kparams(ctx, w, a, kp)) return -1;
-    // 64 x 256 tiles for one plane; two planes keep 64 x 128 (their
-    // accumulators would not fit twice).
-    const int tj = !two && w->Np % 256 == 0 ? 2 : 1;
+    // 64 x 128 tiles up to 256 channels (four blocks per CU), 64 x 256 above
+    // (each column tile repeats the coding); two planes always 64 x 128.
+    int tj = !two && w->Np % 256 == 0 && cr.C > 256 ? 2 : 1;
+    if (ctx->conv_cols == 128 || two) tj = 1;
+    if (ctx->conv_cols == 256 && !two && w->Np % 256 == 0) tj = 2;
     kp.tiles_n = w->Np / (128 * tj);
     kp.tiles_m = (T_out + kCvBM - 1) / kCvBM;
     const int tiles = kp.tiles_n * kp.tiles_m;

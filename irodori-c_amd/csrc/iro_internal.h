@@ -68,6 +68,7 @@ struct IroHipContext {
     int gemm_wt_rows = 0; // rows per whole-tile block: 0 chosen per GEMM, 64 or 128
     int conv_mode = 2;    // kernel-7 convolutions: 2 the GEMM codes its own rows,
                           // 1 a one-pass im2col, 0 the two-pass im2col
+    int conv_cols = 0;    // output channels per block of that GEMM: 0 chosen, 128, 256
     int band_quant = 0;   // W1/W3 kernel quantizes the SwiGLU hidden state itself (opt-in)
     // band exchange state of that kernel: zero between launches
     unsigned *band_state = nullptr;
@@ -184,6 +185,7 @@ struct ConvRows {
     int T, C, stride, dilation, padding;
 };
 bool conv7_gemm_ok(const IroHipWeight *w, const ConvRows &cr);
+bool conv7_gemm_pays(const ConvRows &cr, int T_out);
 // iro_codec.hip: snake (reciprocal form) of x into y with each row's lo/hi.
 bool snake_rows_ok(const float *x, int C, const float *y);
 int launch_snake_rows(IroHipContext *ctx, const float *x, int T, int C, const float *alpha,

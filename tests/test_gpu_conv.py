@@ -22,7 +22,7 @@ CASES = [  # T, C, N, kernel, stride, dilation, padding
     (33, 6, 10, 7, 1, 1, 3),
     (300, 96, 96, 7, 1, 9, 27),
     (5, 4, 4, 7, 1, 1, 3),
-    # kernel 7 with C % 16 == 0, 64 <= C <= 256: the GEMM that codes its own rows
+    # kernel 7 with C % 32 == 0, 64 <= C <= 256: the GEMM that codes its own rows
     (50, 64, 64, 7, 1, 1, 3),
     (70, 80, 40, 7, 2, 2, 6),
     (130, 64, 300, 7, 1, 5, 15),
@@ -57,17 +57,45 @@ def test_conv_small(ctx, oracle, T, C, N, k, st, dil, pad, residual):
     assert_bits_equal(got, want, "conv output")
 
 
-@pytest.mark.parametrize("mode", [0, 1, 2], ids=["two-pass", "one-pass", "gemm-codes"])
+@pytest.mark.parametrize("mode,cols", [(0, 0), (1, 0), (2, 0), (2, 128), (2, 256)],
+                         ids=["two-pass", "one-pass", "gemm-codes", "gemm-codes-128",
+                              "gemm-codes-256"])
 @pytest.mark.parametrize("residual", [0, 1], ids=["one-plane", "two-plane"])
-def test_conv7_modes_agree(ctx, oracle, mode, residual):
+def test_conv7_modes_agree(ctx, oracle, mode, cols, residual):
     """Each kernel-7 form (two-pass im2col, one-pass im2col, the GEMM that
-    codes its own rows) gives the reference's output."""
+    codes its own rows with either column tile) gives the reference's
+    output."""
     ctx.set_gemm_tile(-6, mode)
+    ctx.set_gemm_tile(-8, cols)
     try:
-        got, want = _conv(ctx, oracle, 2000, 96, 96, 7, 1, 3, 9, residual, 55)
+        got, want = _conv(ctx, oracle, 2000, 96, 256, 7, 1, 3, 9, residual, 55)
     finally:
         ctx.set_gemm_tile(-6, 2)
+        ctx.set_gemm_tile(-8, 0)
     assert_bits_equal(got, want, "conv output")
+
+
+def test_conv7_gemm_codes_wide_long(ctx):
+    """Above 256 channels the GEMM that codes its own rows runs on long
+    inputs only (here 320 channels, 65600 steps, 64 x 256 tiles); its output
+    equals the one-pass im2col form's, which the oracle tests above pin."""
+    T, C, N = 65600, 320, 256
+    x = gauss(31, (T, C))
+    x[100:140] = 0.0
+    w = gauss(32, (N, 7 * C), 0.02)
+    b = gauss(33, (N,), 0.01)
+    W = ctx.weight(ctx.to_device(w), N, 7 * C)
+    xd, bd = ctx.to_device(x), ctx.to_device(b)
+    outs = []
+    for mode in (2, 1):
+        ctx.set_gemm_tile(-6, mode)
+        try:
+            yd = ctx.empty((T, N), np.float32)
+            ctx.conv1d(xd, T, C, W, 7, 1, 3, 9, bd, 0, yd)
+            outs.append(yd.numpy())
+        finally:
+            ctx.set_gemm_tile(-6, 2)
+    assert_bits_equal(outs[0], outs[1], "conv output, GEMM codes vs im2col")
 
 
 @pytest.mark.parametrize("T,C,N,dil,pad", [(24000, 512, 512, 1, 3), (6000, 1024, 256, 3, 9)],
