@@ -278,9 +278,15 @@ int residual_unit(IroHipContext *ctx, const float *input, int T, int C, const Ir
         return -1;
     if (t_out != T) return set_error(ctx, "dacvae residual: Conv7 changed the length");
     // dacvae.c:967-968: snake with conv0's bias and alpha1, in place, then
-    // dacvae.c:983-1012: output = input, then += conv1(hidden) + bias.  The
-    // in-place snake is the 1x1 quantizer's pre-op where it takes the shape
-    // (its reciprocal form, C <= 1536), else its own pass.
+    // dacvae.c:983-1012: output = input, then += conv1(hidden) + bias.  Up to
+    // 256 channels one kernel does all of it; else the in-place snake is the
+    // 1x1 quantizer's pre-op where it takes the shape (its reciprocal form,
+    // C <= 1536), else its own pass.
+    if (conv0_bias && alpha1 && ctx->conv_mode == 2) {
+        const int rc = launch_conv1x1_snake(ctx, conv1, hidden, T, conv0_bias, alpha1, two1,
+                                            conv1_bias, input, output);
+        if (rc <= 0) return rc;
+    }
     if (conv0_bias && alpha1 && C <= kSnakeMaxChannels) {
         const SnakePre sp{conv0_bias, alpha1};
         const int rc = conv1x1_skip(ctx, hidden, input, T, conv1, conv1_bias, two1, output, &sp);

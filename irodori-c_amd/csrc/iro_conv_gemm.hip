@@ -30,6 +30,8 @@
 // plane.
 #include "iro_gemm_core.h"
 #include "iro_conv_row.h"
+#include "iro_quant_row.h"
+#include "iro_snake.h"
 
 namespace iro {
 namespace {
@@ -202,7 +204,189 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
     epilogue<CONV, EPI_LINEAR, TWO, TI, TJ, BM>(p, acc, acc2, cp, rl, nullptr, m0, nb0, lane);
 }
 
+// The 1x1 of a decoder residual unit (dacvae.c:967-1012) as one kernel:
+// the in-place snake_bias of conv0's output (snake_bias_forward,
+// dacvae.c:910-931, reciprocal form), the row quantization of the result
+// (ops.c:321-348; two-term ops.c:427-442 with RES), the GEMM and
+// output = skip + lin(q1) + bias (+ lin(q2)) -- so neither the snaked rows
+// nor their codes reach HBM.  With C <= 192 a 64-row block holds whole
+// rows: phase 1 loads them as flat float4 chunks (every lane busy), snakes
+// them with per-channel bias, alpha and reciprocal from LDS into an LDS
+// tile; phase 2 quantizes each tile row with the row quantizer of
+// iro_quant_row.h (half a wavefront per row up to 128 channels), writing
+// the codes into LDS in MFMA fragment order and the row parameters where the
+// epilogue reads them; then each wave runs the C/32 k blocks of MFMAs
+// against its weight fragments and the epilogue adds the skip rows.  One
+// column tile covers all N (TJ = Np / 128).  Rows past M hold zeros and are
+// never stored.
+constexpr int kRsBM = 64;
+
+template <int CONV, bool TWO, int TJ, bool HALF>
+__global__ __launch_bounds__(256, 2) void conv1x1_snake_kernel(KParams p, const float *__restrict__ hid,
+                                                               const float *__restrict__ sbias,
+                                                               const float *__restrict__ salpha,
+                                                               unsigned k4_magic) {
+    constexpr int TI = 2, BM = kRsBM, PL = TWO ? 2 : 1;
+    extern __shared__ __attribute__((aligned(16))) float rs_lds[];
+    __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
+    const int C = p.K, KB = C / 32, pitch = C;
+    float *s_b = rs_lds, *s_a = s_b + C, *s_i = s_a + C, *tile = s_i + C;
+    uint8_t *codes = reinterpret_cast<uint8_t *>(tile + BM * pitch);  // PL planes of BM x C
+    const int plane = BM * C;
+
+    int bx, by;
+    if (!tile_of(blockIdx.x, p.tiles_m, p.tiles_n, p.tiles_per_xcd, p.row_major, bx, by)) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int m0 = by * BM;
+    const int nb0 = bx * 4 * TJ + wave * TJ;
+
+    for (int c = tid; c < C; c += 256) {
+        const float a = salpha[c];
+        s_b[c] = sbias[c];
+        s_a[c] = a;
+        s_i[c] = snake_inv(a);
+    }
+    const ColParams<TJ> cp = load_cols<EPI_LINEAR, TJ>(p, nb0, lane, m0, BM);
+    // Phase 1: float4 f = tid + 256 u of the block is row f / (C/4).
+    const int k4 = C >> 2, chunks = BM * k4;  // <= 4096
+    constexpr int U = 16;                     // 4096 / 256
+    float4 v4[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int f = tid + 256 * u;
+        v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (f < chunks) {
+            const int r = __umulhi(2u * f, k4_magic);
+            if (m0 + r < p.M)
+                v4[u] = *reinterpret_cast<const float4 *>(hid + (size_t)m0 * C + 4 * f);
+        }
+    }
+    __syncthreads();  // the staged parameters
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int f = tid + 256 * u;
+        if (f < chunks) {
+            const int r = __umulhi(2u * f, k4_magic), c4 = f - r * k4;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m0 + r < p.M) {
+                const float4 b = *reinterpret_cast<const float4 *>(s_b + 4 * c4);
+                const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
+                const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
+                const float4 xv = make_float4(v4[u].x + b.x, v4[u].y + b.y, v4[u].z + b.z,
+                                              v4[u].w + b.w);
+                o = snake_value4<true, CONV == 1>(xv, a, i);
+            }
+            *reinterpret_cast<float4 *>(tile + r * pitch + 4 * c4) = o;
+        }
+    }
+    __syncthreads();
+    // Phase 2: row quantization from the tile, codes in fragment order.
+    {
+        constexpr int WL = HALF ? 32 : 64, RPB = 256 / WL;
+        const int ln = tid & (WL - 1);
+        for (int r = tid / WL; r < BM; r += RPB) {
+            float4 v[1];
+            const int col = ln * 4;
+            v[0] = col < C ? *reinterpret_cast<const float4 *>(tile + r * pitch + col)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            quant_row<CONV, 1, TWO, false, HALF>(v, r, C, ln, codes, -KB, rl.sx[0], rl.zx[0],
+                                                 nullptr, TWO ? codes + plane : nullptr,
+                                                 rl.sx[TWO ? 1 : 0], rl.zx[TWO ? 1 : 0],
+                                                 0x80808080u);
+        }
+    }
+    __syncthreads();
+
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(p);
+    const int jstride = p.kb_count * 1024;
+    const int wbase = nb0 * jstride;
+    v16i acc[TI][TJ], acc2[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[i][j][r] = 0;
+                acc2[i][j][r] = 0;
+            }
+    for (int kb = 0; kb < KB; ++kb) {
+        v4i b[TJ], a[PL][TI];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) b[j] = load_frag(wr, lane * 16, wbase + j * jstride + kb * 1024);
+#pragma unroll
+        for (int pl = 0; pl < PL; ++pl)
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+                a[pl][i] = *reinterpret_cast<const v4i *>(codes + pl * plane + ((i * KB + kb) * 64 + lane) * 16);
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0][i], b[j], acc[i][j], 0, 0, 0);
+                if (TWO)
+                    acc2[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[PL - 1][i], b[j], acc2[i][j], 0, 0, 0);
+            }
+    }
+    epilogue<CONV, EPI_LINEAR, TWO, TI, TJ, BM>(p, acc, acc2, cp, rl, nullptr, m0, nb0, lane);
+}
+
 }  // namespace
+
+int launch_conv1x1_snake(IroHipContext *ctx, const IroHipWeight *w, const float *hidden, int T,
+                         const float *snake_bias, const float *snake_alpha, bool two,
+                         const float *bias, const float *skip, float *output) {
+    const int C = w->K;
+    const int tj = w->Np / 128;
+    if (C % 32 || C < 64 || C > 256 || w->layout != 0 || (tj != 1 && tj != 2) || (two && tj != 1) ||
+        (((uintptr_t)hidden) & 15) || !snake_bias || !snake_alpha)
+        return 1;
+    const size_t lds = sizeof(float) * ((size_t)3 * C + (size_t)kRsBM * C) +
+                       (size_t)kRsBM * C * (two ? 2 : 1);
+    if (lds > 65536) return 1;  // two planes above 160 channels
+    GemmArgs a;
+    a.M = T;
+    a.K = C;
+    a.bias = bias;
+    a.y = output;
+    a.yin = skip;
+    a.ldy = w->N;
+    a.accumulate = 1;
+    KParams kp;
+    if (fill_kparams(ctx, w, a, kp)) return -1;
+    kp.tiles_n = 1;
+    kp.tiles_m = (T + kRsBM - 1) / kRsBM;
+    kp.tiles_per_xcd = (kp.tiles_m + 7) / 8;
+    kp.row_major = 1;
+    const dim3 grid((unsigned)(8 * kp.tiles_per_xcd)), block(256);
+    const bool half = C <= 128;
+    // floor(f / (C/4)) == umulhi(2 f, ceil(2^31 / (C/4))) for the chunk
+    // indices f < 4096 used: the rounding adds less than 2^13 / 2^32 < 4 / C.
+    const unsigned k4 = (unsigned)C / 4, magic = (unsigned)((0x80000000ull + k4 - 1) / k4);
+    prof_begin(ctx);
+#define IRO_RS(CV, TW, TJ, HF)                                                                  \
+    hipLaunchKernelGGL((conv1x1_snake_kernel<CV, TW, TJ, HF>), grid, block, lds, ctx->stream, kp, \
+                       hidden, snake_bias, snake_alpha, magic)
+    if (ctx->convention == IRO_HIP_GCC_FASTMATH) {
+        if (two) { if (half) IRO_RS(1, true, 1, true); else IRO_RS(1, true, 1, false); }
+        else if (tj == 2) { if (half) IRO_RS(1, false, 2, true); else IRO_RS(1, false, 2, false); }
+        else { if (half) IRO_RS(1, false, 1, true); else IRO_RS(1, false, 1, false); }
+    } else {
+        if (two) { if (half) IRO_RS(0, true, 1, true); else IRO_RS(0, true, 1, false); }
+        else if (tj == 2) { if (half) IRO_RS(0, false, 2, true); else IRO_RS(0, false, 2, false); }
+        else { if (half) IRO_RS(0, false, 1, true); else IRO_RS(0, false, 1, false); }
+    }
+#undef IRO_RS
+    IRO_HIP_CHECK_LAUNCH(ctx);
+    // Algorithmic work: 2 * C * N per row and plane; bytes: the rows, the
+    // skip rows and the output once, the weight once.
+    const double planes = two ? 2 : 1;
+    prof_end(ctx, PK_CONV_GEMM, 2.0 * T * w->N * C * planes,
+             4.0 * T * C + 8.0 * T * w->N + (double)w->N * C);
+    return 0;
+}
 
 // Shapes the kernel takes: C a multiple of 32 from 64 to 1024, a window of
 // at most 128 rows (stride 1, dilation <= 10).

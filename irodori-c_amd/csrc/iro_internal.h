@@ -186,6 +186,13 @@ struct ConvRows {
 };
 bool conv7_gemm_ok(const IroHipWeight *w, const ConvRows &cr);
 bool conv7_gemm_pays(const ConvRows &cr, int T_out);
+// A decoder residual unit's 1x1 with its in-place snake_bias and row
+// quantization in one kernel (C % 32 == 0, 64 <= C <= 192, two planes up to
+// 160); returns 1
+// (nothing launched) for other shapes.
+int launch_conv1x1_snake(IroHipContext *ctx, const IroHipWeight *w, const float *hidden, int T,
+                         const float *snake_bias, const float *snake_alpha, bool two,
+                         const float *bias, const float *skip, float *output);
 // iro_codec.hip: snake (reciprocal form) of x into y with each row's lo/hi.
 bool snake_rows_ok(const float *x, int C, const float *y);
 int launch_snake_rows(IroHipContext *ctx, const float *x, int T, int C, const float *alpha,

@@ -64,12 +64,16 @@ def test_snake_refuses_unaligned_channels(ctx_strict):
         ctx_strict.snake(x, 3, 6, a, x)
 
 
-# The in-place snake before the 1x1 runs inside its quantizer up to 1536
-# channels (one row per half wave up to 128, 1..6 column chunks above) and as
-# its own quotient-form pass beyond.
+# The 1x1 with its in-place snake_bias and row quantization is one kernel
+# for C % 32 == 0 up to 192 channels (two planes up to 160; half a wavefront
+# per row up to 128); above, the snake runs inside the 1x1's quantizer up to
+# 1536 channels (one row per half wave up to 128, 1..6 column chunks above)
+# and as its own quotient-form pass beyond.
 UNITS = [(96, 300, 9, True), (96, 300, 1, False), (192, 120, 3, True), (384, 50, 1, False),
          (96, 5, 9, True), (768, 24, 3, False), (96, 20000, 9, True), (4, 33, 1, True),
-         (136, 40, 3, False), (1280, 7, 1, True), (1536, 6, 1, True), (1540, 4, 3, False)]
+         (136, 40, 3, False), (1280, 7, 1, True), (1536, 6, 1, True), (1540, 4, 3, False),
+         (192, 70, 9, False), (128, 66, 1, True), (64, 65, 3, False), (160, 40, 1, True),
+         (160, 129, 3, False)]
 
 
 @pytest.mark.parametrize("C,T,dil,two", UNITS)
@@ -87,8 +91,9 @@ def test_residual_unit(ctx, oracle, C, T, dil, two):
     assert_bits_equal(out.numpy(), oracle.residual_unit(conv, x, u, two, two), "residual unit")
 
 
+@pytest.mark.parametrize("two", [True, False], ids=["two-plane", "one-plane"])
 @pytest.mark.parametrize("C,T", [(96, 50), (192, 30), (768, 9)])
-def test_residual_unit_large_hidden(ctx, oracle, C, T):
+def test_residual_unit_large_hidden(ctx, oracle, C, T, two):
     """Inputs scaled so some sines of the fused snake take sinf's |y| >= 120
     path next to ordinary ones in the same four columns."""
     conv = ctx.convention
@@ -100,8 +105,8 @@ def test_residual_unit_large_hidden(ctx, oracle, C, T):
     out = ctx.empty((T, C), np.float32)
     ctx.dacvae_residual(ctx.to_device(x), T, C, w0, ctx.to_device(u["alpha0"]),
                         ctx.to_device(u["b0"]), ctx.to_device(u["alpha1"]), 3, w1,
-                        ctx.to_device(u["b1"]), True, True, out)
-    want = oracle.residual_unit(conv, x, u, True, True)
+                        ctx.to_device(u["b1"]), two, two, out)
+    want = oracle.residual_unit(conv, x, u, two, two)
     assert_bits_equal(out.numpy(), want, "residual unit, large hidden values")
 
 
