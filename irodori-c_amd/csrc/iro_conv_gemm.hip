@@ -209,7 +209,8 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
 // dacvae.c:910-931, reciprocal form), the row quantization of the result
 // (ops.c:321-348; two-term ops.c:427-442 with RES), the GEMM and
 // output = skip + lin(q1) + bias (+ lin(q2)) -- so neither the snaked rows
-// nor their codes reach HBM.  With C <= 192 a 64-row block holds whole
+// nor their codes reach HBM.  With C <= 192 a 64-row (32-row above 128
+// channels) block holds whole
 // rows: phase 1 loads them as flat float4 chunks (every lane busy), snakes
 // them with per-channel bias, alpha and reciprocal from LDS into an LDS
 // tile; phase 2 quantizes each tile row with the row quantizer of
@@ -219,14 +220,13 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
 // against its weight fragments and the epilogue adds the skip rows.  One
 // column tile covers all N (TJ = Np / 128).  Rows past M hold zeros and are
 // never stored.
-constexpr int kRsBM = 64;
 
-template <int CONV, bool TWO, int TJ, bool HALF>
+template <int CONV, bool TWO, int TJ, bool HALF, int TI>
 __global__ __launch_bounds__(256, 2) void conv1x1_snake_kernel(KParams p, const float *__restrict__ hid,
                                                                const float *__restrict__ sbias,
                                                                const float *__restrict__ salpha,
                                                                unsigned k4_magic) {
-    constexpr int TI = 2, BM = kRsBM, PL = TWO ? 2 : 1;
+    constexpr int BM = 32 * TI, PL = TWO ? 2 : 1;
     extern __shared__ __attribute__((aligned(16))) float rs_lds[];
     __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
     const int C = p.K, KB = C / 32, pitch = C;
@@ -250,8 +250,8 @@ __global__ __launch_bounds__(256, 2) void conv1x1_snake_kernel(KParams p, const 
     }
     const ColParams<TJ> cp = load_cols<EPI_LINEAR, TJ>(p, nb0, lane, m0, BM);
     // Phase 1: float4 f = tid + 256 u of the block is row f / (C/4).
-    const int k4 = C >> 2, chunks = BM * k4;  // <= 4096
-    constexpr int U = 16;                     // 4096 / 256
+    const int k4 = C >> 2, chunks = BM * k4;  // <= 64 * 64
+    constexpr int U = 16 * TI / 2;            // BM * 64 / 256
     float4 v4[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -343,9 +343,12 @@ int launch_conv1x1_snake(IroHipContext *ctx, const IroHipWeight *w, const float 
     if (C % 32 || C < 64 || C > 256 || w->layout != 0 || (tj != 1 && tj != 2) || (two && tj != 1) ||
         (((uintptr_t)hidden) & 15) || !snake_bias || !snake_alpha)
         return 1;
-    const size_t lds = sizeof(float) * ((size_t)3 * C + (size_t)kRsBM * C) +
-                       (size_t)kRsBM * C * (two ? 2 : 1);
-    if (lds > 65536) return 1;  // two planes above 160 channels
+    // 64-row blocks up to 128 channels, 32-row blocks above (LDS for four
+    // blocks per CU).
+    const int bm = C <= 128 ? 64 : 32;
+    const size_t lds = sizeof(float) * ((size_t)3 * C + (size_t)bm * C) +
+                       (size_t)bm * C * (two ? 2 : 1);
+    if (lds > 65536) return 1;
     GemmArgs a;
     a.M = T;
     a.K = C;
@@ -357,7 +360,7 @@ int launch_conv1x1_snake(IroHipContext *ctx, const IroHipWeight *w, const float 
     KParams kp;
     if (fill_kparams(ctx, w, a, kp)) return -1;
     kp.tiles_n = 1;
-    kp.tiles_m = (T + kRsBM - 1) / kRsBM;
+    kp.tiles_m = (T + bm - 1) / bm;
     kp.tiles_per_xcd = (kp.tiles_m + 7) / 8;
     kp.row_major = 1;
     const dim3 grid((unsigned)(8 * kp.tiles_per_xcd)), block(256);
@@ -367,8 +370,14 @@ int launch_conv1x1_snake(IroHipContext *ctx, const IroHipWeight *w, const float 
     const unsigned k4 = (unsigned)C / 4, magic = (unsigned)((0x80000000ull + k4 - 1) / k4);
     prof_begin(ctx);
 #define IRO_RS(CV, TW, TJ, HF)                                                                  \
-    hipLaunchKernelGGL((conv1x1_snake_kernel<CV, TW, TJ, HF>), grid, block, lds, ctx->stream, kp, \
-                       hidden, snake_bias, snake_alpha, magic)
+    do {                                                                                       \
+        if (bm == 64)                                                                          \
+            hipLaunchKernelGGL((conv1x1_snake_kernel<CV, TW, TJ, HF, 2>), grid, block, lds,     \
+                               ctx->stream, kp, hidden, snake_bias, snake_alpha, magic);        \
+        else                                                                                   \
+            hipLaunchKernelGGL((conv1x1_snake_kernel<CV, TW, TJ, HF, 1>), grid, block, lds,     \
+                               ctx->stream, kp, hidden, snake_bias, snake_alpha, magic);        \
+    } while (0)
     if (ctx->convention == IRO_HIP_GCC_FASTMATH) {
         if (two) { if (half) IRO_RS(1, true, 1, true); else IRO_RS(1, true, 1, false); }
         else if (tj == 2) { if (half) IRO_RS(1, false, 2, true); else IRO_RS(1, false, 2, false); }
