@@ -153,3 +153,27 @@ def test_conv1x1_skip(ctx, oracle, T, C, residual, in_place):
     assert_bits_equal(out.numpy(), want, "conv1x1 onto skip")
     if not in_place:
         assert_bits_equal(sd.numpy(), skip, "skip rows left unchanged")
+
+
+def test_convtranspose_long_short_k_tiles(ctx):
+    """A long ConvTranspose with a short reduction (the decoder's last
+    upsample: k = 192) takes 128 x 128 tiles of the chunked GEMM kernel;
+    its output equals the 64 x 256 tile path's, which the oracle tests
+    above pin."""
+    T, Ci, Co, k, st, pad, opad = 140000, 192, 96, 4, 2, 1, 0
+    x = gauss(41, (T, Ci))
+    w_export = gauss(42, (Ci, k * Co), 0.02)
+    b = gauss(43, (Co,), 0.01)
+    W = ctx.weight(ctx.to_device(w_export), k * Co, Ci, transposed=True)
+    xd, bd = ctx.to_device(x), ctx.to_device(b)
+    outs = []
+    for tile in ((0, 0), (2, 2)):
+        ctx.set_gemm_tile(*tile)
+        try:
+            To = (T - 1) * st - 2 * pad + k + opad
+            yd = ctx.empty((To, Co), np.float32)
+            ctx.convtranspose1d(xd, T, Ci, W, Co, k, st, pad, opad, bd, 0, yd)
+            outs.append(yd.numpy())
+        finally:
+            ctx.set_gemm_tile(0, 0)
+    assert_bits_equal(outs[0], outs[1], "convtranspose output, 128x128 vs 64x256 tiles")
