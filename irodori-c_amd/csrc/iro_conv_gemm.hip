@@ -209,8 +209,7 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
 // dacvae.c:910-931, reciprocal form), the row quantization of the result
 // (ops.c:321-348; two-term ops.c:427-442 with RES), the GEMM and
 // output = skip + lin(q1) + bias (+ lin(q2)) -- so neither the snaked rows
-// nor their codes reach HBM.  With C <= 192 a 64-row (32-row above 128
-// channels) block holds whole
+// nor their codes reach HBM.  With C <= 192 a 32-row block holds whole
 // rows: phase 1 loads them as flat float4 chunks (every lane busy), snakes
 // them with per-channel bias, alpha and reciprocal from LDS into an LDS
 // tile; phase 2 quantizes each tile row with the row quantizer of
@@ -222,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
 // never stored.
 
 template <int CONV, bool TWO, int TJ, bool HALF, int TI>
-__global__ __launch_bounds__(256, 2) void conv1x1_snake_kernel(KParams p, const float *__restrict__ hid,
+__global__ __launch_bounds__(256, TI == 1 ? 4 : 2) void conv1x1_snake_kernel(KParams p, const float *__restrict__ hid,
                                                                const float *__restrict__ sbias,
                                                                const float *__restrict__ salpha,
                                                                unsigned k4_magic) {
@@ -250,36 +249,37 @@ __global__ __launch_bounds__(256, 2) void conv1x1_snake_kernel(KParams p, const 
     }
     const ColParams<TJ> cp = load_cols<EPI_LINEAR, TJ>(p, nb0, lane, m0, BM);
     // Phase 1: float4 f = tid + 256 u of the block is row f / (C/4).
+    // The raw rows go to the tile first, eight float4 loads per thread in
+    // flight at a time, and are snaked there in place by a loop that is not
+    // unrolled (one copy of the snake's code).  Rows past M stay zero.
     const int k4 = C >> 2, chunks = BM * k4;  // <= 64 * 64
-    constexpr int U = 16 * TI / 2;            // BM * 64 / 256
-    float4 v4[U];
+    constexpr int G = 8;
+    for (int base = 0; base < chunks; base += 256 * G) {
+        float4 v4[G];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int f = tid + 256 * u;
-        v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (f < chunks) {
-            const int r = __umulhi(2u * f, k4_magic);
-            if (m0 + r < p.M)
+        for (int u = 0; u < G; ++u) {
+            const int f = base + tid + 256 * u;
+            v4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (f < chunks && m0 + (int)__umulhi(2u * f, k4_magic) < p.M)
                 v4[u] = *reinterpret_cast<const float4 *>(hid + (size_t)m0 * C + 4 * f);
         }
-    }
-    __syncthreads();  // the staged parameters
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int f = tid + 256 * u;
-        if (f < chunks) {
-            const int r = __umulhi(2u * f, k4_magic), c4 = f - r * k4;
-            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (m0 + r < p.M) {
-                const float4 b = *reinterpret_cast<const float4 *>(s_b + 4 * c4);
-                const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
-                const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
-                const float4 xv = make_float4(v4[u].x + b.x, v4[u].y + b.y, v4[u].z + b.z,
-                                              v4[u].w + b.w);
-                o = snake_value4<true, CONV == 1>(xv, a, i);
-            }
-            *reinterpret_cast<float4 *>(tile + r * pitch + 4 * c4) = o;
+        for (int u = 0; u < G; ++u) {
+            const int f = base + tid + 256 * u;
+            if (f < chunks) *reinterpret_cast<float4 *>(tile + 4 * f) = v4[u];
         }
+    }
+    __syncthreads();  // the staged parameters and rows
+    const int live = (p.M - m0 < BM ? p.M - m0 : BM) * k4;  // chunks of rows below M
+#pragma unroll 1
+    for (int f = tid; f < live; f += 256) {
+        const int c4 = f - (int)__umulhi(2u * f, k4_magic) * k4;
+        const float4 v = *reinterpret_cast<const float4 *>(tile + 4 * f);
+        const float4 b = *reinterpret_cast<const float4 *>(s_b + 4 * c4);
+        const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
+        const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
+        const float4 xv = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+        *reinterpret_cast<float4 *>(tile + 4 * f) = snake_value4<true, CONV == 1>(xv, a, i);
     }
     __syncthreads();
     // Phase 2: row quantization from the tile, codes in fragment order.
@@ -343,9 +343,10 @@ int launch_conv1x1_snake(IroHipContext *ctx, const IroHipWeight *w, const float 
     if (C % 32 || C < 64 || C > 256 || w->layout != 0 || (tj != 1 && tj != 2) || (two && tj != 1) ||
         (((uintptr_t)hidden) & 15) || !snake_bias || !snake_alpha)
         return 1;
-    // 64-row blocks up to 128 channels, 32-row blocks above (LDS for four
-    // blocks per CU).
-    const int bm = C <= 128 ? 64 : 32;
+    // 32-row blocks: four waves per SIMD (128 registers) and four blocks
+    // per CU in LDS (stage-3 two-plane 1x1 268 -> 252 us against 64-row
+    // blocks, whose two-plane epilogue needs 166 registers).
+    const int bm = 32;
     const size_t lds = sizeof(float) * ((size_t)3 * C + (size_t)bm * C) +
                        (size_t)bm * C * (two ? 2 : 1);
     if (lds > 65536) return 1;
