@@ -40,11 +40,20 @@ constexpr int kKT = 128;    // keys per score block
 constexpr int kPitch = 68;  // LDS row pitch (floats) of 64-wide tiles
 constexpr int kPVK = 64;    // keys per PV chunk
 
-// The source of joined key j of batch b, head column h*64.
+// The source of joined key j < S + nvalid[b] of batch b, head column h*64.
+// Branch-free, so the callers' row loads are not split by a divergent branch
+// (which made the compiler wait for and spill each one): both candidate
+// rows are formed and one selected, and the context row index is read at a
+// clamped position that is always inside rows[b*C .. b*C + C) (C >= 1 and
+// j - S < nvalid[b] <= C).
 __device__ __forceinline__ const float *key_row(const float *self, const float *ctxr,
                                                 const int *rows, int b, int S, int C, int D,
                                                 int j) {
-    return j < S ? self + ((size_t)b * S + j) * D : ctxr + (size_t)rows[b * C + (j - S)] * D;
+    const int jc = j - S;
+    const int r = rows[b * C + (jc > 0 ? jc : 0)];
+    const float *ps = self + ((size_t)b * S + (j < S ? j : 0)) * D;
+    const float *pc = ctxr + (size_t)r * D;
+    return j < S ? ps : pc;
 }
 
 __global__ __launch_bounds__(256) void attn_scores_kernel(
@@ -217,8 +226,17 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     // Staging: P element (query (tid >> 6) + 4 i, key tid & 63); V float4s
     // tid + 256 i of the chunk's 64 x 64 tile.
     const int kj = tid & 63, qi0 = tid >> 6;
+    // The staged V rows are four named registers, not an array: as an array
+    // held across the chunk loop the compiler kept them in scratch and waited
+    // for each prefetch at once to store it there.
     float pr[NP];
-    float4 vr[4];
+    float4 vr0, vr1, vr2, vr3;
+    auto vload = [&](int kc, int i) {
+        const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
+        const int jv = kc + r < J ? kc + r : J - 1;
+        return *reinterpret_cast<const float4 *>(key_row(v, cv, rows, b, S, C, D, jv) + h * 64 +
+                                                 c4);
+    };
     auto load = [&](int kc) {
         const int j = kc + kj < J ? kc + kj : J - 1;
 #pragma unroll
@@ -226,13 +244,10 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
             const int s = q0 + qi0 + 4 * i < S ? q0 + qi0 + 4 * i : S - 1;
             pr[i] = sc[((size_t)bh * S + s) * Jp + j];
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
-            const int jv = kc + r < J ? kc + r : J - 1;
-            vr[i] = *reinterpret_cast<const float4 *>(key_row(v, cv, rows, b, S, C, D, jv) +
-                                                      h * 64 + c4);
-        }
+        vr0 = vload(kc, 0);
+        vr1 = vload(kc, 1);
+        vr2 = vload(kc, 2);
+        vr3 = vload(kc, 3);
     };
     const int tq = tid >> 4, tn = tid & 15;
     float acc[QPT][4];
@@ -245,11 +260,14 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(
     for (int kc = 0; kc < J; kc += kPVK) {
 #pragma unroll
         for (int i = 0; i < NP; ++i) Ps[kj * PP + qi0 + 4 * i] = pr[i] / sum_s[qi0 + 4 * i];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        auto vstore = [&](int i, const float4 &x) {
             const int idx = tid + 256 * i, r = idx >> 4, c4 = (idx & 15) * 4;
-            *reinterpret_cast<float4 *>(&Vs[r * kPitch + c4]) = vr[i];
-        }
+            *reinterpret_cast<float4 *>(&Vs[r * kPitch + c4]) = x;
+        };
+        vstore(0, vr0);
+        vstore(1, vr1);
+        vstore(2, vr2);
+        vstore(3, vr3);
         __syncthreads();
         if (kc + kPVK < J) load(kc + kPVK);
         auto step = [&](int kk) {
