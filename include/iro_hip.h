@@ -65,9 +65,9 @@ void *iro_hip_stream(IroHipContext *ctx);
    -5 rows per whole-tile block (0 chosen per GEMM, 64, 128),
    -6 kernel-7 convolution codes (2, the default: the GEMM codes the input
       rows itself from their ranges where that is measured faster -- 64..256
-      channels in multiples of 32, or up to 1024 on inputs of 65536 rows or
-      more -- else as 1; 1 window ranges and im2col codes in one pass; 0
-      two passes),
+      channels in multiples of 32, 384 on inputs of 16384 rows or more, up
+      to 1024 on inputs of 65536 rows or more -- else as 1; 3 the same wherever the kernel takes the shape; 1
+      window ranges and im2col codes in one pass; 0 two passes),
    -7 SwiGLU hidden state (0, the default: stored in fp32 and quantized by
       a row quantization launch; 1: the W1/W3 kernel quantizes it for W2
       itself, its blocks exchanging row ranges through device memory, when

@@ -387,9 +387,10 @@ int iro_hip_set_gemm_tile(IroHipContext *ctx, int ti, int tj) {
         ctx->gemm_lds = tj;
         return 0;
     }
-    if (ti == -6) {  // tj: kernel-7 convolutions, 2 the GEMM codes its rows (default),
-                     // 1 a one-pass im2col, 0 the two-pass im2col
-        if (tj < 0 || tj > 2) return set_error(ctx, "set_gemm_tile: conv mode 0, 1 or 2");
+    if (ti == -6) {  // tj: kernel-7 convolutions, 2 the GEMM codes its rows where it
+                     // pays (default), 3 wherever it takes the shape, 1 a one-pass
+                     // im2col, 0 the two-pass im2col
+        if (tj < 0 || tj > 3) return set_error(ctx, "set_gemm_tile: conv mode 0..3");
         ctx->conv_mode = tj;
         return 0;
     }
@@ -766,7 +767,8 @@ int conv1d_int8(IroHipContext *ctx, const float *input, int T, int C, const IroH
     // Kernel 7: the GEMM codes the input rows itself from their ranges,
     // which the snake pass (if any) produces with its output rows.
     ConvRows cr{snake_alpha ? snake_out : input, nullptr, nullptr, T, C, stride, dilation, padding};
-    if (kernel == 7 && ctx->conv_mode == 2 && conv7_gemm_ok(w, cr) && conv7_gemm_pays(cr, T_out) &&
+    if (kernel == 7 && ctx->conv_mode >= 2 && conv7_gemm_ok(w, cr) &&
+        (ctx->conv_mode == 3 || conv7_gemm_pays(cr, T_out)) &&
         (!snake_alpha || snake_rows_ok(input, C, snake_out))) {
         if (ws.commit()) return -1;
         float *lo = ws.at<float>(olo), *hi = ws.at<float>(ohi);

@@ -408,12 +408,15 @@ bool conv7_gemm_ok(const IroHipWeight *w, const ConvRows &cr) {
 
 // Where it beats the im2col path (which writes the codes and reads them
 // back): up to 256 channels always (C = 96, two planes: 286 against 579 us
-// at T = 480000; C = 192: 224 against 373 us at T = 240000), wider rows on
-// long inputs only (C = 384, T = 120000: 347 against 489 us; C = 768,
-// T = 60000: 473 against 542 us), where the im2col traffic outweighs the
-// coding work each column tile repeats; on short ones it loses (C = 512,
-// T = 24000: 100 against 94 us; C = 1024, T = 6000: 77 against 51 us).
-bool conv7_gemm_pays(const ConvRows &cr, int T_out) { return cr.C <= 256 || T_out >= 65536; }
+// at T = 480000; C = 192: 224 against 373 us at T = 240000), 384 channels
+// from 16384 steps (T = 30000: 91 against 105 us), wider rows on long
+// inputs only (C = 768, T = 60000: 473 against 542 us), where the im2col
+// traffic outweighs the coding work each column tile repeats; on short ones
+// it loses (C = 768, T = 3000: 62 against 54 us; C = 512, T = 24000: 100
+// against 94 us; C = 1024, T = 6000: 77 against 51 us).
+bool conv7_gemm_pays(const ConvRows &cr, int T_out) {
+    return cr.C <= 256 || (cr.C <= 384 && T_out >= 16384) || T_out >= 65536;
+}
 
 int launch_conv7_gemm(IroHipContext *ctx, const IroHipWeight *w, const ConvRows &cr, int T_out,
                       bool two, const float *bias, float *y) {

@@ -66,8 +66,9 @@ struct IroHipContext {
     int gemm_spb = 0;     // column slabs per whole-tile block (0: chosen per GEMM)
     int gemm_lds = 0;     // LDS-pipelined GEMM: 0 shape chosen per GEMM, -1 off, > 0 forced shape
     int gemm_wt_rows = 0; // rows per whole-tile block: 0 chosen per GEMM, 64 or 128
-    int conv_mode = 2;    // kernel-7 convolutions: 2 the GEMM codes its own rows,
-                          // 1 a one-pass im2col, 0 the two-pass im2col
+    int conv_mode = 2;    // kernel-7 convolutions: 2 the GEMM codes its own rows where
+                          // that pays, 3 wherever it can, 1 a one-pass im2col, 0 the
+                          // two-pass im2col
     int conv_cols = 0;    // output channels per block of that GEMM: 0 chosen, 128, 256
     int band_quant = 0;   // W1/W3 kernel quantizes the SwiGLU hidden state itself (opt-in)
     // band exchange state of that kernel: zero between launches

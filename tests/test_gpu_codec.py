@@ -110,6 +110,32 @@ def test_residual_unit_large_hidden(ctx, oracle, C, T, two):
     assert_bits_equal(out.numpy(), want, "residual unit, large hidden values")
 
 
+def test_residual_unit_long_384_modes_agree(ctx):
+    """At 384 channels on 16384 steps or more the unit's Conv7 takes the
+    snake pass with row ranges and the GEMM that codes its own rows; its
+    output equals the im2col form's (conv mode 1), which the oracle tests
+    above pin at shorter lengths."""
+    C, T, dil = 384, 16500, 3
+    rng = np.random.default_rng(C + T)
+    u = cp.residual_unit(rng, C, dil)
+    x = rng.standard_normal((T, C), dtype=np.float32)
+    w0 = ctx.weight(ctx.to_device(u["w0"]), C, 7 * C)
+    w1 = ctx.weight(ctx.to_device(u["w1"]), C, C)
+    xd = ctx.to_device(x)
+    outs = []
+    for mode in (2, 1):
+        ctx.set_gemm_tile(-6, mode)
+        try:
+            out = ctx.empty((T, C), np.float32)
+            ctx.dacvae_residual(xd, T, C, w0, ctx.to_device(u["alpha0"]), ctx.to_device(u["b0"]),
+                                ctx.to_device(u["alpha1"]), dil, w1, ctx.to_device(u["b1"]),
+                                False, False, out)
+            outs.append(out.numpy())
+        finally:
+            ctx.set_gemm_tile(-6, 2)
+    assert_bits_equal(outs[0], outs[1], "residual unit, GEMM codes vs im2col")
+
+
 def _decoder(ctx, seed):
     import iro_hip
     p = cp.decoder(seed)

@@ -75,11 +75,13 @@ def test_conv7_modes_agree(ctx, oracle, mode, cols, residual):
     assert_bits_equal(got, want, "conv output")
 
 
-def test_conv7_gemm_codes_wide_long(ctx):
+@pytest.mark.parametrize("T,C,N", [(65600, 320, 256), (16500, 384, 384)],
+                         ids=["C320-T65600-256cols", "C384-T16500"])
+def test_conv7_gemm_codes_wide_long(ctx, T, C, N):
     """Above 256 channels the GEMM that codes its own rows runs on long
-    inputs only (here 320 channels, 65600 steps, 64 x 256 tiles); its output
-    equals the one-pass im2col form's, which the oracle tests above pin."""
-    T, C, N = 65600, 320, 256
+    inputs only (384 channels from 16384 steps, wider from 65536); its
+    output equals the one-pass im2col form's, which the oracle tests above
+    pin."""
     x = gauss(31, (T, C))
     x[100:140] = 0.0
     w = gauss(32, (N, 7 * C), 0.02)
