@@ -209,10 +209,12 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
 // dacvae.c:910-931, reciprocal form), the row quantization of the result
 // (ops.c:321-348; two-term ops.c:427-442 with RES), the GEMM and
 // output = skip + lin(q1) + bias (+ lin(q2)) -- so neither the snaked rows
-// nor their codes reach HBM.  With C <= 192 a 32-row block holds whole
-// rows: phase 1 loads them as flat float4 chunks (every lane busy), snakes
-// them with per-channel bias, alpha and reciprocal from LDS into an LDS
-// tile; phase 2 quantizes each tile row with the row quantizer of
+// nor their codes reach HBM.  With C <= 192 a block of 32 * TI rows holds
+// whole rows (LDS: the tile, the codes and the per-channel parameters within
+// 64 KiB): phase 1 copies them into an LDS tile as flat float4 chunks (every
+// lane busy) and snakes them there in place with per-channel bias, alpha
+// and reciprocal from LDS; phase 2 quantizes each tile row with the row
+// quantizer of
 // iro_quant_row.h (half a wavefront per row up to 128 channels), writing
 // the codes into LDS in MFMA fragment order and the row parameters where the
 // epilogue reads them; then each wave runs the C/32 k blocks of MFMAs
