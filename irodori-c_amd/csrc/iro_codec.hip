@@ -35,14 +35,16 @@ __global__ __launch_bounds__(256) void snake_kernel(const float *__restrict__ x,
                                                     long long n4, const float *__restrict__ bias,
                                                     const float *__restrict__ alpha, float *y) {
     __shared__ float s_alpha[INV ? kSnakeMaxChannels : 1], s_inv[INV ? kSnakeMaxChannels : 1];
+    __shared__ uint32_t s_pio4[24];
+    stage_invpio4(s_pio4, threadIdx.x);
     if (INV) {
         for (int c = threadIdx.x; c < C; c += 256) {
             const float a = alpha[c];
             s_alpha[c] = a;
             s_inv[c] = snake_inv(a);
         }
-        __syncthreads();
     }
+    __syncthreads();
     for (long long i = blockIdx.x * 256ll + threadIdx.x; i < n4; i += (long long)gridDim.x * 256) {
         const long long e = 4 * i;
         const int c = (int)(e % C);
@@ -57,7 +59,7 @@ __global__ __launch_bounds__(256) void snake_kernel(const float *__restrict__ x,
         const float4 a = make_float4(ap[c], ap[c + 1], ap[c + 2], ap[c + 3]);
         const float4 inv = INV ? make_float4(s_inv[c], s_inv[c + 1], s_inv[c + 2], s_inv[c + 3])
                                : make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4 *>(y + e) = snake_value4<INV, FMA>(v, a, inv);
+        *reinterpret_cast<float4 *>(y + e) = snake_value4<INV, FMA>(v, a, inv, s_pio4);
     }
 }
 
@@ -141,7 +143,9 @@ __global__ __launch_bounds__(256) void snake_rows_kernel(const float *__restrict
                                                          float *__restrict__ row_lo,
                                                          float *__restrict__ row_hi) {
     extern __shared__ __attribute__((aligned(16))) float snake_rows_lds[];
+    __shared__ uint32_t s_pio4[24];
     float *s_a = snake_rows_lds, *s_i = s_a + C, *tile = s_i + C;
+    stage_invpio4(s_pio4, threadIdx.x);
     for (int c = threadIdx.x; c < C; c += 256) {
         const float a = alpha[c];
         s_a[c] = a;
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(256) void snake_rows_kernel(const float *__restrict
             const int c4 = f - (int)__umulhi(2u * f, k4_magic) * k4;
             const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
             const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
-            const float4 o = snake_value4<true, FMA>(v4[j], a, i);
+            const float4 o = snake_value4<true, FMA>(v4[j], a, i, s_pio4);
             *reinterpret_cast<float4 *>(y + (size_t)row0 * C + 4 * f) = o;
             *reinterpret_cast<float4 *>(tile + 4 * f) = o;
         }

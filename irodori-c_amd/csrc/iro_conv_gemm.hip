@@ -229,6 +229,7 @@ __global__ __launch_bounds__(256, TI == 1 ? 4 : 2) void conv1x1_snake_kernel(KPa
                                                                unsigned k4_magic) {
     constexpr int BM = 32 * TI, PL = TWO ? 2 : 1;
     extern __shared__ __attribute__((aligned(16))) float rs_lds[];
+    __shared__ uint32_t s_pio4[24];
     __shared__ __attribute__((aligned(16))) RowLds<BM, TWO> rl;
     const int C = p.K, KB = C / 32, pitch = C;
     float *s_b = rs_lds, *s_a = s_b + C, *s_i = s_a + C, *tile = s_i + C;
@@ -243,6 +244,7 @@ __global__ __launch_bounds__(256, TI == 1 ? 4 : 2) void conv1x1_snake_kernel(KPa
     const int m0 = by * BM;
     const int nb0 = bx * 4 * TJ + wave * TJ;
 
+    stage_invpio4(s_pio4, tid);
     for (int c = tid; c < C; c += 256) {
         const float a = salpha[c];
         s_b[c] = sbias[c];
@@ -281,7 +283,7 @@ __global__ __launch_bounds__(256, TI == 1 ? 4 : 2) void conv1x1_snake_kernel(KPa
         const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
         const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
         const float4 xv = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
-        *reinterpret_cast<float4 *>(tile + 4 * f) = snake_value4<true, CONV == 1>(xv, a, i);
+        *reinterpret_cast<float4 *>(tile + 4 * f) = snake_value4<true, CONV == 1>(xv, a, i, s_pio4);
     }
     __syncthreads();
     // Phase 2: row quantization from the tile, codes in fragment order.

@@ -78,7 +78,9 @@ __global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict_
                                                         int32_t *__restrict__ z2, uint32_t sflip) {
     static_assert(!HALF || CH == 1, "a half-wave row holds at most 128 columns");
     extern __shared__ __attribute__((aligned(16))) float snake_lds[];
+    __shared__ uint32_t s_pio4[24];
     float *s_b = snake_lds, *s_a = s_b + K, *s_i = s_a + K, *tile = s_i + K;
+    stage_invpio4(s_pio4, threadIdx.x);
     for (int c = threadIdx.x; c < K; c += 256) {
         const float a = alpha[c];
         s_b[c] = bias[c];
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict_
             const float4 xv = make_float4(v4[j].x + b.x, v4[j].y + b.y, v4[j].z + b.z,
                                           v4[j].w + b.w);
             *reinterpret_cast<float4 *>(tile + r * K + 4 * c4) =
-                snake_value4<true, CONV == 1>(xv, a, i);
+                snake_value4<true, CONV == 1>(xv, a, i, s_pio4);
         }
     }
     __syncthreads();

@@ -83,9 +83,11 @@ __device__ __forceinline__ SinCosArg sincosf_reduce_small(float y) {
 // The large reduction, for finite |y| >= 120 (other y give some SinCosArg
 // that sincosf_finish replaces): a 32 x 96-bit product of the mantissa with
 // 4/pi gives n and a 2.62 fixed-point remainder, scaled by pi * 2^-62.
-__device__ __forceinline__ SinCosArg sincosf_reduce_large(float y) {
+// invpio4: kInvPio4 or a copy of it (in LDS, where a kernel stages one).
+__device__ __forceinline__ SinCosArg sincosf_reduce_large(float y,
+                                                          const uint32_t *invpio4 = kInvPio4) {
     const uint32_t yi = __float_as_uint(y);
-    const uint32_t *arr = &kInvPio4[(yi >> 26) & 15];
+    const uint32_t *arr = &invpio4[(yi >> 26) & 15];
     const int shift = (yi >> 23) & 7;
     uint32_t xi = ((yi & 0xffffff) | 0x800000) << shift;
     uint64_t res0 = (uint32_t)(xi * arr[0]);

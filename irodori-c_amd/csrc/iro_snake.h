@@ -27,19 +27,28 @@ __device__ __forceinline__ float snake_value(float xv, float a, float inv) {
     return snake_finish<INV, FMA>(xv, sinf_glibc(a * xv), a, inv);
 }
 
+// A kernel's LDS copy of kInvPio4 for the large reduction (a per-lane
+// table read then comes from LDS): threads 0..23 fill it, and a barrier must
+// follow before snake_value4 reads it.
+__device__ __forceinline__ void stage_invpio4(uint32_t *dst, int tid) {
+    if (tid < 24) dst[tid] = kInvPio4[tid];
+}
+
 // snake_value of four elements: sinf's fast reduction, branch-free, on all
 // four (a large y replaced by 0 there), the large reduction for the elements
 // with |y| >= 120 only, then one polynomial each, so the evaluations
 // interleave and a wave holding both kinds runs the polynomial once.
 template <bool INV, bool FMA>
-__device__ __forceinline__ float4 snake_value4(float4 xv, float4 a, float4 inv) {
+__device__ __forceinline__ float4 snake_value4(float4 xv, float4 a, float4 inv,
+                                               const uint32_t *invpio4 = kInvPio4) {
     const float y[4] = {a.x * xv.x, a.y * xv.y, a.z * xv.z, a.w * xv.w};
     SinCosArg r[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) r[k] = sincosf_reduce_small(sincosf_is_small(y[k]) ? y[k] : 0.0f);
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-        if (__builtin_expect(!sincosf_is_small(y[k]), 0)) r[k] = sincosf_reduce_large(y[k]);
+        if (__builtin_expect(!sincosf_is_small(y[k]), 0))
+            r[k] = sincosf_reduce_large(y[k], invpio4);
     return make_float4(snake_finish<INV, FMA>(xv.x, sincosf_finish(y[0], r[0], 0), a.x, inv.x),
                        snake_finish<INV, FMA>(xv.y, sincosf_finish(y[1], r[1], 0), a.y, inv.y),
                        snake_finish<INV, FMA>(xv.z, sincosf_finish(y[2], r[2], 0), a.z, inv.z),
