@@ -837,8 +837,20 @@ int iro_hip_convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_i
                                  const IroHipWeight *w, int C_out, int kernel, int stride,
                                  int padding, int output_padding, const float *bias,
                                  int residual, float *output, int *t_out) {
+    return convtranspose1d_int8(ctx, input, T_in, C_in, w, C_out, kernel, stride, padding,
+                                output_padding, bias, residual, output, t_out, nullptr, nullptr);
+}
+
+}  // extern "C"
+
+namespace iro {
+
+int convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_in, int C_in,
+                         const IroHipWeight *w, int C_out, int kernel, int stride, int padding,
+                         int output_padding, const float *bias, int residual, float *output,
+                         int *t_out, const float *snake_alpha, float *snake_out) {
     if (!ctx || !input || !w || !output || T_in <= 0 || C_in <= 0 || C_out <= 0 || kernel <= 0 ||
-        stride <= 0 || padding < 0 || output_padding < 0)
+        stride <= 0 || padding < 0 || output_padding < 0 || (snake_alpha && !snake_out))
         return set_error(ctx, "convtranspose1d_int8: invalid arguments");
     // dacvae.c:350-358
     const long long To = (long long)(T_in - 1) * stride - 2LL * padding + kernel + output_padding;
@@ -856,9 +868,24 @@ int iro_hip_convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_i
     if (ws.commit()) return -1;
     const ActBufs b = act_at(ws, C_in, residual != 0, off);
     float *expanded = ws.at<float>(oexp);
-    if (launch_quant_rows(ctx, input, T_in, C_in, C_in, b.q1, b.ld, b.s1, b.z1, nullptr, b.q2,
-                          b.s2, b.z2, true))
-        return -1;
+    // The snake of the input rows (if any) inside the quantizer where it
+    // takes the shape; else as its own pass into snake_out.
+    int qrc = 1;
+    if (snake_alpha && C_in <= 1536) {
+        const SnakePre sp{nullptr, snake_alpha};
+        qrc = launch_quant_rows(ctx, input, T_in, C_in, C_in, b.q1, b.ld, b.s1, b.z1, nullptr,
+                                b.q2, b.s2, b.z2, true, &sp);
+        if (qrc < 0) return -1;
+    }
+    if (qrc == 1) {
+        if (snake_alpha) {
+            if (iro_hip_snake(ctx, input, T_in, C_in, snake_alpha, snake_out)) return -1;
+            input = snake_out;
+        }
+        if (launch_quant_rows(ctx, input, T_in, C_in, C_in, b.q1, b.ld, b.s1, b.z1, nullptr, b.q2,
+                              b.s2, b.z2, true))
+            return -1;
+    }
     GemmArgs a = gemm_args(b, T_in, C_in);
     a.y = expanded;
     a.ldy = (int)ncols;
@@ -866,6 +893,10 @@ int iro_hip_convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_i
     return launch_convt_gather(ctx, expanded, T_in, C_out, kernel, stride, padding, T_out, bias,
                                output);
 }
+
+}  // namespace iro
+
+extern "C" {
 
 // ---- backend queries -------------------------------------------------------------------
 

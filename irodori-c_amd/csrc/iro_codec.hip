@@ -511,13 +511,14 @@ int iro_hip_dacvae_decode_int8(IroHipDACVAE *d, const float *state, int frames,
     for (int s = 0; s < IRO_HIP_DACVAE_STAGES; ++s) {
         const IroHipDACVAEStageF32 &st = d->f32.stage[s];
         // dacvae.c:1255-1264 (convtranspose1d_forward_impl, dacvae.c:736-748):
-        // snake(alpha) on the input rows, then the int8 upsample with its bias.
+        // snake(alpha) on the input rows (inside the upsample's row quantizer,
+        // so the snaked rows never reach HBM), then the int8 upsample with its
+        // bias.
         int t_up = 0;
-        if (iro_hip_snake(ctx, cur, tt, st.c_in, st.alpha, act) ||
-            iro_hip_convtranspose1d_int8(ctx, act, tt, st.c_in, d->upsample[s], st.c_out,
-                                         st.kernel, st.stride, st.padding, st.output_padding,
-                                         st.up_bias, (residual_mask & GROUP_UPSAMPLE) != 0, spare,
-                                         &t_up))
+        if (convtranspose1d_int8(ctx, cur, tt, st.c_in, d->upsample[s], st.c_out, st.kernel,
+                                 st.stride, st.padding, st.output_padding, st.up_bias,
+                                 (residual_mask & GROUP_UPSAMPLE) != 0, spare, &t_up, st.alpha,
+                                 act))
             return -1;
         tt = t_up;
         std::swap(cur, spare);

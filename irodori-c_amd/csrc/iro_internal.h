@@ -205,13 +205,21 @@ int conv1d_int8(IroHipContext *ctx, const float *input, int T, int C, const IroH
                 int kernel, int stride, int dilation, int padding, const float *bias,
                 int residual, float *output, int *t_out, const float *snake_alpha,
                 float *snake_out);
+// iro_hip_convtranspose1d_int8 likewise: with snake_alpha the input rows'
+// snake (iro_snake_forward, dacvae.c:830-857) runs inside the row
+// quantizer where it takes the shape, else into snake_out first.
+int convtranspose1d_int8(IroHipContext *ctx, const float *input, int T_in, int C_in,
+                         const IroHipWeight *w, int C_out, int kernel, int stride, int padding,
+                         int output_padding, const float *bias, int residual, float *output,
+                         int *t_out, const float *snake_alpha, float *snake_out);
 // Returns 1 (nothing launched) when conv7_gemm_ok refuses the shape.
 int launch_conv7_gemm(IroHipContext *ctx, const IroHipWeight *w, const ConvRows &cr, int T_out,
                       bool two, const float *bias, float *y);
 
-// Snake applied to each element before it is quantized: x + bias[c], then
-// the reciprocal-form snake with alpha[c] (the in-place snake_bias of a
-// residual unit, at most 1536 channels).
+// Snake applied to each element before it is quantized: x + bias[c] (x as
+// it is when bias is null), then the reciprocal-form snake with alpha[c]
+// (the in-place snake_bias of a residual unit, or the snake before an
+// upsample; at most 1536 channels).
 struct SnakePre {
     const float *bias;
     const float *alpha;

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void quant_rows_half(const float *__restrict__
 // with per-channel bias, alpha and reciprocal staged in LDS, and writes the
 // tile [R, K] to LDS.  Phase 2 quantizes the tile's rows as quant_rows_vec
 // (HALF: quant_rows_half) does.  Dynamic LDS: 3 K + R K floats.
-template <int CONV, int CH, bool RES, bool HALF>
+template <int CONV, int CH, bool RES, bool HALF, bool BIAS>
 __global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict__ x, int M, int K,
                                                         int ldx, int R, unsigned k4_magic,
                                                         const float *__restrict__ bias,
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict_
     stage_invpio4(s_pio4, threadIdx.x);
     for (int c = threadIdx.x; c < K; c += 256) {
         const float a = alpha[c];
-        s_b[c] = bias[c];
+        s_b[c] = BIAS ? bias[c] : 0.0f;
         s_a[c] = a;
         s_i[c] = snake_inv(a);
     }
@@ -109,8 +109,11 @@ __global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict_
             const float4 b = *reinterpret_cast<const float4 *>(s_b + 4 * c4);
             const float4 a = *reinterpret_cast<const float4 *>(s_a + 4 * c4);
             const float4 i = *reinterpret_cast<const float4 *>(s_i + 4 * c4);
-            const float4 xv = make_float4(v4[j].x + b.x, v4[j].y + b.y, v4[j].z + b.z,
-                                          v4[j].w + b.w);
+            // No bias (the snake before an upsample): the rows as they are
+            // (adding 0 would turn -0 into +0).
+            const float4 xv = BIAS ? make_float4(v4[j].x + b.x, v4[j].y + b.y, v4[j].z + b.z,
+                                                 v4[j].w + b.w)
+                                   : v4[j];
             *reinterpret_cast<float4 *>(tile + r * K + 4 * c4) =
                 snake_value4<true, CONV == 1>(xv, a, i, s_pio4);
         }
@@ -305,7 +308,7 @@ __global__ __launch_bounds__(256) void fill_kernel(uint8_t *__restrict__ dst, ui
 bool quant_snake_ok(const float *x, int K, int ldx, const uint8_t *q1, int ldq,
                     const uint8_t *q2, const SnakePre &sp) {
     return (K % 4 == 0) && (ldx % 4 == 0) && (ldq % 4 == 0) && (((uintptr_t)x) & 15) == 0 &&
-           (((uintptr_t)q1) & 3) == 0 && (((uintptr_t)q2) & 3) == 0 && sp.bias && sp.alpha &&
+           (((uintptr_t)q1) & 3) == 0 && (((uintptr_t)q2) & 3) == 0 && sp.alpha &&
            K <= kSnakeMaxChannels;
 }
 
@@ -329,8 +332,16 @@ int quant_rows_snake_dispatch(IroHipContext *ctx, const float *x, int M, int K, 
     const size_t lds = sizeof(float) * ((size_t)3 * K + (size_t)R * K);
     hipStream_t st = ctx->stream;
 #define IRO_QS(CH, HALF)                                                                          \
-    hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF>), grid, block, lds, st, x, M, K, ldx, \
-                       R, magic, sp.bias, sp.alpha, q1, ldq, s1, z1, q2, s2, z2, sflip)
+    do {                                                                                           \
+        if (sp.bias)                                                                               \
+            hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF, true>), grid, block, lds, st, \
+                               x, M, K, ldx, R, magic, sp.bias, sp.alpha, q1, ldq, s1, z1, q2, s2,  \
+                               z2, sflip);                                                         \
+        else                                                                                       \
+            hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF, false>), grid, block, lds,    \
+                               st, x, M, K, ldx, R, magic, sp.bias, sp.alpha, q1, ldq, s1, z1, q2,  \
+                               s2, z2, sflip);                                                     \
+    } while (0)
     const int ch = (K + 255) / 256;
     if (K <= 128) IRO_QS(1, true);
     else if (ch <= 1) IRO_QS(1, false);
