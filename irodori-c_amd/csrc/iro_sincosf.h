@@ -35,12 +35,30 @@ __constant__ uint32_t kInvPio4[24] = {
 // quadrants 2 and 3 whose cosine coefficients are exactly the first's
 // negated; negation commutes with every rounding, so `neg` negates the
 // cosine result instead.  Both polynomials are formed from constants (no
-// per-lane table loads) and the lane's one selected.
-__device__ __forceinline__ float sincos_poly_sel(double x, double x2, int k, bool neg) {
+// per-lane table loads) and the lane's one selected.  ad holds the two
+// coefficients that enter a fused multiply-add as its addend (s2, c3).
+struct SinCosAddends {
+    double s2, c3;
+};
+constexpr SinCosAddends kSinCosAddends = {0x1.1107605230bc4p-7, -0x1.6c087e89a359dp-10};
+
+// The addends in vector registers: a fused multiply-add reads at most one
+// scalar operand, so with both operands constant each evaluation would first
+// copy the addend into a register pair; a caller that evaluates several
+// elements takes them from here once (the empty asm hides the values, so the
+// copies are not re-created per element).
+__device__ __forceinline__ SinCosAddends sincos_addends() {
+    SinCosAddends ad = kSinCosAddends;
+    asm("" : "+v"(ad.s2), "+v"(ad.c3));
+    return ad;
+}
+
+__device__ __forceinline__ float sincos_poly_sel(double x, double x2, int k, bool neg,
+                                                 const SinCosAddends &ad = kSinCosAddends) {
     constexpr double c0 = 0x1p0, c1 = -0x1.ffffffd0c621cp-2, c2 = 0x1.55553e1068f19p-5,
-                     c3 = -0x1.6c087e89a359dp-10, c4 = 0x1.99343027bf8c3p-16;
-    constexpr double s1 = -0x1.555545995a603p-3, s2 = 0x1.1107605230bc4p-7,
-                     s3 = -0x1.994eb3774cf24p-13;
+                     c4 = 0x1.99343027bf8c3p-16;
+    constexpr double s1 = -0x1.555545995a603p-3, s3 = -0x1.994eb3774cf24p-13;
+    const double s2 = ad.s2, c3 = ad.c3;
     const double x3 = x * x2;
     const double sp = __builtin_fma(x2, s3, s2);
     const double x7 = x3 * x2;
@@ -104,9 +122,10 @@ __device__ __forceinline__ SinCosArg sincosf_reduce_large(float y,
 // cosine = 0: sinf(y); 1: cosf(y) from y's reduction: the quadrant's
 // polynomial, or glibc's own result for |y| < 2^-12 (y, or 1) and for
 // non-finite y (NaN).
-__device__ __forceinline__ float sincosf_finish(float y, const SinCosArg &a, int cosine) {
+__device__ __forceinline__ float sincosf_finish(float y, const SinCosArg &a, int cosine,
+                                                const SinCosAddends &ad = kSinCosAddends) {
     const double xs = ((a.m + 1) & 2) ? -a.x : a.x;  // an exact sign flip
-    const float v = sincos_poly_sel(xs, a.x * a.x, a.n ^ cosine, (a.m & 2) != 0);
+    const float v = sincos_poly_sel(xs, a.x * a.x, a.n ^ cosine, (a.m & 2) != 0, ad);
     const uint32_t top = (__float_as_uint(y) >> 20) & 0x7ff;
     if (top >= 0x7f8) return (y - y) / (y - y);
     return top < 0x398 ? (cosine ? 1.0f : y) : v;

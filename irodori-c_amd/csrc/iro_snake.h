@@ -49,10 +49,11 @@ __device__ __forceinline__ float4 snake_value4(float4 xv, float4 a, float4 inv,
     for (int k = 0; k < 4; ++k)
         if (__builtin_expect(!sincosf_is_small(y[k]), 0))
             r[k] = sincosf_reduce_large(y[k], invpio4);
-    return make_float4(snake_finish<INV, FMA>(xv.x, sincosf_finish(y[0], r[0], 0), a.x, inv.x),
-                       snake_finish<INV, FMA>(xv.y, sincosf_finish(y[1], r[1], 0), a.y, inv.y),
-                       snake_finish<INV, FMA>(xv.z, sincosf_finish(y[2], r[2], 0), a.z, inv.z),
-                       snake_finish<INV, FMA>(xv.w, sincosf_finish(y[3], r[3], 0), a.w, inv.w));
+    const SinCosAddends ad = sincos_addends();
+    return make_float4(snake_finish<INV, FMA>(xv.x, sincosf_finish(y[0], r[0], 0, ad), a.x, inv.x),
+                       snake_finish<INV, FMA>(xv.y, sincosf_finish(y[1], r[1], 0, ad), a.y, inv.y),
+                       snake_finish<INV, FMA>(xv.z, sincosf_finish(y[2], r[2], 0, ad), a.z, inv.z),
+                       snake_finish<INV, FMA>(xv.w, sincosf_finish(y[3], r[3], 0, ad), a.w, inv.w));
 }
 
 // The reciprocal the INV form hoists out of its loop (dacvae.c:827-828).
