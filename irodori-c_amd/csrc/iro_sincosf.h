@@ -76,7 +76,7 @@ __device__ __forceinline__ float sincos_poly_sel(double x, double x2, int k, boo
 
 // Whether y takes the fast reduction: |y| < 120 (NaN excluded).
 __device__ __forceinline__ bool sincosf_is_small(float y) {
-    return ((__float_as_uint(y) >> 20) & 0x7ff) < 0x42f;
+    return (__float_as_uint(y) & 0x7ff00000u) < 0x42f00000u;  // top 12 bits < 0x42f
 }
 
 // y reduced to x (double, |x| <= pi/4) in quadrant n; m is n plus the sign
@@ -124,11 +124,13 @@ __device__ __forceinline__ SinCosArg sincosf_reduce_large(float y,
 // non-finite y (NaN).
 __device__ __forceinline__ float sincosf_finish(float y, const SinCosArg &a, int cosine,
                                                 const SinCosAddends &ad = kSinCosAddends) {
-    const double xs = ((a.m + 1) & 2) ? -a.x : a.x;  // an exact sign flip
+    // x negated when bit 1 of m + 1 is set: that bit moved to the sign bit
+    const uint64_t flip = (uint64_t)(((uint32_t)(a.m + 1) << 30) & 0x80000000u) << 32;
+    const double xs = __builtin_bit_cast(double, __builtin_bit_cast(uint64_t, a.x) ^ flip);
     const float v = sincos_poly_sel(xs, a.x * a.x, a.n ^ cosine, (a.m & 2) != 0, ad);
-    const uint32_t top = (__float_as_uint(y) >> 20) & 0x7ff;
-    if (top >= 0x7f8) return (y - y) / (y - y);
-    return top < 0x398 ? (cosine ? 1.0f : y) : v;
+    const uint32_t top = __float_as_uint(y) & 0x7ff00000u;  // top 12 bits, in place
+    if (top >= 0x7f800000u) return (y - y) / (y - y);
+    return top < 0x39800000u ? (cosine ? 1.0f : y) : v;
 }
 
 // cosine = 0: sinf(y); 1: cosf(y), every float y.

@@ -44,7 +44,13 @@ __device__ __forceinline__ float4 snake_value4(float4 xv, float4 a, float4 inv,
     const float y[4] = {a.x * xv.x, a.y * xv.y, a.z * xv.z, a.w * xv.w};
     SinCosArg r[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) r[k] = sincosf_reduce_small(sincosf_is_small(y[k]) ? y[k] : 0.0f);
+    for (int k = 0; k < 4; ++k) {
+        // selected in single precision (the empty asm keeps the compiler from
+        // moving the select past the widening, which would take two)
+        float ys = sincosf_is_small(y[k]) ? y[k] : 0.0f;
+        asm("" : "+v"(ys));
+        r[k] = sincosf_reduce_small(ys);
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k)
         if (__builtin_expect(!sincosf_is_small(y[k]), 0))
