@@ -134,7 +134,7 @@ int launch_snake(IroHipContext *ctx, const float *x, int T, int C, const float *
 // input rows (dacvae.c:599-603) with the row ranges its quantization needs,
 // in one pass.  A block takes R rows (R C <= 4096): phase 1 snakes them as
 // flat float4 chunks (every lane busy) into y and an LDS tile, phase 2
-// reduces each row of the tile with one wavefront.
+// reduces each row of the tile with eight lanes (fmin/fmax: any order).
 template <bool FMA>
 __global__ __launch_bounds__(256) void snake_rows_kernel(const float *__restrict__ x, int T, int C,
                                                          int R, unsigned k4_magic,
@@ -174,17 +174,19 @@ __global__ __launch_bounds__(256) void snake_rows_kernel(const float *__restrict
         }
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    for (int r = threadIdx.x >> 6; r < rows; r += 4) {
+    // eight lanes per row, 32 rows per pass: every lane of an aligned group
+    // of eight shares the row, so the group exchange reads active lanes only
+    const int sub = threadIdx.x & 7;
+    for (int r = threadIdx.x >> 3; r < rows; r += 32) {
         float lo = 0.0f, hi = 0.0f;
-        for (int c4 = lane; c4 < k4; c4 += 64) {
+        for (int c4 = sub; c4 < k4; c4 += 8) {
             const float4 v = *reinterpret_cast<const float4 *>(tile + r * C + 4 * c4);
             lo = sel_min(lo, v.x); lo = sel_min(lo, v.y); lo = sel_min(lo, v.z); lo = sel_min(lo, v.w);
             hi = sel_max(hi, v.x); hi = sel_max(hi, v.y); hi = sel_max(hi, v.z); hi = sel_max(hi, v.w);
         }
-        lo = wave_min(lo);
-        hi = wave_max(hi);
-        if (lane == 0) {
+        lo = group8_range<false>(lo);
+        hi = group8_range<true>(hi);
+        if (sub == 0) {
             row_lo[row0 + r] = lo;
             row_hi[row0 + r] = hi;
         }

@@ -147,6 +147,15 @@ __device__ __forceinline__ float half_range(float v) {
     v = op(v, dpp_mov<0x140>(v));
     return op(v, swz_xor16(v));
 }
+// The same over each aligned group of eight lanes (quad swaps, then the
+// half-row mirror pairs lane i with lane 7 - i of its group).
+template <bool MAX>
+__device__ __forceinline__ float group8_range(float v) {
+    auto op = [](float a, float b) { return MAX ? __builtin_fmaxf(a, b) : __builtin_fminf(a, b); };
+    v = op(v, dpp_mov<0xB1>(v));
+    v = op(v, dpp_mov<0x4E>(v));
+    return op(v, dpp_mov<0x141>(v));
+}
 __device__ __forceinline__ float wave_min(float v) { return wave_range<false>(v); }
 __device__ __forceinline__ float wave_max(float v) { return wave_range<true>(v); }
 __device__ __forceinline__ int wave_sum(int v) {
