@@ -213,16 +213,15 @@ __global__ __launch_bounds__(256, 2) void conv7_gemm_kernel(KParams p, ConvRows 
 // whole rows (LDS: the tile, the codes and the per-channel parameters within
 // 64 KiB): phase 1 copies them into an LDS tile as flat float4 chunks (every
 // lane busy) and snakes them there in place with per-channel bias, alpha
-// and reciprocal from LDS; phase 2 quantizes each tile row with the row
-// quantizer of
-// iro_quant_row.h (half a wavefront per row up to 128 channels), writing
+// and reciprocal from LDS; phase 2 quantizes each tile row with the
+// eight-lane row quantizer of iro_quant_row.h (quant_row_g8), writing
 // the codes into LDS in MFMA fragment order and the row parameters where the
 // epilogue reads them; then each wave runs the C/32 k blocks of MFMAs
 // against its weight fragments and the epilogue adds the skip rows.  One
 // column tile covers all N (TJ = Np / 128).  Rows past M hold zeros and are
 // never stored.
 
-template <int CONV, bool TWO, int TJ, bool HALF, int TI>
+template <int CONV, bool TWO, int TJ, int TI>
 __global__ __launch_bounds__(256, TI == 1 ? 4 : 2) void conv1x1_snake_kernel(KParams p, const float *__restrict__ hid,
                                                                const float *__restrict__ sbias,
                                                                const float *__restrict__ salpha,
@@ -286,19 +285,19 @@ __global__ __launch_bounds__(256, TI == 1 ? 4 : 2) void conv1x1_snake_kernel(KPa
         *reinterpret_cast<float4 *>(tile + 4 * f) = snake_value4<true, CONV == 1>(xv, a, i, s_pio4);
     }
     __syncthreads();
-    // Phase 2: row quantization from the tile, codes in fragment order.
+    // Phase 2: row quantization from the tile, codes in fragment order;
+    // eight lanes per row (32 rows per pass), C / 32 float4 per lane.
     {
-        constexpr int WL = HALF ? 32 : 64, RPB = 256 / WL;
-        const int ln = tid & (WL - 1);
-        for (int r = tid / WL; r < BM; r += RPB) {
-            float4 v[1];
-            const int col = ln * 4;
-            v[0] = col < C ? *reinterpret_cast<const float4 *>(tile + r * pitch + col)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-            quant_row<CONV, 1, TWO, false, HALF>(v, r, C, ln, codes, -KB, rl.sx[0], rl.zx[0],
-                                                 nullptr, TWO ? codes + plane : nullptr,
-                                                 rl.sx[TWO ? 1 : 0], rl.zx[TWO ? 1 : 0],
-                                                 0x80808080u);
+        const int sub = tid & 7, nch = C >> 5;
+        for (int r = tid >> 3; r < BM; r += 32) {
+            float4 v[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                v[c] = c < nch ? *reinterpret_cast<const float4 *>(tile + r * pitch + (c * 8 + sub) * 4)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            quant_row_g8<CONV, 8, TWO>(v, nch, r, sub, codes, -KB, rl.sx[0], rl.zx[0],
+                                       TWO ? codes + plane : nullptr, rl.sx[TWO ? 1 : 0],
+                                       rl.zx[TWO ? 1 : 0], 0x80808080u);
         }
     }
     __syncthreads();
@@ -369,28 +368,21 @@ int launch_conv1x1_snake(IroHipContext *ctx, const IroHipWeight *w, const float 
     kp.tiles_per_xcd = (kp.tiles_m + 7) / 8;
     kp.row_major = 1;
     const dim3 grid((unsigned)(8 * kp.tiles_per_xcd)), block(256);
-    const bool half = C <= 128;
     // floor(f / (C/4)) == umulhi(2 f, ceil(2^31 / (C/4))) for the chunk
     // indices f < 4096 used: the rounding adds less than 2^13 / 2^32 < 4 / C.
     const unsigned k4 = (unsigned)C / 4, magic = (unsigned)((0x80000000ull + k4 - 1) / k4);
     prof_begin(ctx);
-#define IRO_RS(CV, TW, TJ, HF)                                                                  \
-    do {                                                                                       \
-        if (bm == 64)                                                                          \
-            hipLaunchKernelGGL((conv1x1_snake_kernel<CV, TW, TJ, HF, 2>), grid, block, lds,     \
-                               ctx->stream, kp, hidden, snake_bias, snake_alpha, magic);        \
-        else                                                                                   \
-            hipLaunchKernelGGL((conv1x1_snake_kernel<CV, TW, TJ, HF, 1>), grid, block, lds,     \
-                               ctx->stream, kp, hidden, snake_bias, snake_alpha, magic);        \
-    } while (0)
+#define IRO_RS(CV, TW, TJ)                                                                      \
+    hipLaunchKernelGGL((conv1x1_snake_kernel<CV, TW, TJ, 1>), grid, block, lds, ctx->stream, kp, \
+                       hidden, snake_bias, snake_alpha, magic)
     if (ctx->convention == IRO_HIP_GCC_FASTMATH) {
-        if (two) { if (half) IRO_RS(1, true, 1, true); else IRO_RS(1, true, 1, false); }
-        else if (tj == 2) { if (half) IRO_RS(1, false, 2, true); else IRO_RS(1, false, 2, false); }
-        else { if (half) IRO_RS(1, false, 1, true); else IRO_RS(1, false, 1, false); }
+        if (two) IRO_RS(1, true, 1);
+        else if (tj == 2) IRO_RS(1, false, 2);
+        else IRO_RS(1, false, 1);
     } else {
-        if (two) { if (half) IRO_RS(0, true, 1, true); else IRO_RS(0, true, 1, false); }
-        else if (tj == 2) { if (half) IRO_RS(0, false, 2, true); else IRO_RS(0, false, 2, false); }
-        else { if (half) IRO_RS(0, false, 1, true); else IRO_RS(0, false, 1, false); }
+        if (two) IRO_RS(0, true, 1);
+        else if (tj == 2) IRO_RS(0, false, 2);
+        else IRO_RS(0, false, 1);
     }
 #undef IRO_RS
     IRO_HIP_CHECK_LAUNCH(ctx);

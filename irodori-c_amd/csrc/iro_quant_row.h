@@ -115,5 +115,69 @@ __device__ __forceinline__ void quant_row(float4 (&v)[CH], int row, int K, int l
     }
 }
 
+// quant_row with eight lanes per row (an aligned group of eight; `lane` is
+// 0..7 within it): lane L holds columns 4*(8c + L) .. +3 for c < nch (nch
+// the same in every lane, K == 32 nch), so every held column is in range
+// and the reductions stay inside the group.  Same arithmetic, codes and
+// row parameters as quant_row.
+template <int CONV, int CHM, bool RES>
+__device__ __forceinline__ void quant_row_g8(float4 (&v)[CHM], int nch, int row, int lane,
+                                             uint8_t *__restrict__ q1, int ldq,
+                                             float *__restrict__ s1, int32_t *__restrict__ z1,
+                                             uint8_t *__restrict__ q2, float *__restrict__ s2,
+                                             int32_t *__restrict__ z2, uint32_t sflip) {
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CHM; ++c)
+        if (c < nch) {
+            lo = sel_min(lo, v[c].x); lo = sel_min(lo, v[c].y);
+            lo = sel_min(lo, v[c].z); lo = sel_min(lo, v[c].w);
+            hi = sel_max(hi, v[c].x); hi = sel_max(hi, v[c].y);
+            hi = sel_max(hi, v[c].z); hi = sel_max(hi, v[c].w);
+        }
+    lo = group8_range<false>(lo);
+    hi = group8_range<true>(hi);
+    const RowQ r = row_params<CONV>(lo, hi);
+    float lo2 = 0.0f, hi2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CHM; ++c)
+        if (c < nch) {
+            const int col = (c * 8 + lane) * 4;
+            float4 qv;
+            const uint32_t packed = codes4<CONV>(v[c], r, RES ? &qv : nullptr);
+            *reinterpret_cast<uint32_t *>(q1 + code_off(row, col, ldq)) = packed ^ sflip;
+            if (RES) {
+                v[c].x = residual_value<CONV>(v[c].x, qv.x, r);
+                v[c].y = residual_value<CONV>(v[c].y, qv.y, r);
+                v[c].z = residual_value<CONV>(v[c].z, qv.z, r);
+                v[c].w = residual_value<CONV>(v[c].w, qv.w, r);
+                lo2 = sel_min(lo2, v[c].x); lo2 = sel_min(lo2, v[c].y);
+                lo2 = sel_min(lo2, v[c].z); lo2 = sel_min(lo2, v[c].w);
+                hi2 = sel_max(hi2, v[c].x); hi2 = sel_max(hi2, v[c].y);
+                hi2 = sel_max(hi2, v[c].z); hi2 = sel_max(hi2, v[c].w);
+            }
+        }
+    if (lane == 0) {
+        s1[row] = r.s;
+        z1[row] = r.zp;
+    }
+    if (RES) {
+        lo2 = group8_range<false>(lo2);
+        hi2 = group8_range<true>(hi2);
+        const RowQ r2 = row_params<CONV>(lo2, hi2);
+#pragma unroll
+        for (int c = 0; c < CHM; ++c)
+            if (c < nch) {
+                const int col = (c * 8 + lane) * 4;
+                const uint32_t packed = codes4<CONV>(v[c], r2, nullptr);
+                *reinterpret_cast<uint32_t *>(q2 + code_off(row, col, ldq)) = packed ^ sflip;
+            }
+        if (lane == 0) {
+            s2[row] = r2.s;
+            z2[row] = r2.zp;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace iro
