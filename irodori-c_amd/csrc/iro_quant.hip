@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void quant_rows_half(const float *__restrict__
 // with per-channel bias, alpha and reciprocal staged in LDS, and writes the
 // tile [R, K] to LDS.  Phase 2 quantizes the tile's rows as quant_rows_vec
 // (HALF: quant_rows_half) does.  Dynamic LDS: 3 K + R K floats.
-template <int CONV, int CH, bool RES, bool HALF, bool BIAS>
+template <int CONV, int CH, bool RES, bool HALF, bool BIAS, bool G8>
 __global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict__ x, int M, int K,
                                                         int ldx, int R, unsigned k4_magic,
                                                         const float *__restrict__ bias,
@@ -119,6 +119,20 @@ __global__ __launch_bounds__(256) void quant_rows_snake(const float *__restrict_
         }
     }
     __syncthreads();
+    if (G8) {
+        // Phase 2 with eight lanes per row (32 rows per pass), K / 32 float4
+        // per lane (K a multiple of 32, at most 256).
+        const int sub = threadIdx.x & 7, nch = K >> 5;
+        for (int r = threadIdx.x >> 3; r < rows; r += 32) {
+            float4 v[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                v[c] = c < nch ? *reinterpret_cast<const float4 *>(tile + r * K + (c * 8 + sub) * 4)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            quant_row_g8<CONV, 8, RES>(v, nch, row0 + r, sub, q1, ldq, s1, z1, q2, s2, z2, sflip);
+        }
+        return;
+    }
     // Phase 2: rows of the tile, one per wave (HALF: per 32-lane half).
     constexpr int WL = HALF ? 32 : 64, RPB = 256 / WL;
     const int lane = threadIdx.x & (WL - 1);
@@ -323,7 +337,10 @@ template <int CONV, bool RES>
 int quant_rows_snake_dispatch(IroHipContext *ctx, const float *x, int M, int K, int ldx,
                               const SnakePre &sp, uint8_t *q1, int ldq, float *s1, int32_t *z1,
                               uint8_t *q2, float *s2, int32_t *z2, uint32_t sflip) {
-    const int R = snake_tile_rows(K);
+    // Eight lanes per row where every lane holds whole float4 of the row.
+    const bool g8 = K % 32 == 0 && K <= 256;
+    const int fit = 4096 / K;
+    const int R = g8 ? (fit >= 32 ? fit / 32 * 32 : fit) : snake_tile_rows(K);
     const unsigned k4 = (unsigned)K / 4;
     // floor(f / k4) == umulhi(2 f, ceil(2^31 / k4)) for the chunk indices
     // f < 1024 used: the rounding adds less than 2^11 / 2^32 < 1 / k4.
@@ -331,23 +348,24 @@ int quant_rows_snake_dispatch(IroHipContext *ctx, const float *x, int M, int K, 
     const dim3 grid((unsigned)((M + R - 1) / R)), block(256);
     const size_t lds = sizeof(float) * ((size_t)3 * K + (size_t)R * K);
     hipStream_t st = ctx->stream;
-#define IRO_QS(CH, HALF)                                                                          \
+#define IRO_QS(CH, HALF, G8)                                                                      \
     do {                                                                                           \
         if (sp.bias)                                                                               \
-            hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF, true>), grid, block, lds, st, \
-                               x, M, K, ldx, R, magic, sp.bias, sp.alpha, q1, ldq, s1, z1, q2, s2,  \
-                               z2, sflip);                                                         \
-        else                                                                                       \
-            hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF, false>), grid, block, lds,    \
+            hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF, true, G8>), grid, block, lds, \
                                st, x, M, K, ldx, R, magic, sp.bias, sp.alpha, q1, ldq, s1, z1, q2,  \
                                s2, z2, sflip);                                                     \
+        else                                                                                       \
+            hipLaunchKernelGGL((quant_rows_snake<CONV, CH, RES, HALF, false, G8>), grid, block,     \
+                               lds, st, x, M, K, ldx, R, magic, sp.bias, sp.alpha, q1, ldq, s1, z1, \
+                               q2, s2, z2, sflip);                                                 \
     } while (0)
     const int ch = (K + 255) / 256;
-    if (K <= 128) IRO_QS(1, true);
-    else if (ch <= 1) IRO_QS(1, false);
-    else if (ch <= 2) IRO_QS(2, false);
-    else if (ch <= 4) IRO_QS(4, false);
-    else IRO_QS(6, false);
+    if (g8) IRO_QS(1, false, true);
+    else if (K <= 128) IRO_QS(1, true, false);
+    else if (ch <= 1) IRO_QS(1, false, false);
+    else if (ch <= 2) IRO_QS(2, false, false);
+    else if (ch <= 4) IRO_QS(4, false, false);
+    else IRO_QS(6, false, false);
 #undef IRO_QS
     IRO_HIP_CHECK_LAUNCH(ctx);
     return 0;

@@ -110,6 +110,31 @@ def test_residual_unit_large_hidden(ctx, oracle, C, T, two):
     assert_bits_equal(out.numpy(), want, "residual unit, large hidden values")
 
 
+@pytest.mark.parametrize("two", [True, False], ids=["two-plane", "one-plane"])
+@pytest.mark.parametrize("C,T", [(32, 90), (64, 70), (96, 70), (192, 45), (256, 33), (160, 40)])
+def test_residual_unit_snake_quantizer_path(ctx, oracle, C, T, two):
+    """Conv mode 1 routes the unit's 1x1 through the row quantizer that
+    applies the snake_bias itself (eight lanes per row where the channels
+    are a multiple of 32 up to 256, one wavefront or half of one per row
+    otherwise)."""
+    conv = ctx.convention
+    rng = np.random.default_rng(11 * C + T)
+    u = cp.residual_unit(rng, C, 3)
+    x = rng.standard_normal((T, C), dtype=np.float32)
+    w0 = ctx.weight(ctx.to_device(u["w0"]), C, 7 * C)
+    w1 = ctx.weight(ctx.to_device(u["w1"]), C, C)
+    out = ctx.empty((T, C), np.float32)
+    ctx.set_gemm_tile(-6, 1)
+    try:
+        ctx.dacvae_residual(ctx.to_device(x), T, C, w0, ctx.to_device(u["alpha0"]),
+                            ctx.to_device(u["b0"]), ctx.to_device(u["alpha1"]), 3, w1,
+                            ctx.to_device(u["b1"]), two, two, out)
+    finally:
+        ctx.set_gemm_tile(-6, 2)
+    want = oracle.residual_unit(conv, x, u, two, two)
+    assert_bits_equal(out.numpy(), want, "residual unit, snake in the row quantizer")
+
+
 def test_residual_unit_long_384_modes_agree(ctx):
     """At 384 channels on 16384 steps or more the unit's Conv7 takes the
     snake pass with row ranges and the GEMM that codes its own rows; its
