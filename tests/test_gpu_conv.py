@@ -179,3 +179,26 @@ def test_convtranspose_long_short_k_tiles(ctx):
         finally:
             ctx.set_gemm_tile(0, 0)
     assert_bits_equal(outs[0], outs[1], "convtranspose output, 128x128 vs 64x256 tiles")
+
+
+def test_conv1x1_skip_long_short_k_tiles(ctx):
+    """A long 1x1 with a 384-row weight (the decoder's stage-1 1x1) takes
+    128 x 128 tiles of the chunked GEMM kernel; its output equals the
+    64-row whole-tile path's, which the oracle tests above pin."""
+    T, C = 30000, 384
+    hidden = gauss(71, (T, C))
+    skip = gauss(72, (T, C))
+    w = gauss(73, (C, C), 0.02)
+    b = gauss(74, (C,), 0.01)
+    W = ctx.weight(ctx.to_device(w), C, C)
+    hd, sd, bd = ctx.to_device(hidden), ctx.to_device(skip), ctx.to_device(b)
+    outs = []
+    for tile in ((0, 0), (2, 1)):
+        ctx.set_gemm_tile(*tile)
+        try:
+            out = ctx.empty((T, C), np.float32)
+            ctx.conv1x1_skip(hd, sd, T, W, bd, 0, out)
+            outs.append(out.numpy())
+        finally:
+            ctx.set_gemm_tile(0, 0)
+    assert_bits_equal(outs[0], outs[1], "conv1x1 onto skip, 128x128 vs whole 64-row tiles")
