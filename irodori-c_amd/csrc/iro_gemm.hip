@@ -1049,6 +1049,8 @@ int launch_silu_selfcheck(IroHipContext *ctx, unsigned long long *out) {
 void gemm_prof_end(IroHipContext *ctx, const GemmArgs &a, const IroHipWeight *w, Epi epi,
                    bool two);
 
+int ctx_cus(const IroHipContext *ctx) { return ctx->cus > 0 ? ctx->cus : 256; }
+
 int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K, int N) {
     if (M <= 32 || ctx->gemm_lds < 0 || K % 32) return 0;
     // Default: the QKVG projection (measured at 2250 x 1024 -> 4096: 23.2 us
@@ -1059,6 +1061,13 @@ int gemm_lds_cfg(const IroHipContext *ctx, Epi epi, bool two, int M, int K, int 
     // 6000 rows, K = 7168, N = 256 it was slower, 60 against 34 us).
     if (ctx->gemm_lds == 0 && epi != EPI_QKVG) {
         if (epi == EPI_LINEAR && !two && M >= 16384 && K >= 2048 && N >= 512 &&
+            lds_cfg_ok(LDS_192x256_CFG, two, epi))
+            return LDS_192x256_CFG;
+        // Wide one-plane linears of a few thousand rows (the decoder's
+        // stage-1 upsample: 3000 x 7680, K = 768): 77.8 us against 115 us
+        // with the whole-tile kernel (its quantization and gather included).
+        if (epi == EPI_LINEAR && !two && M <= 8192 && K >= 512 && K <= 1024 && N >= 6144 &&
+            (long long)((M + 191) / 192) * (N / 256) >= ctx_cus(ctx) &&
             lds_cfg_ok(LDS_192x256_CFG, two, epi))
             return LDS_192x256_CFG;
         return 0;

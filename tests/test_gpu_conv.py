@@ -202,3 +202,26 @@ def test_conv1x1_skip_long_short_k_tiles(ctx):
         finally:
             ctx.set_gemm_tile(0, 0)
     assert_bits_equal(outs[0], outs[1], "conv1x1 onto skip, 128x128 vs whole 64-row tiles")
+
+
+def test_convtranspose_wide_lds_kernel(ctx):
+    """The decoder's stage-1 upsample (3000 rows, k = 768, 20 taps of 384
+    channels) takes the LDS-pipelined GEMM; its output equals the output
+    with that kernel switched off, which the oracle tests above pin."""
+    T, Ci, Co, k, st, pad, opad = 3000, 768, 384, 20, 10, 5, 0
+    x = gauss(51, (T, Ci))
+    w_export = gauss(52, (Ci, k * Co), 0.02)
+    b = gauss(53, (Co,), 0.01)
+    W = ctx.weight(ctx.to_device(w_export), k * Co, Ci, transposed=True)
+    xd, bd = ctx.to_device(x), ctx.to_device(b)
+    outs = []
+    for lds in (0, -1):
+        ctx.set_gemm_tile(-4, lds)
+        try:
+            To = (T - 1) * st - 2 * pad + k + opad
+            yd = ctx.empty((To, Co), np.float32)
+            ctx.convtranspose1d(xd, T, Ci, W, Co, k, st, pad, opad, bd, 0, yd)
+            outs.append(yd.numpy())
+        finally:
+            ctx.set_gemm_tile(-4, 0)
+    assert_bits_equal(outs[0], outs[1], "convtranspose output, LDS-pipelined vs whole-tile GEMM")
