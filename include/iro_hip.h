@@ -253,9 +253,9 @@ int iro_hip_weight_load(IroHipContext *ctx, const char *path, IroHipWeight **out
 int iro_hip_dit_adaln_params(IroHipContext *ctx, const float *cond, int B, int D, int R,
                              const float *const *weights, int n_adaln, float *out);
 
-/* The device tanhf on all 2^32 float inputs, hashed as the oracle's
-   orc_tanhf_digest hashes libm's (a known-answer check of the restatement;
-   takes a few seconds). */
+/* The device tanhf on all 2^32 float inputs as one digest, to compare with
+   the same digest of libm's tanhf computed on the host (equal exactly when
+   every result agrees, barring a hash collision); takes a few seconds. */
 int iro_hip_selfcheck_tanhf(IroHipContext *ctx, unsigned long long *digest);
 
 /* ops.c:221-234, iro_linear of the scalar build: y [M, N] = x [M, K] @ w
